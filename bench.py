@@ -1,0 +1,218 @@
+"""Headline benchmark: batched decode indexer scoring + top-K on one MI355X.
+
+Workload: B=16 independent sequences, L=32768 bf16 keys
+~ N(0,1) with 1% "hot" keys scaled x4, q bf16 ~ N(0,1)/sqrt(128), fp32 head
+weights ~ N(0,1/64), exact top-K=2048 per sequence (stable_topk set
+semantics).  One step = dense scores of all 16 x 32768 keys + the top-K of
+every sequence, inputs resident in HBM.  Four distinct key sets (4 x 128 MiB)
+are rotated so that the 256 MB last-level cache cannot hold the step's keys.
+
+Prints one JSON line (see the driver contract) with a `roofline` object for
+the dominant kernel (the scoring kernel, timed with HIP events on the stream
+it runs on) and a `cpu_baseline` object (the oracle's CPU restatement of the
+reference path timed on this host on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BATCH = 16
+LENGTH = 32768
+TOPK = 2048
+ROTATIONS = 4
+HOT_FRACTION = 0.01
+SEED = 1582
+
+
+def parse_args() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    return parser.parse_args()
+
+
+def make_inputs(device):
+    import torch
+
+    gen = torch.Generator(device=device).manual_seed(SEED)
+    cpu_gen = torch.Generator().manual_seed(SEED)
+    q = (torch.randn(BATCH, 64, 128, generator=gen, device=device) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(BATCH, 64, generator=gen, device=device) / 8.0
+    key_sets = []
+    hot = round(HOT_FRACTION * LENGTH)
+    for _ in range(ROTATIONS):
+        keys = torch.randn(BATCH, LENGTH, 128, generator=gen, device=device)
+        for b in range(BATCH):
+            idx = torch.randperm(LENGTH, generator=cpu_gen)[:hot].to(device)
+            keys[b, idx] *= 4.0
+        key_sets.append(keys.to(torch.bfloat16))
+        del keys
+    return q, w, key_sets
+
+
+def cpu_baseline(q, w, keys, k: int, budget_s: float) -> tuple[dict, "object"]:
+    """Oracle restatement of the reference CPU path: torch fp32 dense score
+    (reference progressive_kernel.py:45-55) + numpy stable_topk (metrics.py:9-22)."""
+
+    import torch
+
+    from oracle import scores as S
+    from oracle import topk as T
+
+    threads = torch.get_num_threads()
+    q0, w0, k0 = q[0].cpu(), w[0].cpu(), keys[0].cpu()
+    reps = 0
+    start = time.perf_counter()
+    top = None
+    while True:
+        scores = S.torch_full_scores(q0, w0, k0)
+        top = T.stable_topk(scores.numpy(), k)
+        reps += 1
+        if time.perf_counter() - start >= budget_s and reps >= 3:
+            break
+    elapsed = time.perf_counter() - start
+    value = reps * LENGTH / elapsed / 1e9
+    info = {
+        "value": value,
+        "unit": "G keys/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} x (1 sequence, L={LENGTH}, K={k}) scored + stable_topk in {elapsed:.1f} s",
+    }
+    return info, top
+
+
+def main() -> None:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build (the path shards by sequence, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from dsa_amd import _lib, metrics
+
+    _lib.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    q, w, key_sets = make_inputs(device)
+    scores = torch.empty(BATCH, LENGTH, device=device, dtype=torch.float32)
+    out_idx = torch.empty(BATCH, TOPK, device=device, dtype=torch.int64)
+    stream = torch.cuda.current_stream(device)
+    s_ptr = stream.cuda_stream
+
+    def score(keys):
+        _lib.call(
+            "dsa_full_scores", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(),
+            BATCH, LENGTH, _lib.DTYPE_BF16, s_ptr,
+        )
+
+    def select():
+        _lib.call(
+            "dsa_topk", scores.data_ptr(), None, BATCH, LENGTH, LENGTH, None, TOPK, 0,
+            out_idx.data_ptr(), None, s_ptr,
+        )
+
+    for i in range(args.warmup):
+        score(key_sets[i % ROTATIONS])
+        select()
+    torch.cuda.synchronize()
+
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(3 * args.steps)]
+    wall0 = time.perf_counter()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(args.steps):
+        marks[3 * i].record(stream)
+        score(key_sets[i % ROTATIONS])
+        marks[3 * i + 1].record(stream)
+        select()
+        marks[3 * i + 2].record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_time(t1)
+    score_ms = [marks[3 * i].elapsed_time(marks[3 * i + 1]) for i in range(args.steps)]
+    topk_ms = [marks[3 * i + 1].elapsed_time(marks[3 * i + 2]) for i in range(args.steps)]
+    ms_per_step = total_ms / args.steps
+    keys_per_step = BATCH * LENGTH
+    value = keys_per_step / (ms_per_step / 1e3) / 1e9
+
+    # Algorithmic bytes of the scoring kernel per launch: every key row once
+    # (256 B), one fp32 score written per key, the query block and weights once
+    # per sequence.
+    score_bytes = keys_per_step * (256 + 4) + BATCH * (64 * 128 * 2 + 64 * 4)
+    score_avg_ms = sum(score_ms) / len(score_ms)
+    achieved = score_bytes / (score_avg_ms / 1e3) / 1e9
+    # Whole-step algorithmic bytes (keys + q + w + K index/score outputs).
+    step_bytes = keys_per_step * 256 + BATCH * (64 * 128 * 2 + 64 * 4) + BATCH * TOPK * (4 + 4)
+
+    # Parity of one sequence against the oracle (Recall@K of the GPU set).
+    baseline = None
+    recall = None
+    if not args.no_cpu_baseline:
+        score(key_sets[0])
+        select()
+        torch.cuda.synchronize()
+        baseline, cpu_top = cpu_baseline(q, w, key_sets[0], TOPK, args.cpu_seconds)
+        recall = metrics.topk_recall(out_idx[0].cpu().numpy(), cpu_top)
+
+    line = {
+        "metric": "G keys scored/s + % HBM roofline, B=16 L=32K bf16 top-K2048; Recall@K",
+        "value": round(value, 3),
+        "unit": "G keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2 batched decode: B=16 x L=32768 bf16 keys (1% hot x4), 64x128 indexer, fp32 weights, exact top-K=2048 per sequence, 4 rotated key sets",
+            "batch": BATCH,
+            "length": LENGTH,
+            "topk": TOPK,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "dense_scores_kernel<bf16, M=4>",
+            "kernel_avg_us": round(score_avg_ms * 1e3, 3),
+            "algorithmic_bytes": score_bytes,
+        },
+        "step": {
+            "score_us": round(score_avg_ms * 1e3, 3),
+            "topk_us": round(sum(topk_ms) / len(topk_ms) * 1e3, 3),
+            "algorithmic_bytes": step_bytes,
+            "hbm_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "wall_s": round(wall, 3),
+        },
+        "recall_at_k": recall,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,138 @@
+"""ctypes binding of libdsa_amd.so (the C ABI declared in include/dsa_amd.h).
+
+The library is loaded lazily from the package directory.  There is no
+fallback: if the shared object is missing or does not load, every GPU entry
+point raises ``RuntimeError("HIP extension not built ...")``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libdsa_amd.so"
+ABI_VERSION = 1
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+DTYPE_FP8_E4M3 = 3
+
+_TORCH_DTYPES = {
+    torch.float32: DTYPE_F32,
+    torch.float16: DTYPE_F16,
+    torch.bfloat16: DTYPE_BF16,
+    torch.float8_e4m3fn: DTYPE_FP8_E4M3,
+}
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+# name -> argument types (every entry point returns int32 status unless listed)
+_SIGNATURES: dict[str, list] = {
+    "dsa_full_scores": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p],
+    "dsa_score_queries": [
+        _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64,
+        _i64, _i32, _p,
+    ],
+    "dsa_route_heads": [_p, _i64, _i64, _i64, _i32, _p, _p, _p],
+    "dsa_h8_block_max": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
+    "dsa_masked_full_scores": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
+    "dsa_progressive_scores": [
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _p,
+    ],
+    "dsa_promote_blocks": [_p, _p, _p, _p, _i64, _p],
+    "dsa_topk": [_p, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p, _p],
+    "dsa_topk_long": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
+    "dsa_block_max": [_p, _i64, _i64, _i64, _i32, _p, _p],
+    "dsa_block_key_norms": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p],
+    "dsa_temporal_score_radius": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+}
+_RESTYPES: dict[str, object] = {
+    "dsa_topk_long_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def exported_names() -> list[str]:
+    """Every symbol this binding expects the library to export."""
+
+    return sorted([*_SIGNATURES, *_RESTYPES, "dsa_last_error", "dsa_abi_version"])
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is not built."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY_PATH.exists():
+            raise RuntimeError(
+                f"HIP extension not built: {LIBRARY_PATH} is missing "
+                "(run `python -m dsa_amd.build`)"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+        except OSError as exc:  # pragma: no cover - depends on the host
+            raise RuntimeError(f"HIP extension not built or not loadable: {exc}") from exc
+        lib.dsa_last_error.restype = ctypes.c_char_p
+        lib.dsa_last_error.argtypes = []
+        lib.dsa_abi_version.restype = ctypes.c_int
+        lib.dsa_abi_version.argtypes = []
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        for name, (restype, argtypes) in _RESTYPES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.dsa_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libdsa_amd ABI {version} != expected {ABI_VERSION}; rebuild")
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke a status-returning entry point; raise RuntimeError on failure."""
+
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        message = lib.dsa_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {status}): {message}")
+
+
+def query(name: str, *args):
+    """Invoke a value-returning entry point."""
+
+    return getattr(load(), name)(*args)
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    """Device address of a tensor (None for a missing optional argument)."""
+
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_of(tensor: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on the tensor's device."""
+
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _TORCH_DTYPES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}") from None

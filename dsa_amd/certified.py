@@ -1,0 +1,74 @@
+"""Block key-norm summaries and the certified temporal radius on the GPU.
+
+Mirrors ``temporal_dsa.certified`` (reference ``src/temporal_dsa/certified.py``)
+for the two functions that feed pruning bounds: ``block_key_norms``
+(certified.py:51-62) and ``temporal_score_radius`` (certified.py:18-48).  The
+reference's float64 score oracle ``relu_index_score`` is a test oracle and
+lives in ``oracle/``.  Results are fp32 (the reference computes in float64).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def block_key_norms(keys: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Maximum key L2 norm per block and head for keys ``[tokens, heads, dim]``.
+
+    A shared-key cache ``[tokens, dim]`` is treated as one head.
+    """
+
+    if not keys.is_cuda:
+        raise ValueError("HIP kernels require GPU tensors")
+    if keys.ndim == 2:
+        keys = keys.unsqueeze(1)
+    if keys.ndim != 3:
+        raise ValueError("keys must have shape [tokens,heads,dim]")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    tokens, heads, dim = keys.shape
+    keys = keys.contiguous()
+    blocks = (tokens + block_size - 1) // block_size
+    out = torch.empty((blocks, heads), device=keys.device, dtype=torch.float32)
+    if tokens == 0:
+        return out
+    _lib.call(
+        "dsa_block_key_norms", _lib.ptr(keys), tokens, heads, dim, block_size,
+        _lib.dtype_code(keys.dtype), _lib.ptr(out), _lib.stream_of(keys),
+    )
+    return out
+
+
+def temporal_score_radius(
+    q_now: torch.Tensor,
+    q_prev: torch.Tensor,
+    w_now: torch.Tensor,
+    w_prev: torch.Tensor,
+    block_key_norm: torch.Tensor,
+) -> torch.Tensor:
+    """Certified |I_t - I_(t-1)| radius for every key block, fp32 ``[blocks]``.
+
+    radius_b = sum_h norm[b,h] * (|w_now-w_prev|_h ||q_prev,h|| + |w_now|_h ||q_now,h-q_prev,h||)
+    """
+
+    tensors = (q_now, q_prev, w_now, w_prev, block_key_norm)
+    if not all(t.is_cuda for t in tensors):
+        raise ValueError("HIP kernels require GPU tensors")
+    if q_now.shape != q_prev.shape or q_now.ndim != 2:
+        raise ValueError("query tensors must have shape [heads,dim]")
+    if w_now.shape != w_prev.shape or w_now.shape != (q_now.shape[0],):
+        raise ValueError("weight tensors must have shape [heads]")
+    if block_key_norm.ndim != 2 or block_key_norm.shape[1] != q_now.shape[0]:
+        raise ValueError("block_key_norm must have shape [blocks,heads]")
+    heads, dim = q_now.shape
+    f32 = [t.to(torch.float32).contiguous() for t in tensors]
+    out = torch.empty(block_key_norm.shape[0], device=q_now.device, dtype=torch.float32)
+    if out.numel() == 0:
+        return out
+    _lib.call(
+        "dsa_temporal_score_radius", *(_lib.ptr(t) for t in f32), block_key_norm.shape[0], heads,
+        dim, _lib.ptr(out), _lib.stream_of(q_now),
+    )
+    return out

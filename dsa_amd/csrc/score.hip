@@ -1,0 +1,634 @@
+// Indexer scoring kernels: dense batched scores (the decode hot path), the
+// fp32 accuracy path, and the block-granular H8 / masked / progressive kernels.
+//
+// score[s] = sum_h w_h * ReLU(q_h . k_s) over 64 heads x 128 dims.  The
+// 64x128 . 128xN head contraction runs on v_mfma_f32_16x16x32_{bf16,f16}; the
+// ReLU, the signed head weight and the 64-head reduction are applied to the
+// accumulators in registers, so only the fp32 score leaves the kernel.
+#include "common.hpp"
+#include "status.hpp"
+
+namespace dsa {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Key row formats.  `load` fetches the lane's 32-dim slice of one key of a
+// 16-key tile; `step(raw, j)` yields the 8 dims of MFMA k-step j as bf16/f16.
+// ---------------------------------------------------------------------------
+struct KeysB16 {  // bf16 or fp16 rows, 256 B
+  static constexpr int kRowBytes = 256;
+  static constexpr int kRaw = 4;
+  static constexpr bool kScaled = false;
+  __device__ static __forceinline__ void load(const uint8_t* base, int key, int g,
+                                              uint4 (&raw)[kRaw]) {
+    const uint4* p = reinterpret_cast<const uint4*>(base + (size_t)key * kRowBytes + g * 64);
+#pragma unroll
+    for (int c = 0; c < kRaw; ++c) raw[c] = p[c];
+  }
+  __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) { return raw[j]; }
+};
+
+struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
+  static constexpr int kRowBytes = 128;
+  static constexpr int kRaw = 2;
+  static constexpr bool kScaled = true;
+  __device__ static __forceinline__ void load(const uint8_t* base, int key, int g,
+                                              uint4 (&raw)[kRaw]) {
+    const uint4* p = reinterpret_cast<const uint4*>(base + (size_t)key * kRowBytes + g * 32);
+    raw[0] = p[0];
+    raw[1] = p[1];
+  }
+  __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) {
+    const uint4 v = raw[j >> 1];
+    return fp8x8_to_bf16x8((j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y));
+  }
+};
+
+// w_h * ReLU(acc) summed over the M-tiles' head slots held by this lane.
+template <class Tag, int M, class KF>
+__device__ __forceinline__ float tile_contrib(const uint4 (&qa)[M][4], const float (&wr)[M][4],
+                                              const uint4 (&raw)[KF::kRaw]) {
+  floatx4 acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint4 kf = KF::step(raw, j);
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = mfma_16x16x32(Tag{}, qa[m][j], kf, acc[m]);
+  }
+  float v = 0.f;
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v = fmaf(wr[m][i], fmaxf(acc[m][i], 0.f), v);
+  return v;
+}
+
+// Loads the A fragments of M head tiles.  Row slot s of the stacked tiles is
+// head ids[s] (or head s when ids == nullptr) for s < count, else a zero row.
+template <int M>
+__device__ __forceinline__ void load_head_tiles(const uint16_t* q, const float* w,
+                                                const int32_t* ids, int count, int r, int g,
+                                                uint4 (&qa)[M][4], float (&wr)[M][4]) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int slot = 16 * m + r;
+    const int head = slot < count ? (ids ? ids[slot] : slot) : -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      qa[m][j] = head >= 0 ? *reinterpret_cast<const uint4*>(q + head * kHeadDim + 32 * g + 8 * j)
+                           : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ws = 16 * m + 4 * g + i;
+      const int wh = ws < count ? (ids ? ids[ws] : ws) : -1;
+      wr[m][i] = wh >= 0 ? w[wh] : 0.f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dense scores for many query "sequences".  Sequence s has its own query block
+// (head_count heads gathered by head_ids, or heads 0..head_count-1) and weights,
+// and reads key set s / queries_per_keyset.  This one kernel covers batched
+// decode (one query per key set), multi-query scoring with an optional causal
+// mask (many queries per key set) and head-sparse verifier scoring.
+//
+// Flat grid: workgroup x = s * wgs_per_seq + chunk, 4 waves per workgroup; a
+// unit is 64 consecutive keys (4 MFMA tiles).  Each wave keeps its sequence's
+// query block in registers (16 VGPRs per 16-head tile of A fragments) and
+// streams units with a two-deep register prefetch.  After the four tiles of a
+// unit the per-lane partials are transposed and reduced across the four lane
+// groups so that lane l ends with the score of key 64u + l and the store is one
+// coalesced 256-byte row.
+// ---------------------------------------------------------------------------
+struct DenseArgs {
+  const uint16_t* q;
+  int64_t q_stride;  // elements between sequences' query blocks
+  const float* w;
+  int64_t w_stride;
+  const int32_t* head_ids;  // nullable
+  int64_t ids_stride;       // 0: one id list shared by all sequences
+  int32_t head_count;
+  const uint8_t* keys;
+  int64_t key_stride;  // key rows between key sets
+  int32_t queries_per_keyset;
+  const float* scales;
+  int64_t scale_stride;
+  float* out;
+  int64_t out_stride;
+  int32_t length;
+  int32_t causal_offset;  // < 0: no mask; else key j is valid for query t iff j <= t + offset
+  int32_t units_per_wg;
+  int32_t wgs_per_seq;
+};
+
+template <class KF>
+__device__ __forceinline__ void dense_load_unit(const uint8_t* keys, int u, int last, int r, int g,
+                                                uint4 (&buf)[4][KF::kRaw]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) KF::load(keys, min(u * 64 + 16 * t + r, last), g, buf[t]);
+}
+
+template <class Tag, class KF, int M>
+__device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], const float (&wr)[M][4],
+                                                   const uint4 (&buf)[4][KF::kRaw], int u,
+                                                   int valid, int L, int lane, int g,
+                                                   const float* scales, float* out) {
+  float s[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, M, KF>(qa, wr, buf[t]);
+  // Lane group g keeps tile g: two exchange rounds instead of four reductions.
+  const bool odd = g & 1;
+  const bool high = g & 2;
+  float keep_a = odd ? s[1] : s[0];
+  float keep_b = odd ? s[3] : s[2];
+  const float send_a = odd ? s[0] : s[1];
+  const float send_b = odd ? s[2] : s[3];
+  keep_a += __shfl_xor(send_a, 16, kWave);
+  keep_b += __shfl_xor(send_b, 16, kWave);
+  float keep = high ? keep_b : keep_a;
+  const float send = high ? keep_a : keep_b;
+  keep += __shfl_xor(send, 32, kWave);
+  const int key = u * 64 + lane;
+  if (key < L) {
+    if constexpr (KF::kScaled) keep *= scales[key >> 7];
+    out[key] = key < valid ? keep : -__builtin_inff();
+  }
+}
+
+template <class Tag, class KF, int M>
+__global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int64_t seq = blockIdx.x / a.wgs_per_seq;
+  const int chunk = blockIdx.x % a.wgs_per_seq;
+  const int L = a.length;
+  const int64_t keyset = seq / a.queries_per_keyset;
+  int valid = L;
+  if (a.causal_offset >= 0)
+    valid = min(L, (int)(seq % a.queries_per_keyset) + a.causal_offset + 1);
+
+  const uint8_t* keys = a.keys + keyset * a.key_stride * KF::kRowBytes;
+  float* out = a.out + seq * a.out_stride;
+  const float* scales = KF::kScaled ? a.scales + keyset * a.scale_stride : nullptr;
+
+  const int n_units = (L + 63) >> 6;
+  const int u_end = min(n_units, (chunk + 1) * a.units_per_wg);
+  int u = chunk * a.units_per_wg + wave;
+  if (u >= u_end) return;
+  // Units wholly past the causal limit only need -inf.
+  const int u_compute_end = min(u_end, (valid + 63) >> 6);
+  for (int uu = u; uu < u_end; uu += 4) {
+    const int key = uu * 64 + lane;
+    if (uu >= u_compute_end && key < L) out[key] = -__builtin_inff();
+  }
+  if (u >= u_compute_end) return;
+
+  uint4 qa[M][4];
+  float wr[M][4];
+  const int32_t* ids = a.head_ids ? a.head_ids + seq * a.ids_stride : nullptr;
+  load_head_tiles<M>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, ids, a.head_count, r, g, qa,
+                     wr);
+
+  const int last = max(valid, 1) - 1;
+  uint4 buf0[4][KF::kRaw];
+  uint4 buf1[4][KF::kRaw];
+  dense_load_unit<KF>(keys, u, last, r, g, buf0);
+  while (true) {
+    const int u1 = u + 4;
+    if (u1 < u_compute_end) dense_load_unit<KF>(keys, u1, last, r, g, buf1);
+    dense_compute_unit<Tag, KF, M>(qa, wr, buf0, u, valid, L, lane, g, scales, out);
+    if (u1 >= u_compute_end) break;
+    const int u2 = u1 + 4;
+    if (u2 < u_compute_end) dense_load_unit<KF>(keys, u2, last, r, g, buf0);
+    dense_compute_unit<Tag, KF, M>(qa, wr, buf1, u1, valid, L, lane, g, scales, out);
+    if (u2 >= u_compute_end) break;
+    u = u2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 keys and queries (accuracy path): v_mfma_f32_16x16x4_f32, queries
+// staged once per workgroup in LDS (rows padded to 129 floats), one 16-key
+// tile per wave.  k-step j of lane group g uses dim 32 * g + j.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dense_scores_f32_kernel(const float* q_all,
+                                                               const float* w_all,
+                                                               const float* keys_all,
+                                                               float* out_all, int L) {
+  __shared__ float qs[kHeads][kHeadDim + 1];
+  const int64_t b = blockIdx.y;
+  const float* q = q_all + b * (kHeads * kHeadDim);
+  for (int i = threadIdx.x; i < kHeads * kHeadDim; i += blockDim.x)
+    qs[i / kHeadDim][i % kHeadDim] = q[i];
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int key0 = (blockIdx.x * 4 + wave) * 16;
+  if (key0 >= L) return;
+  const float* w = w_all + b * kHeads;
+  const float* keys = keys_all + b * (int64_t)L * kHeadDim;
+  const int key = min(key0 + r, L - 1);
+  float kv[32];
+  const float4* kp = reinterpret_cast<const float4*>(keys + (size_t)key * kHeadDim + 32 * g);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float4 v = kp[c];
+    kv[4 * c + 0] = v.x;
+    kv[4 * c + 1] = v.y;
+    kv[4 * c + 2] = v.z;
+    kv[4 * c + 3] = v.w;
+  }
+  float total = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[16 * m + r][32 * g + j], kv[j], acc, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) total = fmaf(w[16 * m + 4 * g + i], fmaxf(acc[i], 0.f), total);
+  }
+  total = reduce_lane_groups(total);
+  if (g == 0 && key0 + r < L) out_all[b * (int64_t)L + key0 + r] = total;
+}
+
+// ---------------------------------------------------------------------------
+// Block-granular kernels (one wave per decision block of 16 * T keys).
+// ---------------------------------------------------------------------------
+enum BlockMode { kModeH8 = 0, kModeMasked = 1, kModeProgressive = 2 };
+
+struct BlockArgs {
+  const uint16_t* q;
+  const float* w;
+  const uint8_t* keys;
+  const float* scales;
+  const int32_t* selected;
+  const int32_t* remaining;
+  const uint8_t* mask;  // cold (H8), keep (masked), direct (progressive)
+  const float* threshold;
+  float* out_scores;
+  int32_t* out_indices;
+  int8_t* accepted;
+  float* block_max;
+  int32_t* counter;
+  int32_t length;
+  int32_t compact;
+};
+
+template <class KF>
+__device__ __forceinline__ float key_scale(const float* scales, int key) {
+  if constexpr (KF::kScaled) return scales[key >> 7];
+  return 1.f;
+}
+
+template <class Tag, class KF, int MODE, int T>
+__global__ __launch_bounds__(256) void block_kernel(BlockArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int L = a.length;
+  constexpr int kBlock = 16 * T;
+  const int nb = (L + kBlock - 1) / kBlock;
+  const int block = blockIdx.x * 4 + wave;
+  if (block >= nb) return;
+  const int start = block * kBlock;
+  const float neg_inf = -__builtin_inff();
+  const bool flag = a.mask[block] != 0;
+
+  if constexpr (MODE == kModeMasked) {
+    if (!flag) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int key = start + 16 * t + r;
+        if (g == 0 && key < L) a.out_scores[key] = neg_inf;
+      }
+      return;
+    }
+    uint4 qa[4][4];
+    float wr[4][4];
+    load_head_tiles<4>(a.q, a.w, nullptr, kHeads, r, g, qa, wr);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint4 raw[KF::kRaw];
+      const int key = start + 16 * t + r;
+      KF::load(a.keys, min(key, L - 1), g, raw);
+      float v = reduce_lane_groups(tile_contrib<Tag, 4, KF>(qa, wr, raw));
+      if (g == 0 && key < L) a.out_scores[key] = v * key_scale<KF>(a.scales, key);
+    }
+  } else if constexpr (MODE == kModeH8) {
+    if (!flag) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int key = start + 16 * t + r;
+        if (g == 0 && key < L) a.out_scores[key] = neg_inf;
+      }
+      if (lane == 0) a.block_max[block] = neg_inf;
+      return;
+    }
+    uint4 qa[1][4];
+    float wr[1][4];
+    load_head_tiles<1>(a.q, a.w, a.selected, kVerifierHeads, r, g, qa, wr);
+    float maximum = neg_inf;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      uint4 raw[KF::kRaw];
+      const int key = start + 16 * t + r;
+      KF::load(a.keys, min(key, L - 1), g, raw);
+      float v = reduce_lane_groups(tile_contrib<Tag, 1, KF>(qa, wr, raw));
+      v = key < L ? v * key_scale<KF>(a.scales, key) : neg_inf;
+      maximum = fmaxf(maximum, v);
+      if (g == 0 && key < L) a.out_scores[key] = v;
+    }
+    maximum = wave_max(maximum);
+    if (lane == 0) a.block_max[block] = maximum;
+  } else {  // kModeProgressive
+    uint4 qs[1][4];
+    float ws[1][4];
+    load_head_tiles<1>(a.q, a.w, a.selected, kVerifierHeads, r, g, qs, ws);
+    uint4 raw[T][KF::kRaw];
+    float p[T];
+    float maximum = neg_inf;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int key = start + 16 * t + r;
+      KF::load(a.keys, min(key, L - 1), g, raw[t]);
+      p[t] = reduce_lane_groups(tile_contrib<Tag, 1, KF>(qs, ws, raw[t]));
+      if (key < L) maximum = fmaxf(maximum, p[t] * key_scale<KF>(a.scales, key));
+    }
+    maximum = wave_max(maximum);
+    const bool promote = !flag && maximum >= *a.threshold;
+    const bool accept = flag || promote;
+    if (accept) {
+      uint4 qr[4][4];
+      float wrr[4][4];
+      load_head_tiles<4>(a.q, a.w, a.remaining, kHeads - kVerifierHeads, r, g, qr, wrr);
+#pragma unroll
+      for (int t = 0; t < T; ++t) p[t] += reduce_lane_groups(tile_contrib<Tag, 4, KF>(qr, wrr, raw[t]));
+    }
+    if (lane == 0) {
+      a.accepted[block] = accept ? 1 : 0;
+      a.block_max[block] = flag ? neg_inf : maximum;
+    }
+    if (!a.compact) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int key = start + 16 * t + r;
+        if (g == 0 && key < L)
+          a.out_scores[key] = accept ? p[t] * key_scale<KF>(a.scales, key) : neg_inf;
+      }
+    } else if (accept) {
+      const int valid = min(kBlock, L - start);
+      int slot = 0;
+      if (lane == 0) slot = atomicAdd(a.counter, valid);
+      slot = __shfl(slot, 0, kWave);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int offset = 16 * t + r;
+        if (g == 0 && offset < valid) {
+          a.out_scores[slot + offset] = p[t] * key_scale<KF>(a.scales, start + offset);
+          a.out_indices[slot + offset] = start + offset;
+        }
+      }
+    }
+  }
+}
+
+__global__ void promote_blocks_kernel(const uint8_t* direct, const float* block_max,
+                                      const float* threshold, uint8_t* accepted, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) accepted[i] = (direct[i] != 0 || block_max[i] >= *threshold) ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch helpers.
+// ---------------------------------------------------------------------------
+int units_per_workgroup(int64_t sequences, int64_t length) {
+  // Aim for about eight workgroups of four waves per CU over all sequences
+  // while keeping at least four units (one per wave) in each workgroup.
+  const int64_t units = (length + 63) / 64;
+  const int64_t target_wgs = 2048;
+  int64_t per = (units * sequences + target_wgs - 1) / target_wgs;
+  per = per < 4 ? 4 : per;
+  per = (per + 3) / 4 * 4;
+  return (int)per;
+}
+
+template <class Tag, class KF, int M>
+int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
+  const int64_t units = (a.length + 63) / 64;
+  a.units_per_wg = units_per_workgroup(sequences, a.length);
+  a.wgs_per_seq = (int32_t)((units + a.units_per_wg - 1) / a.units_per_wg);
+  const int64_t grid = sequences * a.wgs_per_seq;
+  if (grid > 0x7fffffffLL) return fail(DSA_STATUS_INVALID_ARGUMENT, "problem too large");
+  hipLaunchKernelGGL((dense_scores_kernel<Tag, KF, M>), dim3((unsigned)grid), dim3(256), 0, stream,
+                     a);
+  return check_launch("dense_scores_kernel");
+}
+
+template <class Tag, class KF>
+int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
+  switch ((a.head_count + 15) / 16) {
+    case 1: return launch_dense_m<Tag, KF, 1>(a, sequences, stream);
+    case 2: return launch_dense_m<Tag, KF, 2>(a, sequences, stream);
+    case 3: return launch_dense_m<Tag, KF, 3>(a, sequences, stream);
+    default: return launch_dense_m<Tag, KF, 4>(a, sequences, stream);
+  }
+}
+
+template <class Tag, class KF, int MODE>
+int launch_block(const BlockArgs& a, int block_size, hipStream_t stream) {
+  const int nb = (a.length + block_size - 1) / block_size;
+  dim3 grid((unsigned)((nb + 3) / 4));
+  switch (block_size) {
+    case 16: hipLaunchKernelGGL((block_kernel<Tag, KF, MODE, 1>), grid, dim3(256), 0, stream, a); break;
+    case 32: hipLaunchKernelGGL((block_kernel<Tag, KF, MODE, 2>), grid, dim3(256), 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((block_kernel<Tag, KF, MODE, 4>), grid, dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((block_kernel<Tag, KF, MODE, 8>), grid, dim3(256), 0, stream, a); break;
+  }
+  return check_launch("block_kernel");
+}
+
+template <int MODE>
+int dispatch_block(BlockArgs& a, int block_size, int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case kBF16: return launch_block<Bf16Tag, KeysB16, MODE>(a, block_size, stream);
+    case kF16: return launch_block<F16Tag, KeysB16, MODE>(a, block_size, stream);
+    case kFP8E4M3: return launch_block<Bf16Tag, KeysFP8, MODE>(a, block_size, stream);
+    default:
+      return fail(DSA_STATUS_INVALID_ARGUMENT, "block kernels take fp16/bf16/fp8 keys, got dtype %d",
+                  dtype);
+  }
+}
+
+int check_block_common(const void* q, const float* w, const void* keys, int64_t length,
+                       int32_t block_size) {
+  DSA_REQUIRE(q && w && keys, "queries, weights and keys must be non-null");
+  DSA_REQUIRE(length > 0 && length < (int64_t(1) << 30), "length %lld out of range",
+              (long long)length);
+  DSA_REQUIRE(block_size == 16 || block_size == 32 || block_size == 64 || block_size == 128,
+              "block_size must be 16, 32, 64 or 128 (got %d)", block_size);
+  return DSA_STATUS_OK;
+}
+
+}  // namespace
+}  // namespace dsa
+
+using namespace dsa;
+
+extern "C" int dsa_score_queries(const void* queries, int64_t q_stride, const float* weights,
+                                 int64_t w_stride, const int32_t* head_ids, int64_t ids_stride,
+                                 int32_t head_count, const void* keys, int64_t key_stride,
+                                 int64_t queries_per_keyset, const float* key_scales,
+                                 int64_t scale_stride, float* out, int64_t out_stride,
+                                 int64_t sequences, int64_t length, int64_t causal_offset,
+                                 int32_t key_dtype, void* stream) {
+  DSA_REQUIRE(queries && weights && keys && out, "null pointer argument");
+  DSA_REQUIRE(sequences > 0, "sequences must be positive");
+  DSA_REQUIRE(length > 0 && length < (int64_t(1) << 30), "length %lld out of range",
+              (long long)length);
+  DSA_REQUIRE(head_count > 0 && head_count <= kHeads, "head_count %d outside [1, 64]", head_count);
+  DSA_REQUIRE(queries_per_keyset > 0 && queries_per_keyset < (int64_t(1) << 31),
+              "queries_per_keyset out of range");
+  DSA_REQUIRE(causal_offset < (int64_t(1) << 30), "causal_offset out of range");
+  DSA_REQUIRE(out_stride >= length, "out_stride < length");
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(queries) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(keys) % 16 == 0,
+              "queries and keys must be 16-byte aligned");
+  DSA_REQUIRE(q_stride % 8 == 0, "q_stride must keep 16-byte alignment");
+  DenseArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.q_stride = q_stride;
+  a.w = weights;
+  a.w_stride = w_stride;
+  a.head_ids = head_ids;
+  a.ids_stride = ids_stride;
+  a.head_count = head_count;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.key_stride = key_stride;
+  a.queries_per_keyset = (int32_t)queries_per_keyset;
+  a.scales = key_scales;
+  a.scale_stride = scale_stride;
+  a.out = out;
+  a.out_stride = out_stride;
+  a.length = (int32_t)length;
+  a.causal_offset = causal_offset < 0 ? -1 : (int32_t)causal_offset;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (key_dtype) {
+    case kBF16: return launch_dense<Bf16Tag, KeysB16>(a, sequences, s);
+    case kF16: return launch_dense<F16Tag, KeysB16>(a, sequences, s);
+    case kFP8E4M3:
+      DSA_REQUIRE(key_scales, "fp8 keys need key_scales");
+      return launch_dense<Bf16Tag, KeysFP8>(a, sequences, s);
+    default:
+      return fail(DSA_STATUS_INVALID_ARGUMENT, "dsa_score_queries takes fp16/bf16/fp8 keys (got %d)",
+                  key_dtype);
+  }
+}
+
+extern "C" int dsa_full_scores(const void* queries, const float* weights, const void* keys,
+                               const float* key_scales, float* out, int64_t batch, int64_t length,
+                               int32_t key_dtype, void* stream) {
+  DSA_REQUIRE(queries && weights && keys && out, "null pointer argument");
+  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
+  DSA_REQUIRE(length > 0 && length < (int64_t(1) << 30), "length %lld out of range",
+              (long long)length);
+  if (key_dtype == kF32) {
+    dim3 grid((unsigned)((length + 63) / 64), (unsigned)batch);
+    hipLaunchKernelGGL(dense_scores_f32_kernel, grid, dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const float*>(queries),
+                       weights, static_cast<const float*>(keys), out, (int)length);
+    return check_launch("dense_scores_f32_kernel");
+  }
+  return dsa_score_queries(queries, kHeads * kHeadDim, weights, kHeads, nullptr, 0, kHeads, keys,
+                           length, 1, key_scales, (length + 127) / 128, out, length, batch, length,
+                           -1, key_dtype, stream);
+}
+
+extern "C" int dsa_h8_block_max(const void* queries, const float* weights, const void* keys,
+                                const int32_t* selected_heads, const uint8_t* cold_blocks,
+                                float* partial, float* block_max, int64_t length,
+                                int32_t block_size, int32_t key_dtype, void* stream) {
+  if (int st = check_block_common(queries, weights, keys, length, block_size)) return st;
+  DSA_REQUIRE(selected_heads && cold_blocks && partial && block_max, "null pointer argument");
+  DSA_REQUIRE(key_dtype != kFP8E4M3, "fp8 keys need scales; use the fp16/bf16 path");
+  BlockArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.w = weights;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.selected = selected_heads;
+  a.mask = cold_blocks;
+  a.out_scores = partial;
+  a.block_max = block_max;
+  a.length = (int32_t)length;
+  return dispatch_block<kModeH8>(a, block_size, key_dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsa_masked_full_scores(const void* queries, const float* weights, const void* keys,
+                                      const uint8_t* keep_blocks, float* out, int64_t length,
+                                      int32_t block_size, int32_t key_dtype, void* stream) {
+  if (int st = check_block_common(queries, weights, keys, length, block_size)) return st;
+  DSA_REQUIRE(keep_blocks && out, "null pointer argument");
+  DSA_REQUIRE(key_dtype != kFP8E4M3, "fp8 keys need scales; use the fp16/bf16 path");
+  BlockArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.w = weights;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.mask = keep_blocks;
+  a.out_scores = out;
+  a.length = (int32_t)length;
+  return dispatch_block<kModeMasked>(a, block_size, key_dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsa_progressive_scores(const void* queries, const float* weights, const void* keys,
+                                      const int32_t* selected_heads,
+                                      const int32_t* remaining_heads,
+                                      const uint8_t* direct_blocks, const float* threshold,
+                                      float* out_scores, int32_t* out_indices, int8_t* accepted,
+                                      float* block_max, int32_t* counter, int64_t length,
+                                      int32_t block_size, int32_t compact, int32_t key_dtype,
+                                      void* stream) {
+  if (int st = check_block_common(queries, weights, keys, length, block_size)) return st;
+  DSA_REQUIRE(selected_heads && remaining_heads && direct_blocks && threshold && out_scores &&
+                  accepted && block_max,
+              "null pointer argument");
+  DSA_REQUIRE(!compact || (out_indices && counter), "compact output needs indices and counter");
+  DSA_REQUIRE(key_dtype != kFP8E4M3, "fp8 keys need scales; use the fp16/bf16 path");
+  BlockArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.w = weights;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.selected = selected_heads;
+  a.remaining = remaining_heads;
+  a.mask = direct_blocks;
+  a.threshold = threshold;
+  a.out_scores = out_scores;
+  a.out_indices = out_indices;
+  a.accepted = accepted;
+  a.block_max = block_max;
+  a.counter = counter;
+  a.length = (int32_t)length;
+  a.compact = compact ? 1 : 0;
+  return dispatch_block<kModeProgressive>(a, block_size, key_dtype,
+                                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsa_promote_blocks(const uint8_t* direct_blocks, const float* block_max,
+                                  const float* threshold, uint8_t* accepted, int64_t blocks,
+                                  void* stream) {
+  DSA_REQUIRE(direct_blocks && block_max && threshold && accepted, "null pointer argument");
+  DSA_REQUIRE(blocks > 0, "blocks must be positive");
+  const unsigned grid = (unsigned)((blocks + 255) / 256);
+  hipLaunchKernelGGL(promote_blocks_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), direct_blocks, block_max, threshold,
+                     accepted, blocks);
+  return check_launch("promote_blocks_kernel");
+}

@@ -1,0 +1,143 @@
+// Block summaries used by the temporal pruning bounds:
+//   * per-block maxima of score rows (reference replay.py:149-150, approx.py:53-55)
+//   * per-block maximum key norms (reference certified.py:51-62)
+//   * the certified temporal radius (reference certified.py:18-48)
+#include "common.hpp"
+#include "status.hpp"
+
+namespace dsa {
+namespace {
+
+// One thread per (row, block).
+__global__ __launch_bounds__(256) void block_max_kernel(const float* scores, int64_t rows,
+                                                        int length, int64_t row_stride, int bs,
+                                                        float* out) {
+  const int nb = (length + bs - 1) / bs;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / nb;
+  const int block = (int)(gid % nb);
+  if (row >= rows) return;
+  const float* x = scores + row * row_stride;
+  const int start = block * bs;
+  const int stop = min(length, start + bs);
+  float m = -__builtin_inff();
+  for (int i = start; i < stop; ++i) m = fmaxf(m, x[i]);
+  // numpy's max propagates NaN; fmaxf drops it.  Scores are NaN-free by contract.
+  out[row * nb + block] = m;
+}
+
+__device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dtype) {
+  switch (dtype) {
+    case kF32: return static_cast<const float*>(p)[i];
+    case kF16: return (float)static_cast<const _Float16*>(p)[i];
+    case kBF16: return __uint_as_float(uint32_t(static_cast<const uint16_t*>(p)[i]) << 16);
+    default: {
+      const uint32_t byte = static_cast<const uint8_t*>(p)[i];
+      return __builtin_amdgcn_cvt_pk_f32_fp8(byte, false)[0];
+    }
+  }
+}
+
+// One wave per (block, head).
+__global__ __launch_bounds__(256) void block_key_norms_kernel(const void* keys, int64_t tokens,
+                                                              int heads, int dim, int bs,
+                                                              int dtype, float* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nb = (tokens + bs - 1) / bs;
+  if (wid >= nb * heads) return;
+  const int64_t block = wid / heads;
+  const int head = (int)(wid % heads);
+  const int64_t start = block * bs;
+  const int64_t stop = min(tokens, start + bs);
+  float best = 0.f;
+  for (int64_t t = start; t < stop; ++t) {
+    const int64_t row = (t * heads + head) * dim;
+    float acc = 0.f;
+    for (int d = lane; d < dim; d += kWave) {
+      const float x = load_as_float(keys, row + d, dtype);
+      acc = fmaf(x, x, acc);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    best = fmaxf(best, sqrtf(acc));
+  }
+  if (lane == 0) out[block * heads + head] = best;
+}
+
+constexpr int kMaxRadiusHeads = 1024;
+
+__global__ __launch_bounds__(256) void temporal_radius_kernel(const float* q_now,
+                                                              const float* q_prev,
+                                                              const float* w_now,
+                                                              const float* w_prev,
+                                                              const float* norms, int64_t blocks,
+                                                              int heads, int dim, float* out) {
+  __shared__ float coef[kMaxRadiusHeads];
+  for (int h = threadIdx.x; h < heads; h += blockDim.x) {
+    float prev_sq = 0.f;
+    float diff_sq = 0.f;
+    for (int d = 0; d < dim; ++d) {
+      const float p = q_prev[h * dim + d];
+      const float c = q_now[h * dim + d];
+      prev_sq = fmaf(p, p, prev_sq);
+      diff_sq = fmaf(c - p, c - p, diff_sq);
+    }
+    coef[h] = fabsf(w_now[h] - w_prev[h]) * sqrtf(prev_sq) + fabsf(w_now[h]) * sqrtf(diff_sq);
+  }
+  __syncthreads();
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < blocks;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    float r = 0.f;
+    for (int h = 0; h < heads; ++h) r = fmaf(norms[b * heads + h], coef[h], r);
+    out[b] = r;
+  }
+}
+
+}  // namespace
+}  // namespace dsa
+
+using namespace dsa;
+
+extern "C" int dsa_block_max(const float* scores, int64_t rows, int64_t length,
+                             int64_t row_stride, int32_t block_size, float* out, void* stream) {
+  DSA_REQUIRE(scores && out, "null pointer argument");
+  DSA_REQUIRE(rows > 0 && length > 0 && length < (int64_t(1) << 31), "bad shape");
+  DSA_REQUIRE(row_stride >= length, "row_stride < length");
+  DSA_REQUIRE(block_size > 0, "block_size must be positive");
+  const int64_t nb = (length + block_size - 1) / block_size;
+  const int64_t total = rows * nb;
+  hipLaunchKernelGGL(block_max_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), scores, rows, (int)length, row_stride,
+                     (int)block_size, out);
+  return check_launch("block_max_kernel");
+}
+
+extern "C" int dsa_block_key_norms(const void* keys, int64_t tokens, int64_t heads, int64_t dim,
+                                   int32_t block_size, int32_t key_dtype, float* out,
+                                   void* stream) {
+  DSA_REQUIRE(keys && out, "null pointer argument");
+  DSA_REQUIRE(tokens > 0 && heads > 0 && dim > 0, "bad shape");
+  DSA_REQUIRE(block_size > 0, "block_size must be positive");
+  DSA_REQUIRE(key_dtype >= kF32 && key_dtype <= kFP8E4M3, "unknown dtype %d", key_dtype);
+  const int64_t nb = (tokens + block_size - 1) / block_size;
+  const int64_t waves = nb * heads;
+  hipLaunchKernelGGL(block_key_norms_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), keys, tokens, (int)heads, (int)dim,
+                     (int)block_size, (int)key_dtype, out);
+  return check_launch("block_key_norms_kernel");
+}
+
+extern "C" int dsa_temporal_score_radius(const float* q_now, const float* q_prev,
+                                         const float* w_now, const float* w_prev,
+                                         const float* block_key_norm, int64_t blocks,
+                                         int64_t heads, int64_t dim, float* out, void* stream) {
+  DSA_REQUIRE(q_now && q_prev && w_now && w_prev && block_key_norm && out, "null pointer");
+  DSA_REQUIRE(blocks > 0 && heads > 0 && heads <= kMaxRadiusHeads && dim > 0, "bad shape");
+  const int64_t want = (blocks + 255) / 256;
+  const unsigned grid = (unsigned)(want < 1024 ? want : 1024);
+  hipLaunchKernelGGL(temporal_radius_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), q_now, q_prev, w_now, w_prev,
+                     block_key_norm, blocks, (int)heads, (int)dim, out);
+  return check_launch("temporal_radius_kernel");
+}

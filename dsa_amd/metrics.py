@@ -1,0 +1,131 @@
+"""Top-K selection and recall with the reference's metrics API.
+
+Mirrors ``temporal_dsa.metrics`` (reference ``src/temporal_dsa/metrics.py``).
+``stable_topk`` keeps the reference's definition (metrics.py:9-22): the k
+largest values, ties at the cut-off resolved towards the lower index, returned
+sorted by (value desc, index asc).  It runs on the GPU radix-select kernel;
+host (numpy) inputs are copied to the current GPU and the result is returned as
+a numpy int64 array, like the reference.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+
+MAX_K = 4096
+MAX_ROW = 32768
+
+
+def _device() -> torch.device:
+    _lib.load()
+    if not torch.cuda.is_available():
+        raise RuntimeError("stable_topk runs on the GPU; no HIP device is available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def topk(
+    scores: torch.Tensor,
+    k: int,
+    *,
+    sorted: bool = True,
+    row_lengths: torch.Tensor | None = None,
+    return_values: bool = False,
+) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """Row-wise stable top-k of a GPU fp32 matrix ``[rows, L]`` (or vector).
+
+    ``sorted=True`` orders each row by (value desc, index asc); ``sorted=False``
+    returns the same set in ascending index order.  ``row_lengths`` (int32,
+    per row) limits the candidates to a row's first entries; rows with fewer
+    than k candidates are padded with index -1 and value -inf.
+    """
+
+    if not scores.is_cuda:
+        raise ValueError("topk expects a GPU tensor; use stable_topk for host arrays")
+    squeeze = scores.ndim == 1
+    matrix = scores.reshape(1, -1) if squeeze else scores
+    if matrix.ndim != 2:
+        raise ValueError(f"expected a vector or a matrix, got {tuple(scores.shape)}")
+    matrix = matrix.to(torch.float32)
+    if matrix.stride(1) != 1:
+        matrix = matrix.contiguous()
+    rows, length = matrix.shape
+    if not 0 < k <= MAX_K:
+        raise ValueError(f"k={k} outside [1, {MAX_K}]")
+    if length == 0:
+        raise ValueError("cannot take top-k of an empty row")
+    indices = torch.empty((rows, k), device=matrix.device, dtype=torch.int64)
+    values = torch.empty((rows, k), device=matrix.device, dtype=torch.float32) if return_values else None
+    stream = _lib.stream_of(matrix)
+    if length <= MAX_ROW:
+        lengths = None
+        if row_lengths is not None:
+            lengths = row_lengths.to(device=matrix.device, dtype=torch.int32).contiguous()
+            if lengths.numel() != rows:
+                raise ValueError("row_lengths needs one entry per row")
+        _lib.call(
+            "dsa_topk", _lib.ptr(matrix), None, rows, length, matrix.stride(0), _lib.ptr(lengths),
+            k, int(sorted), _lib.ptr(indices), _lib.ptr(values), stream,
+        )
+    else:
+        if row_lengths is not None:
+            raise ValueError(f"row_lengths is supported for rows up to {MAX_ROW} entries")
+        matrix = matrix.contiguous()
+        need = int(_lib.query("dsa_topk_long_workspace_bytes", rows, length, k))
+        workspace = torch.empty(max(need, 1), device=matrix.device, dtype=torch.uint8)
+        _lib.call(
+            "dsa_topk_long", _lib.ptr(matrix), rows, length, k, int(sorted), _lib.ptr(indices),
+            _lib.ptr(values), _lib.ptr(workspace), need, stream,
+        )
+    if squeeze:
+        indices = indices[0]
+        values = values[0] if values is not None else None
+    return (indices, values) if return_values else indices
+
+
+def stable_topk(values: np.ndarray | torch.Tensor, k: int) -> np.ndarray | torch.Tensor:
+    """Descending top-k indices with the index as deterministic tie-breaker.
+
+    Reference: metrics.py:9-22 (same validation and messages).  A GPU tensor
+    yields a GPU int64 tensor; anything else yields a numpy int64 array.
+    """
+
+    on_gpu = isinstance(values, torch.Tensor) and values.is_cuda
+    if isinstance(values, torch.Tensor):
+        shape = tuple(values.shape)
+        size = values.numel()
+    else:
+        array = np.asarray(values)
+        shape = array.shape
+        size = array.size
+    if len(shape) != 1:
+        raise ValueError(f"expected a vector, got {shape}")
+    if not 0 < k <= size:
+        raise ValueError(f"k={k} is invalid for {size} values")
+    if on_gpu:
+        return topk(values, k, sorted=True)
+    device = _device()
+    host = values.detach().cpu().numpy() if isinstance(values, torch.Tensor) else array
+    tensor = torch.from_numpy(np.ascontiguousarray(host, dtype=np.float32)).to(device)
+    return topk(tensor, k, sorted=True).cpu().numpy()
+
+
+def topk_recall(predicted, target) -> float:
+    """Recall@K = |predicted ∩ target| / |target| (reference metrics.py:25-30)."""
+
+    predicted = np.asarray(predicted.cpu() if isinstance(predicted, torch.Tensor) else predicted)
+    target = np.asarray(target.cpu() if isinstance(target, torch.Tensor) else target)
+    if target.size == 0:
+        return 1.0
+    return float(np.intersect1d(predicted, target, assume_unique=False).size / target.size)
+
+
+def normalized_recall_lift(recall: float, k: int, length: int) -> float:
+    """Recall lift over random selection (reference metrics.py:33-37)."""
+
+    random_recall = min(1.0, k / length)
+    if random_recall == 1.0:
+        return 1.0
+    return float((recall - random_recall) / (1.0 - random_recall))

@@ -1,0 +1,209 @@
+/*
+ * dsa_amd.h -- C ABI of the MI355X (gfx950) Lightning-Indexer decode path.
+ *
+ * Every entry point takes raw device pointers, plain sizes and a hipStream_t
+ * passed as `void*` (NULL = the legacy default stream), launches
+ * asynchronously on that stream and returns a status code.  The library never
+ * allocates device memory: outputs and workspaces are owned by the caller.
+ * On a non-zero status dsa_last_error() returns a message for the calling
+ * thread.
+ *
+ * Shapes follow the reference's `temporal_dsa` package (psa1582/dsa):
+ *   queries  [64, 128]   fp16 / bf16 (fp32 for the fp32 path)
+ *   weights  [64]        fp32 (signed head weights)
+ *   keys     [L, 128]    same dtype as queries, or fp8 e4m3fn with one fp32
+ *                        scale per 128-key block (scales must be >= 0)
+ *   score[s] = sum_h w_h * ReLU(q_h . k_s), fp32 accumulation.
+ * All arrays are contiguous row-major.  Block masks are one byte per block
+ * (torch.bool or torch.int8); zero means false.
+ */
+#ifndef DSA_AMD_H
+#define DSA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_ABI_VERSION 1
+
+#define DSA_STATUS_OK 0
+#define DSA_STATUS_INVALID_ARGUMENT 1
+#define DSA_STATUS_HIP_ERROR 2
+#define DSA_STATUS_WORKSPACE_TOO_SMALL 3
+
+/* Key / query element types. */
+#define DSA_DTYPE_F32 0
+#define DSA_DTYPE_F16 1
+#define DSA_DTYPE_BF16 2
+#define DSA_DTYPE_FP8_E4M3 3 /* keys only; queries are bf16 */
+
+/* Message describing the last failure on the calling thread. */
+const char* dsa_last_error(void);
+
+/* DSA_ABI_VERSION of the loaded library. */
+int dsa_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Dense indexer scores for a batch of independent decode sequences.
+ *
+ * Replaces progressive_kernel.py:362-375 (full_scores_triton, batch = 1,
+ * `block_size` only affects the reference's launch tiling) and the Q = 1 case
+ * of sidecar.py:89-107 (LightningIndexerSidecar.score_encoded).
+ *
+ *   queries    [batch, 64, 128]    q_dtype (bf16/f16/f32; bf16 when fp8 keys)
+ *   weights    [batch, 64]         fp32
+ *   keys       [batch, length, 128] key_dtype
+ *   key_scales [batch, ceil(length/128)] fp32, fp8 keys only (else NULL)
+ *   out        [batch, length]     fp32
+ * Strides between sequences are the dense ones (64*128, 64, length*128,
+ * ceil(length/128), length).
+ * ------------------------------------------------------------------------ */
+int dsa_full_scores(const void* queries, const float* weights, const void* keys,
+                    const float* key_scales, float* out, int64_t batch, int64_t length,
+                    int32_t key_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * General query-block scoring: `sequences` query blocks, each scored against
+ * one key set.  Sequence s uses
+ *   queries + s*q_stride      a [H, 128] block (fp16/bf16), H >= head rows used
+ *   weights + s*w_stride      fp32 per head
+ *   head_ids + s*ids_stride   int32 ids of the head_count (<= 64) heads used,
+ *                             or NULL for heads 0..head_count-1
+ *   keys + (s / queries_per_keyset) * key_stride rows   [length, 128]
+ *   key_scales + (s / queries_per_keyset) * scale_stride (fp8 keys only)
+ *   out + s*out_stride        fp32 [length]
+ * causal_offset >= 0 masks key j of query t = s % queries_per_keyset unless
+ * j <= t + causal_offset (masked scores are -inf); < 0 disables the mask.
+ *
+ * Replaces sidecar.py:89-107 (score_encoded: B key sets, Q queries each) and
+ * verifier_scoring.py:49-92 (score_head_sparse: fixed [h_v] or per-query
+ * [Q, h_v] head ids, one shared key set).  Queries and keys must be 16-byte
+ * aligned and q_stride a multiple of 8 elements.
+ * ------------------------------------------------------------------------ */
+int dsa_score_queries(const void* queries, int64_t q_stride, const float* weights,
+                      int64_t w_stride, const int32_t* head_ids, int64_t ids_stride,
+                      int32_t head_count, const void* keys, int64_t key_stride,
+                      int64_t queries_per_keyset, const float* key_scales, int64_t scale_stride,
+                      float* out, int64_t out_stride, int64_t sequences, int64_t length,
+                      int64_t causal_offset, int32_t key_dtype, void* stream);
+
+/* Head routing: per row of weights [rows, heads] (heads <= 64) the `width`
+ * head ids with the largest |w| (positive_only == 0) or max(w, 0)
+ * (positive_only != 0), ties to the lower id, in rank order.  Output to
+ * out_int32 and/or out_int64 [rows, width].
+ * Replaces progressive_kernel.py:37-42 (dynamic_head_ids) and
+ * verifier_scoring.py:142-159 (dynamic_head_indices). */
+int dsa_route_heads(const float* weights, int64_t rows, int64_t heads, int64_t width,
+                    int32_t positive_only, int32_t* out_int32, int64_t* out_int64, void* stream);
+
+/* ------------------------------------------------------------------------
+ * H8 verifier partial scores and per-block maxima.
+ * Replaces progressive_kernel.py:378-404 (h8_block_max_triton) /
+ * progressive_kernel.py:218-246 (_h8_block_max_kernel).
+ *
+ *   selected_heads [8] int32 device array, cold_blocks [ceil(L/bs)] bytes.
+ *   partial[s] = sum over the 8 selected heads where the block is cold, else
+ *   -inf; block_max[b] = max of partial over the block (-inf if not cold).
+ * ------------------------------------------------------------------------ */
+int dsa_h8_block_max(const void* queries, const float* weights, const void* keys,
+                     const int32_t* selected_heads, const uint8_t* cold_blocks, float* partial,
+                     float* block_max, int64_t length, int32_t block_size, int32_t key_dtype,
+                     void* stream);
+
+/* ------------------------------------------------------------------------
+ * Full scores on kept blocks, -inf elsewhere; rejected blocks load no keys.
+ * Replaces progressive_kernel.py:407-424 (masked_full_scores_triton).
+ * ------------------------------------------------------------------------ */
+int dsa_masked_full_scores(const void* queries, const float* weights, const void* keys,
+                           const uint8_t* keep_blocks, float* out, int64_t length,
+                           int32_t block_size, int32_t key_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused progressive scoring: direct blocks get all 64 heads; other blocks get
+ * the 8 selected heads, their maximum is compared with *threshold and blocks
+ * with max >= threshold are promoted to the 56 remaining heads.
+ * Replaces progressive_kernel.py:427-475 (progressive_scores_triton) /
+ * progressive_kernel.py:277-346 (_progressive_kernel).
+ *
+ *   selected_heads [8], remaining_heads [56] int32 device arrays
+ *   direct_blocks  [nb] bytes, threshold [1] fp32 device scalar
+ *   accepted [nb] int8, block_max [nb] fp32 (-inf for direct blocks)
+ *   compact == 0: out_scores [L] = score or -inf, out_indices unused (NULL ok)
+ *   compact != 0: accepted keys are appended to out_scores/out_indices at
+ *                 positions reserved by an atomic add of the block's valid-key
+ *                 count on *counter (int32, zeroed by the caller); after the
+ *                 call *counter is the exact candidate count.  Block order in
+ *                 the compact output is unspecified (keys inside a block stay
+ *                 in address order).
+ * ------------------------------------------------------------------------ */
+int dsa_progressive_scores(const void* queries, const float* weights, const void* keys,
+                           const int32_t* selected_heads, const int32_t* remaining_heads,
+                           const uint8_t* direct_blocks, const float* threshold,
+                           float* out_scores, int32_t* out_indices, int8_t* accepted,
+                           float* block_max, int32_t* counter, int64_t length,
+                           int32_t block_size, int32_t compact, int32_t key_dtype, void* stream);
+
+/* accepted[b] = direct[b] || block_max[b] >= *threshold  (bytes 0/1).
+ * Replaces the torch logical_or at progressive_kernel.py:493. */
+int dsa_promote_blocks(const uint8_t* direct_blocks, const float* block_max,
+                       const float* threshold, uint8_t* accepted, int64_t blocks, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Exact top-k per row with the reference's stable_topk semantics
+ * (metrics.py:9-22): the k largest values, ties at the cut-off resolved
+ * towards the lower index; -0.0 equals +0.0.  NaN is not supported.
+ *
+ *   scores      [rows, row_stride] fp32, the first `length` entries of a row
+ *               are candidates
+ *   row_lengths [rows] int32 or NULL: per-row number of valid leading
+ *               entries (<= length); rows with fewer than k valid entries
+ *               return all of them and pad with index -1 / value -inf
+ *   in_indices  [rows, row_stride] int64 or NULL: candidate i of a row stands
+ *               for key in_indices[i]; ties then break on that key id.  A row
+ *               of in_indices must be strictly increasing.
+ *   sorted != 0: output ordered by (value desc, index asc) like stable_topk;
+ *   sorted == 0: output ordered by ascending index.
+ *   out_indices [rows, k] int64, out_values [rows, k] fp32 (either may be NULL)
+ *   k <= 4096 and length <= 32768 per call; longer rows go through
+ *   dsa_topk_long.
+ * ------------------------------------------------------------------------ */
+int dsa_topk(const float* scores, const int64_t* in_indices, int64_t rows, int64_t length,
+             int64_t row_stride, const int32_t* row_lengths, int64_t k, int32_t sorted,
+             int64_t* out_indices, float* out_values, void* stream);
+
+/* Top-k of rows longer than one workgroup's register tile: rows are cut into
+ * chunks whose local top-k candidates are merged exactly.  `workspace` must
+ * hold dsa_topk_long_workspace_bytes(rows, length, k) bytes. */
+int64_t dsa_topk_long_workspace_bytes(int64_t rows, int64_t length, int64_t k);
+int dsa_topk_long(const float* scores, int64_t rows, int64_t length, int64_t k, int32_t sorted,
+                  int64_t* out_indices, float* out_values, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Per-block maxima of score rows (replay.py:149-150 _block_max,
+ * approx.py:53-55): out[r, b] = max(scores[r, b*bs : min(len, (b+1)*bs)]).
+ * block_size is any positive value.
+ * ------------------------------------------------------------------------ */
+int dsa_block_max(const float* scores, int64_t rows, int64_t length, int64_t row_stride,
+                  int32_t block_size, float* out, void* stream);
+
+/* Per-block maximum key L2 norm (certified.py:51-62 block_key_norms) for keys
+ * [tokens, heads, dim] (heads = 1 for the shared-key layout):
+ * out[b, h] = max over tokens of the block of ||keys[t, h, :]||, fp32. */
+int dsa_block_key_norms(const void* keys, int64_t tokens, int64_t heads, int64_t dim,
+                        int32_t block_size, int32_t key_dtype, float* out, void* stream);
+
+/* Certified temporal radius (certified.py:18-48 temporal_score_radius):
+ * out[b] = sum_h block_key_norm[b, h] * (|w_now-w_prev|_h ||q_prev,h|| +
+ * |w_now|_h ||q_now,h - q_prev,h||).  q: [heads, dim] fp32, w: [heads] fp32. */
+int dsa_temporal_score_radius(const float* q_now, const float* q_prev, const float* w_now,
+                              const float* w_prev, const float* block_key_norm, int64_t blocks,
+                              int64_t heads, int64_t dim, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_AMD_H */

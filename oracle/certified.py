@@ -1,0 +1,42 @@
+"""CPU restatement of the certified temporal bound (test oracle).
+
+Reference: certified.py:18-62.  Per key block b and head h, with n_bh the
+largest key norm in the block, ReLU's 1-Lipschitz property and Cauchy-Schwarz
+give |w_t ReLU(q_t.k) - w_p ReLU(q_p.k)| <= (|w_t - w_p| ||q_p|| + |w_t|
+||q_t - q_p||) ||k||, summed over heads.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def temporal_score_radius(q_now, q_prev, w_now, w_prev, block_key_norm) -> np.ndarray:
+    """Reference: certified.py:18-48."""
+
+    q_now = np.asarray(q_now, dtype=np.float64)
+    q_prev = np.asarray(q_prev, dtype=np.float64)
+    w_now = np.asarray(w_now, dtype=np.float64)
+    w_prev = np.asarray(w_prev, dtype=np.float64)
+    norms = np.asarray(block_key_norm, dtype=np.float64)
+    if q_now.shape != q_prev.shape or q_now.ndim != 2:
+        raise ValueError("query tensors must have shape [heads,dim]")
+    if w_now.shape != w_prev.shape or w_now.shape != (q_now.shape[0],):
+        raise ValueError("weight tensors must have shape [heads]")
+    if norms.ndim != 2 or norms.shape[1] != q_now.shape[0]:
+        raise ValueError("block_key_norm must have shape [blocks,heads]")
+    per_head = np.abs(w_now - w_prev) * np.sqrt((q_prev ** 2).sum(axis=1)) + np.abs(w_now) * np.sqrt(((q_now - q_prev) ** 2).sum(axis=1))
+    return norms @ per_head
+
+
+def block_key_norms(keys, block_size: int) -> np.ndarray:
+    """Largest key L2 norm per block and head, keys [tokens, heads, dim].  Reference: certified.py:51-62."""
+
+    keys = np.asarray(keys, dtype=np.float64)
+    if keys.ndim != 3:
+        raise ValueError("keys must have shape [tokens,heads,dim]")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    norms = np.sqrt((keys ** 2).sum(axis=2))  # [tokens, heads]
+    blocks = (keys.shape[0] + block_size - 1) // block_size
+    return np.stack([norms[b * block_size : (b + 1) * block_size].max(axis=0) for b in range(blocks)])

@@ -1,0 +1,156 @@
+"""GPU parity of the scoring kernels against the CPU oracle.
+
+Tolerances: bf16/fp16 inputs are exact in fp32 products, so the kernels agree
+with the float64 oracle (on the same rounded inputs) to fp32 summation error;
+we bound |gpu - oracle| <= 1e-5 * S + 1e-6 where S = sum_h |w_h| ReLU(q_h.k)
+is the magnitude of the signed sum (a relative bound on the score itself is
+ill-posed near zero).  The fp32 path uses the same bound.
+The reference's own GPU test (bf16 x0.1 inputs, rtol = atol = 3e-3 against
+torch_full_scores) is ported as is.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_amd import progressive_kernel as P
+from dsa_amd import sidecar, verifier_scoring
+from oracle import scores as S
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(length, dtype, seed=1582, scale_q=1 / math.sqrt(128), batch=None):
+    gen = torch.Generator().manual_seed(seed)
+    shape_q = (64, 128) if batch is None else (batch, 64, 128)
+    shape_w = (64,) if batch is None else (batch, 64)
+    shape_k = (length, 128) if batch is None else (batch, length, 128)
+    q = (torch.randn(shape_q, generator=gen) * scale_q).to(dtype)
+    w = torch.randn(shape_w, generator=gen) / 8.0
+    k = torch.randn(shape_k, generator=gen).to(dtype)
+    return q, w, k
+
+
+def assert_scores_close(actual: torch.Tensor, q, w, k, rel=1e-5, abs_=1e-6):
+    ref = S.relu_index_score(q.float().numpy(), k.float().numpy(), w.float().numpy())
+    scale = S.abs_weight_scale(q.float().numpy(), k.float().numpy(), w.float().numpy())
+    got = actual.detach().cpu().double().numpy()
+    err = np.abs(got - ref)
+    bound = rel * scale + abs_
+    worst = int(np.argmax(err - bound))
+    assert np.all(err <= bound), f"key {worst}: got {got[worst]} want {ref[worst]} (scale {scale[worst]})"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("length", [1, 17, 64, 257, 4099])
+def test_full_scores_match_oracle(device, dtype, length) -> None:
+    print(f"full_scores dtype={dtype} L={length}", flush=True)
+    q, w, k = make_inputs(length, dtype)
+    out = P.full_scores_hip(q.to(device), w.to(device), k.to(device))
+    assert out.shape == (length,) and out.dtype == torch.float32
+    assert_scores_close(out, q, w, k)
+
+
+def test_reference_gpu_tolerance_case(device) -> None:
+    # reference tests/test_progressive_kernel.py:131-144
+    torch.manual_seed(1582)
+    gen = torch.Generator().manual_seed(1582)
+    q = (torch.randn(64, 128, generator=gen) * 0.1).to(torch.bfloat16)
+    w = torch.randn(64, generator=gen)
+    k = (torch.randn(257, 128, generator=gen) * 0.1).to(torch.bfloat16)
+    actual = P.full_scores_triton(q.to(device), w.to(device), k.to(device))
+    torch.testing.assert_close(actual.cpu(), S.torch_full_scores(q, w, k), rtol=3e-3, atol=3e-3)
+
+
+def test_fp32_path_config1(device) -> None:
+    # fp32, L=4096, q ~ N(0,1)/sqrt(128), k ~ N(0,1), w ~ N(0,1/64)
+    print("fp32 config1", flush=True)
+    q, w, k = make_inputs(4096, torch.float32)
+    out = P.full_scores_hip(q.to(device), w.to(device), k.to(device))
+    assert_scores_close(out, q, w, k, rel=1e-5, abs_=1e-6)
+
+
+def test_batched_decode_each_sequence(device) -> None:
+    print("batched decode B=3 L=1000", flush=True)
+    q, w, k = make_inputs(1000, torch.bfloat16, batch=3)
+    out = sidecar.score_encoded(q[:, None].to(device), w[:, None].to(device), k.to(device))
+    assert out.shape == (3, 1, 1000)
+    for b in range(3):
+        assert_scores_close(out[b, 0], q[b], w[b], k[b])
+
+
+def test_score_encoded_multi_query_causal(device) -> None:
+    print("score_encoded multi-query causal", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    q = (torch.randn(2, 37, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(2, 37, 64, generator=gen) / 8
+    k = torch.randn(2, 150, 128, generator=gen).to(torch.bfloat16)
+    dense = sidecar.score_encoded(q.to(device), w.to(device), k.to(device)).cpu()
+    causal = sidecar.score_encoded(q.to(device), w.to(device), k.to(device), causal=True).cpu()
+    offset = 150 - 37
+    for b in range(2):
+        for t in (0, 1, 20, 36):
+            assert_scores_close(dense[b, t], q[b, t], w[b, t], k[b])
+            valid = t + offset + 1
+            assert torch.equal(causal[b, t, :valid], dense[b, t, :valid])
+            assert torch.isneginf(causal[b, t, valid:]).all()
+
+
+def test_fp8_keys_with_block_scales(device) -> None:
+    print("fp8 keys", flush=True)
+    gen = torch.Generator().manual_seed(9)
+    length = 300
+    q = (torch.randn(2, 1, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(2, 1, 64, generator=gen) / 8
+    raw = torch.randn(2, length, 128, generator=gen)
+    blocks = (length + 127) // 128
+    scales = torch.empty(2, blocks)
+    keys8 = torch.empty(2, length, 128, dtype=torch.float8_e4m3fn)
+    for b in range(2):
+        for j in range(blocks):
+            seg = raw[b, j * 128 : (j + 1) * 128]
+            scales[b, j] = seg.abs().max() / 448.0
+            keys8[b, j * 128 : (j + 1) * 128] = (seg / scales[b, j]).to(torch.float8_e4m3fn)
+    out = sidecar.score_encoded(q.to(device), w.to(device), keys8.to(device), key_scales=scales.to(device)).cpu()
+    deq = S.dequantize_fp8_blocks(keys8, scales)
+    for b in range(2):
+        ref = S.relu_index_score(q[b, 0].float().numpy(), deq[b], w[b, 0].numpy())
+        scale = S.abs_weight_scale(q[b, 0].float().numpy(), deq[b], w[b, 0].numpy())
+        assert np.all(np.abs(out[b, 0].double().numpy() - ref) <= 1e-5 * scale + 1e-6)
+
+
+def test_score_head_sparse_fixed_and_dynamic(device) -> None:
+    print("score_head_sparse", flush=True)
+    gen = torch.Generator().manual_seed(11)
+    q = (torch.randn(5, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(5, 64, generator=gen) / 8
+    k = torch.randn(333, 128, generator=gen).to(torch.bfloat16)
+    for ids in ([3, 60, 7, 0, 1, 2, 9, 33], list(range(20)), list(range(64))):
+        out = verifier_scoring.score_head_sparse(q.to(device), w.to(device), k.to(device), ids).cpu()
+        for t in range(5):
+            assert_scores_close(out[t], q[t, ids], w[t, ids], k)
+    dyn = verifier_scoring.dynamic_head_indices(w.to(device), 8, "high_weight")
+    assert torch.equal(dyn.cpu(), S.dynamic_head_indices(w, 8, "high_weight"))
+    out = verifier_scoring.score_head_sparse(q.to(device), w.to(device), k.to(device), dyn).cpu()
+    for t in range(5):
+        ids = dyn[t].cpu().tolist()
+        assert_scores_close(out[t], q[t, ids], w[t, ids], k)
+
+
+def test_head_routing_matches_stable_argsort(device) -> None:
+    gen = torch.Generator().manual_seed(12)
+    w = torch.randn(7, 64, generator=gen)
+    w[:, 5] = w[:, 6]
+    w[0] = 0.0  # all ties
+    w[1, 10] = -w[1, 11]
+    for strategy in ("high_weight", "positive_weight"):
+        got = verifier_scoring.dynamic_head_indices(w.to(device), 16, strategy).cpu()
+        assert torch.equal(got, S.dynamic_head_indices(w, 16, strategy)), strategy
+    weights = torch.zeros(64)
+    weights[20] = -4
+    weights[3] = 4
+    assert P.dynamic_head_ids(weights.to(device)).cpu().tolist() == [3, 20, 0, 1, 2, 4, 5, 6]

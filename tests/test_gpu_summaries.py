@@ -1,0 +1,50 @@
+"""GPU block summaries against the oracle: per-block score maxima (exact),
+per-block key norms and the certified radius (fp32 vs float64)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_amd import _lib, certified
+from oracle import certified as C
+from oracle import replay as R
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("block_size", [16, 32, 64, 128, 7])
+def test_block_max_exact(device, block_size) -> None:
+    rng = np.random.default_rng(block_size)
+    host = rng.normal(size=(3, 1001)).astype(np.float32)
+    x = torch.from_numpy(host).to(device)
+    blocks = -(-1001 // block_size)
+    out = torch.empty(3, blocks, device=device)
+    _lib.call("dsa_block_max", x.data_ptr(), 3, 1001, 1001, block_size, out.data_ptr(), _lib.stream_of(x))
+    for r in range(3):
+        np.testing.assert_array_equal(out[r].cpu().numpy(), R.block_maxima(host[r], block_size).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_block_key_norms(device, dtype) -> None:
+    rng = np.random.default_rng(2)
+    keys = torch.from_numpy(rng.normal(size=(70, 3, 128)).astype(np.float32)).to(dtype)
+    got = certified.block_key_norms(keys.to(device), 16).cpu().double().numpy()
+    want = C.block_key_norms(keys.float().numpy(), 16)
+    np.testing.assert_allclose(got, want, rtol=1e-5)
+    shared = certified.block_key_norms(keys[:, 0].to(device), 8).cpu().double().numpy()
+    np.testing.assert_allclose(shared, C.block_key_norms(keys[:, :1].float().numpy(), 8), rtol=1e-5)
+
+
+def test_temporal_radius(device) -> None:
+    rng = np.random.default_rng(1582)
+    q_prev = rng.normal(size=(64, 128))
+    q_now = q_prev + 0.05 * rng.normal(size=(64, 128))
+    w_prev = rng.normal(size=64)
+    w_now = w_prev + 0.05 * rng.normal(size=64)
+    norms = np.abs(rng.normal(size=(300, 64)))
+    want = C.temporal_score_radius(q_now, q_prev, w_now, w_prev, norms)
+    t = lambda a: torch.from_numpy(a.astype(np.float32)).to(device)  # noqa: E731
+    got = certified.temporal_score_radius(t(q_now), t(q_prev), t(w_now), t(w_prev), t(norms)).cpu().double().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5)

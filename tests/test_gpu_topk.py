@@ -1,0 +1,81 @@
+"""GPU top-K is bit-exact against the stable_topk oracle (index sets and
+order), including ties at the cut-off, signed zeros, -inf, short rows and
+the chunked long-row path."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_amd import metrics
+from oracle import topk as T
+
+pytestmark = pytest.mark.gpu
+
+
+def rows_for(kind: str, rows: int, length: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        return rng.normal(size=(rows, length)).astype(np.float32)
+    if kind == "ties":
+        return rng.integers(-3, 4, size=(rows, length)).astype(np.float32)
+    if kind == "zeros":
+        x = rng.choice(np.array([-0.0, 0.0, 1.0, -1.0], dtype=np.float32), size=(rows, length))
+        return x.astype(np.float32)
+    if kind == "neginf":
+        x = rng.normal(size=(rows, length)).astype(np.float32)
+        x[rng.random(size=x.shape) < 0.7] = -np.inf
+        return x
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties", "zeros", "neginf"])
+@pytest.mark.parametrize("length,k", [(1, 1), (7, 3), (100, 100), (300, 17), (4096, 256), (5000, 4096), (32768, 2048)])
+def test_topk_matches_oracle(device, kind, length, k) -> None:
+    print(f"topk kind={kind} L={length} k={k}", flush=True)
+    host = rows_for(kind, 3, length, seed=length + k)
+    x = torch.from_numpy(host).to(device)
+    idx_sorted, val_sorted = metrics.topk(x, k, sorted=True, return_values=True)
+    idx_index = metrics.topk(x, k, sorted=False)
+    for r in range(3):
+        want = T.stable_topk(host[r], k)
+        assert idx_sorted[r].cpu().numpy().tolist() == want.tolist()
+        np.testing.assert_array_equal(val_sorted[r].cpu().numpy(), host[r][want])
+        assert idx_index[r].cpu().numpy().tolist() == np.sort(want).tolist()
+
+
+def test_row_lengths_pad_short_rows(device) -> None:
+    host = rows_for("ties", 4, 600, seed=3)
+    lengths = torch.tensor([600, 10, 0, 257], dtype=torch.int32)
+    k = 64
+    x = torch.from_numpy(host).to(device)
+    idx, val = metrics.topk(x, k, sorted=True, row_lengths=lengths.to(device), return_values=True)
+    idx2 = metrics.topk(x, k, sorted=False, row_lengths=lengths.to(device))
+    for r in range(4):
+        n = int(lengths[r])
+        assert idx[r].cpu().tolist() == T.topk_sorted_padded(host[r], k, n).tolist()
+        assert idx2[r].cpu().tolist() == T.topk_index_order(host[r], k, n).tolist()
+        pad = min(n, k)
+        assert torch.isneginf(val[r, pad:]).all()
+
+
+@pytest.mark.parametrize("length", [40000, 131072])
+def test_long_rows_use_chunked_merge(device, length) -> None:
+    print(f"topk long L={length}", flush=True)
+    host = rows_for("ties", 2, length, seed=length)
+    host[1] = np.random.default_rng(1).normal(size=length).astype(np.float32)
+    x = torch.from_numpy(host).to(device)
+    idx = metrics.topk(x, 2048, sorted=True)
+    idx_set = metrics.topk(x, 2048, sorted=False)
+    for r in range(2):
+        want = T.stable_topk(host[r], 2048)
+        assert idx[r].cpu().numpy().tolist() == want.tolist()
+        assert idx_set[r].cpu().numpy().tolist() == np.sort(want).tolist()
+
+
+def test_stable_topk_reference_cases(device) -> None:
+    assert metrics.stable_topk(np.array([1.0, 3.0, 3.0, 2.0]), 2).tolist() == [1, 2]
+    assert np.array_equal(metrics.stable_topk(np.ones(64, dtype=np.float32), 8), np.arange(8))
+    gpu = metrics.stable_topk(torch.tensor([0.5, 2.0, 2.0], device=device), 2)
+    assert gpu.is_cuda and gpu.cpu().tolist() == [1, 2]

@@ -1,0 +1,80 @@
+"""Host-side logic of the dsa_amd API (no device needed): head-id validation,
+QK accounting, and the input contract errors of the GPU entry points."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_amd import metrics, progressive_kernel as P, sidecar, verifier_scoring
+
+
+def test_split_head_ids_returns_complement() -> None:
+    selected, remaining = P.split_head_ids(torch.tensor([0, 2, 4, 6, 8, 10, 12, 63]))
+    assert selected.numel() == 8 and remaining.numel() == 56
+    assert set(selected.tolist()).isdisjoint(remaining.tolist())
+    assert sorted(selected.tolist() + remaining.tolist()) == list(range(64))
+
+
+@pytest.mark.parametrize("values", [[0, 1], [0, 1, 2, 3, 4, 5, 6, 64], [0, 1, 2, 3, 4, 5, 6, 6]])
+def test_split_head_ids_rejects_invalid(values) -> None:
+    with pytest.raises(ValueError):
+        P.split_head_ids(torch.tensor(values))
+
+
+def test_dynamic_head_ids_host_weights_is_stable_for_ties() -> None:
+    weights = torch.zeros(64)
+    weights[20] = -4
+    weights[3] = 4
+    result = P.dynamic_head_ids(weights)
+    assert result[:2].tolist() == [3, 20] and result[2:].tolist() == [0, 1, 2, 4, 5, 6]
+
+
+def test_progressive_qk_reduction() -> None:
+    assert P.progressive_qk_reduction(8192, 0, 0) == pytest.approx(0.875)
+    assert P.progressive_qk_reduction(8192, 128, 0) == pytest.approx(0.0)
+    work = 2048 * 64 + 6144 * 8 + 1024 * 56
+    assert P.progressive_qk_reduction(8192, 32, 16) == pytest.approx(1 - work / (8192 * 64))
+    with pytest.raises(ValueError):
+        P.progressive_qk_reduction(8192, 129, 0)
+    with pytest.raises(ValueError):
+        P.progressive_qk_reduction(8192, -1, 0)
+
+
+def test_gpu_entry_points_reject_host_tensors() -> None:
+    q = torch.zeros(64, 128, dtype=torch.bfloat16)
+    w = torch.zeros(64)
+    k = torch.zeros(65, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        P.full_scores_hip(q, w, k)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        P.progressive_scores_triton(q, w, k, torch.arange(8), torch.zeros(2, dtype=torch.bool), 0.0)
+    with pytest.raises(ValueError):
+        sidecar.score_encoded(q[None, None], w[None, None], k[None])
+    with pytest.raises(ValueError):
+        metrics.topk(torch.zeros(10), 3)
+    with pytest.raises(ValueError):
+        verifier_scoring.score_head_sparse(q[None], w[None], k, [0])
+
+
+def test_stable_topk_validates_like_the_reference() -> None:
+    with pytest.raises(ValueError, match="expected a vector"):
+        metrics.stable_topk(np.ones((2, 2)), 1)
+    with pytest.raises(ValueError, match="invalid"):
+        metrics.stable_topk(np.ones(3), 4)
+
+
+def test_recall_helpers() -> None:
+    assert metrics.topk_recall(np.array([1, 2]), np.array([2, 3])) == 0.5
+    assert metrics.normalized_recall_lift(0.5, 2, 4) == 0.0
+    assert metrics.topk_recall(torch.tensor([5]), torch.tensor([5])) == 1.0
+
+
+def test_reference_names_are_aliases() -> None:
+    assert P.full_scores_triton is P.full_scores_hip
+    assert P.progressive_scores_triton is P.progressive_scores_hip
+    assert P.two_pass_scores_triton is P.two_pass_scores_hip
+    assert math.ceil(65 / 64) == 2
