@@ -40,6 +40,9 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i32, _p,
     ],
     "dsa_route_heads": [_p, _i64, _i64, _i64, _i32, _p, _p, _p],
+    "dsa_score_topk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
+    "dsa_score_hist": [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _p],
+    "dsa_select_topk": [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
     "dsa_h8_block_max": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
     "dsa_masked_full_scores": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
     "dsa_progressive_scores": [
@@ -54,6 +57,7 @@ _SIGNATURES: dict[str, list] = {
 }
 _RESTYPES: dict[str, object] = {
     "dsa_topk_long_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "dsa_score_topk_workspace_bytes": (_i64, [_i64, _i64]),
 }
 
 _lock = threading.Lock()

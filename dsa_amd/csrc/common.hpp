@@ -24,6 +24,7 @@ constexpr int kHeads = 64;
 constexpr int kHeadDim = 128;
 constexpr int kVerifierHeads = 8;
 constexpr int kWave = 64;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -83,6 +84,41 @@ __device__ __forceinline__ uint32_t float_to_ordered(float f) {
 __device__ __forceinline__ float ordered_to_float(uint32_t o) {
   uint32_t u = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
   return __uint_as_float(u);
+}
+
+// ---------------------------------------------------------------------------
+// Raw buffer resources (gfx9-family descriptor word 3 = 0x00020000).  Buffer
+// loads past num_records return zeros and buffer stores past it are dropped by
+// the hardware, so tails need neither clamped addresses nor branches.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t BufferRsrc;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ BufferRsrc make_buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load_16(BufferRsrc rsrc, uint32_t offset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)offset, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void buffer_store_f32(BufferRsrc rsrc, uint32_t offset, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rsrc, (int)offset, 0, 0);
+}
+__device__ __forceinline__ void buffer_store_16(BufferRsrc rsrc, uint32_t offset, uint4 v) {
+  const u32x4 parts = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(parts, rsrc, (int)offset, 0, 0);
+}
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void buffer_store_u64(BufferRsrc rsrc, uint32_t offset, uint64_t v) {
+  const u32x2 parts = {(uint32_t)v, (uint32_t)(v >> 32)};
+  __builtin_amdgcn_raw_buffer_store_b64(parts, rsrc, (int)offset, 0, 0);
+}
+
+// ReLU as a signed-integer max on the float's bits: negative values (sign bit
+// set) become +0.0, non-negative values pass unchanged.  One VALU op, where
+// fmaxf(x, 0) costs two (NaN quieting).
+__device__ __forceinline__ float relu(float x) {
+  return __int_as_float(max(__float_as_int(x), 0));
 }
 
 // ---------------------------------------------------------------------------

@@ -6,6 +6,7 @@
 // ReLU, the signed head weight and the 64-head reduction are applied to the
 // accumulators in registers, so only the fp32 score leaves the kernel.
 #include "common.hpp"
+#include "select.hpp"
 #include "status.hpp"
 
 namespace dsa {
@@ -25,6 +26,12 @@ struct KeysB16 {  // bf16 or fp16 rows, 256 B
 #pragma unroll
     for (int c = 0; c < kRaw; ++c) raw[c] = p[c];
   }
+  __device__ static __forceinline__ void load_buf(BufferRsrc rsrc, int key, int g,
+                                                  uint4 (&raw)[kRaw]) {
+    const uint32_t off = (uint32_t)key * kRowBytes + g * 64;
+#pragma unroll
+    for (int c = 0; c < kRaw; ++c) raw[c] = buffer_load_16(rsrc, off + 16 * c);
+  }
   __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) { return raw[j]; }
 };
 
@@ -37,6 +44,12 @@ struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
     const uint4* p = reinterpret_cast<const uint4*>(base + (size_t)key * kRowBytes + g * 32);
     raw[0] = p[0];
     raw[1] = p[1];
+  }
+  __device__ static __forceinline__ void load_buf(BufferRsrc rsrc, int key, int g,
+                                                  uint4 (&raw)[kRaw]) {
+    const uint32_t off = (uint32_t)key * kRowBytes + g * 32;
+    raw[0] = buffer_load_16(rsrc, off);
+    raw[1] = buffer_load_16(rsrc, off + 16);
   }
   __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) {
     const uint4 v = raw[j >> 1];
@@ -61,8 +74,22 @@ __device__ __forceinline__ float tile_contrib(const uint4 (&qa)[M][4], const flo
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v = fmaf(wr[m][i], fmaxf(acc[m][i], 0.f), v);
+    for (int i = 0; i < 4; ++i) v = fmaf(wr[m][i], relu(acc[m][i]), v);
   return v;
+}
+
+// A fragments of heads 16m .. 16m+15 for m < M (no gather, no padding).
+template <int M>
+__device__ __forceinline__ void load_dense_head_tiles(const uint16_t* q, const float* w, int r, int g,
+                                                      uint4 (&qa)[M][4], float (&wr)[M][4]) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const uint4* row = reinterpret_cast<const uint4*>(q + (16 * m + r) * kHeadDim + 32 * g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qa[m][j] = row[j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[m][i] = w[16 * m + 4 * g + i];
+  }
 }
 
 // Loads the A fragments of M head tiles.  Row slot s of the stacked tiles is
@@ -122,20 +149,24 @@ struct DenseArgs {
   int32_t causal_offset;  // < 0: no mask; else key j is valid for query t iff j <= t + offset
   int32_t units_per_wg;
   int32_t wgs_per_seq;
+  int64_t total_wgs;  // the launch pads the grid to a multiple of kXcds
+  uint32_t* hist;  // [sequences][kSelectBins] score histogram (kHist only)
 };
 
+// Keys past the valid range read as zeros (buffer bounds check).
 template <class KF>
-__device__ __forceinline__ void dense_load_unit(const uint8_t* keys, int u, int last, int r, int g,
+__device__ __forceinline__ void dense_load_unit(BufferRsrc keys, int u, int r, int g,
                                                 uint4 (&buf)[4][KF::kRaw]) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) KF::load(keys, min(u * 64 + 16 * t + r, last), g, buf[t]);
+  for (int t = 0; t < 4; ++t) KF::load_buf(keys, u * 64 + 16 * t + r, g, buf[t]);
 }
 
-template <class Tag, class KF, int M>
+template <class Tag, class KF, int M, bool kHist>
 __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], const float (&wr)[M][4],
                                                    const uint4 (&buf)[4][KF::kRaw], int u,
                                                    int valid, int L, int lane, int g,
-                                                   const float* scales, float* out) {
+                                                   const float* scales, BufferRsrc out,
+                                                   uint32_t* hist) {
   float s[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, M, KF>(qa, wr, buf[t]);
@@ -152,64 +183,106 @@ __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], cons
   const float send = high ? keep_a : keep_b;
   keep += __shfl_xor(send, 32, kWave);
   const int key = u * 64 + lane;
-  if (key < L) {
-    if constexpr (KF::kScaled) keep *= scales[key >> 7];
-    out[key] = key < valid ? keep : -__builtin_inff();
+  if constexpr (KF::kScaled) keep *= scales[min(key, L - 1) >> 7];
+  // Stores past L are dropped by the buffer bounds check.
+  buffer_store_f32(out, (uint32_t)key * 4, key < valid ? keep : -__builtin_inff());
+  if constexpr (kHist)
+    __hip_atomic_fetch_add(&hist[float_to_ordered(keep) >> 20], key < valid ? 1u : 0u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The streaming part of dense_scores_kernel: query block into registers, then
+// the two-buffer unit loop.
+template <class Tag, class KF, int M, bool kGather, bool kHist>
+__device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int u_first, int64_t seq,
+                                             int valid, int L, int lane, int r, int g,
+                                             BufferRsrc keys, BufferRsrc out, const float* scales,
+                                             uint32_t* hist) {
+  uint4 qa[M][4];
+  float wr[M][4];
+  if constexpr (kGather) {
+    const int32_t* ids = a.head_ids ? a.head_ids + seq * a.ids_stride : nullptr;
+    load_head_tiles<M>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, ids, a.head_count, r, g, qa,
+                       wr);
+  } else {
+    load_dense_head_tiles<M>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa, wr);
+  }
+
+  // Two register buffers.  The next unit's loads are always issued before the
+  // current unit is computed; past the wave's last unit the prefetch re-reads
+  // that last unit (an L2 hit), so no load is conditional and the compiler's
+  // vmcnt waits cover exactly the buffer being consumed.
+  const int u_last = u_first + 4 * (count - 1);
+  uint4 buf0[4][KF::kRaw];
+  uint4 buf1[4][KF::kRaw];
+  dense_load_unit<KF>(keys, u_first, r, g, buf0);
+  for (int i = 0; i < count; i += 2) {
+    const int u = u_first + 4 * i;
+    dense_load_unit<KF>(keys, min(u + 4, u_last), r, g, buf1);
+    dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf0, u, valid, L, lane, g, scales, out, hist);
+    if (i + 1 >= count) break;
+    dense_load_unit<KF>(keys, min(u + 8, u_last), r, g, buf0);
+    dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf1, u + 4, valid, L, lane, g, scales, out, hist);
   }
 }
 
-template <class Tag, class KF, int M>
+template <class Tag, class KF, int M, bool kGather, bool kHist>
 __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
+  // kHist: also count every valid score into the sequence's histogram of the
+  // top 12 bits of its order-preserving key (input of the distributed top-k).
+  __shared__ uint32_t hist[kHist ? kSelectBins : 1];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform control flow: every loop bound below lives in SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int64_t seq = blockIdx.x / a.wgs_per_seq;
-  const int chunk = blockIdx.x % a.wgs_per_seq;
+  // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so
+  // that consecutive logical workgroups (one sequence's chunks) share an XCD
+  // and its L2 fetches that sequence's query block once.
+  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
+  if (logical >= a.total_wgs) return;
+  const int64_t seq = logical / a.wgs_per_seq;
+  const int chunk = (int)(logical % a.wgs_per_seq);
   const int L = a.length;
   const int64_t keyset = seq / a.queries_per_keyset;
   int valid = L;
   if (a.causal_offset >= 0)
     valid = min(L, (int)(seq % a.queries_per_keyset) + a.causal_offset + 1);
 
-  const uint8_t* keys = a.keys + keyset * a.key_stride * KF::kRowBytes;
-  float* out = a.out + seq * a.out_stride;
+  const BufferRsrc keys =
+      make_buffer(a.keys + keyset * a.key_stride * KF::kRowBytes, (uint32_t)valid * KF::kRowBytes);
+  float* out_ptr = a.out + seq * a.out_stride;
+  const BufferRsrc out = make_buffer(out_ptr, (uint32_t)L * 4u);
   const float* scales = KF::kScaled ? a.scales + keyset * a.scale_stride : nullptr;
 
+  // This wave owns units u_first, u_first + 4, ... below u_end; those at or
+  // past u_compute_end lie wholly beyond the causal limit and only get -inf.
   const int n_units = (L + 63) >> 6;
   const int u_end = min(n_units, (chunk + 1) * a.units_per_wg);
-  int u = chunk * a.units_per_wg + wave;
-  if (u >= u_end) return;
-  // Units wholly past the causal limit only need -inf.
+  const int u_first = chunk * a.units_per_wg + wave;
   const int u_compute_end = min(u_end, (valid + 63) >> 6);
-  for (int uu = u; uu < u_end; uu += 4) {
-    const int key = uu * 64 + lane;
-    if (uu >= u_compute_end && key < L) out[key] = -__builtin_inff();
+  const int count = u_compute_end > u_first ? (u_compute_end - u_first + 3) >> 2 : 0;
+  for (int uu = u_first + 4 * count; uu < u_end; uu += 4)
+    buffer_store_f32(out, (uint32_t)(uu * 64 + lane) * 4, -__builtin_inff());
+  if constexpr (kHist) {
+    for (int i = threadIdx.x; i < kSelectBins; i += 256) hist[i] = 0;
+    __syncthreads();
+    if (count > 0)
+      dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, seq, valid, L, lane, r, g, keys, out,
+                                               scales, hist);
+    __syncthreads();
+    uint32_t* ghist = a.hist + seq * kSelectBins;
+    for (int i = threadIdx.x; i < kSelectBins; i += 256) {
+      const uint32_t n = hist[i];
+      if (n) __hip_atomic_fetch_add(&ghist[i], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
   }
-  if (u >= u_compute_end) return;
-
-  uint4 qa[M][4];
-  float wr[M][4];
-  const int32_t* ids = a.head_ids ? a.head_ids + seq * a.ids_stride : nullptr;
-  load_head_tiles<M>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, ids, a.head_count, r, g, qa,
-                     wr);
-
-  const int last = max(valid, 1) - 1;
-  uint4 buf0[4][KF::kRaw];
-  uint4 buf1[4][KF::kRaw];
-  dense_load_unit<KF>(keys, u, last, r, g, buf0);
-  while (true) {
-    const int u1 = u + 4;
-    if (u1 < u_compute_end) dense_load_unit<KF>(keys, u1, last, r, g, buf1);
-    dense_compute_unit<Tag, KF, M>(qa, wr, buf0, u, valid, L, lane, g, scales, out);
-    if (u1 >= u_compute_end) break;
-    const int u2 = u1 + 4;
-    if (u2 < u_compute_end) dense_load_unit<KF>(keys, u2, last, r, g, buf0);
-    dense_compute_unit<Tag, KF, M>(qa, wr, buf1, u1, valid, L, lane, g, scales, out);
-    if (u2 >= u_compute_end) break;
-    u = u2;
-  }
+  if (count == 0) return;
+  dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, seq, valid, L, lane, r, g, keys, out,
+                                           scales, hist);
 }
+
 
 // ---------------------------------------------------------------------------
 // fp32 keys and queries (accuracy path): v_mfma_f32_16x16x4_f32, queries
@@ -412,35 +485,38 @@ __global__ void promote_blocks_kernel(const uint8_t* direct, const float* block_
 // Host-side launch helpers.
 // ---------------------------------------------------------------------------
 int units_per_workgroup(int64_t sequences, int64_t length) {
-  // Aim for about eight workgroups of four waves per CU over all sequences
-  // while keeping at least four units (one per wave) in each workgroup.
+  // About one workgroup of four waves per CU: every wave then streams several
+  // units, so its query-block load and pipeline fill are paid once, while at
+  // least four units (one per wave) stay in each workgroup.
   const int64_t units = (length + 63) / 64;
-  const int64_t target_wgs = 2048;
+  const int64_t target_wgs = 256;
   int64_t per = (units * sequences + target_wgs - 1) / target_wgs;
   per = per < 4 ? 4 : per;
   per = (per + 3) / 4 * 4;
   return (int)per;
 }
 
-template <class Tag, class KF, int M>
+template <class Tag, class KF, int M, bool kGather, bool kHist = false>
 int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
   const int64_t units = (a.length + 63) / 64;
   a.units_per_wg = units_per_workgroup(sequences, a.length);
   a.wgs_per_seq = (int32_t)((units + a.units_per_wg - 1) / a.units_per_wg);
-  const int64_t grid = sequences * a.wgs_per_seq;
+  a.total_wgs = sequences * a.wgs_per_seq;
+  const int64_t grid = (a.total_wgs + kXcds - 1) / kXcds * kXcds;
   if (grid > 0x7fffffffLL) return fail(DSA_STATUS_INVALID_ARGUMENT, "problem too large");
-  hipLaunchKernelGGL((dense_scores_kernel<Tag, KF, M>), dim3((unsigned)grid), dim3(256), 0, stream,
-                     a);
+  hipLaunchKernelGGL((dense_scores_kernel<Tag, KF, M, kGather, kHist>), dim3((unsigned)grid),
+                     dim3(256), 0, stream, a);
   return check_launch("dense_scores_kernel");
 }
 
 template <class Tag, class KF>
 int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
+  if (!a.head_ids && a.head_count == kHeads) return launch_dense_m<Tag, KF, 4, false>(a, sequences, stream);
   switch ((a.head_count + 15) / 16) {
-    case 1: return launch_dense_m<Tag, KF, 1>(a, sequences, stream);
-    case 2: return launch_dense_m<Tag, KF, 2>(a, sequences, stream);
-    case 3: return launch_dense_m<Tag, KF, 3>(a, sequences, stream);
-    default: return launch_dense_m<Tag, KF, 4>(a, sequences, stream);
+    case 1: return launch_dense_m<Tag, KF, 1, true>(a, sequences, stream);
+    case 2: return launch_dense_m<Tag, KF, 2, true>(a, sequences, stream);
+    case 3: return launch_dense_m<Tag, KF, 3, true>(a, sequences, stream);
+    default: return launch_dense_m<Tag, KF, 4, true>(a, sequences, stream);
   }
 }
 
@@ -504,6 +580,8 @@ extern "C" int dsa_score_queries(const void* queries, int64_t q_stride, const fl
                   reinterpret_cast<uintptr_t>(keys) % 16 == 0,
               "queries and keys must be 16-byte aligned");
   DSA_REQUIRE(q_stride % 8 == 0, "q_stride must keep 16-byte alignment");
+  DSA_REQUIRE(length * (key_dtype == kFP8E4M3 ? 128 : 256) < (int64_t(1) << 32),
+              "one key set must stay below 4 GiB");
   DenseArgs a = {};
   a.q = static_cast<const uint16_t*>(queries);
   a.q_stride = q_stride;
@@ -551,6 +629,67 @@ extern "C" int dsa_full_scores(const void* queries, const float* weights, const 
   return dsa_score_queries(queries, kHeads * kHeadDim, weights, kHeads, nullptr, 0, kHeads, keys,
                            length, 1, key_scales, (length + 127) / 128, out, length, batch, length,
                            -1, key_dtype, stream);
+}
+
+extern "C" int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length) {
+  if (batch <= 0 || length <= 0) return 0;
+  return select_workspace_layout(nullptr, batch, length).bytes;
+}
+
+extern "C" int dsa_score_hist(const void* queries, const float* weights, const void* keys,
+                              const float* key_scales, float* scores, int64_t batch,
+                              int64_t length, int32_t key_dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  DSA_REQUIRE(queries && weights && keys && scores, "null pointer argument");
+  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
+  DSA_REQUIRE(length > 0 && length <= int64_t(kSelectChunk) * kMaxSelectChunks,
+              "length %lld outside [1, %d]", (long long)length, kSelectChunk * kMaxSelectChunks);
+  DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16 || key_dtype == kFP8E4M3,
+              "dsa_score_hist takes fp16/bf16/fp8 keys (got %d)", key_dtype);
+  DSA_REQUIRE(key_dtype != kFP8E4M3 || key_scales, "fp8 keys need key_scales");
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(queries) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(keys) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+              "queries, keys (16 B) and workspace (256 B) must be aligned");
+  const int64_t need = dsa_score_topk_workspace_bytes(batch, length);
+  if (!workspace || workspace_bytes < need)
+    return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the decode step needs %lld workspace bytes",
+                (long long)need);
+  const SelectWorkspace ws = select_workspace_layout(workspace, batch, length);
+  DenseArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.q_stride = kHeads * kHeadDim;
+  a.w = weights;
+  a.w_stride = kHeads;
+  a.head_count = kHeads;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.key_stride = length;
+  a.queries_per_keyset = 1;
+  a.scales = key_scales;
+  a.scale_stride = (length + 127) / 128;
+  a.out = scores;
+  a.out_stride = length;
+  a.length = (int32_t)length;
+  a.causal_offset = -1;
+  a.hist = ws.hist;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (key_dtype) {
+    case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true>(a, batch, s);
+    case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true>(a, batch, s);
+    default: return launch_dense_m<Bf16Tag, KeysFP8, 4, false, true>(a, batch, s);
+  }
+}
+
+extern "C" int dsa_score_topk(const void* queries, const float* weights, const void* keys,
+                              const float* key_scales, float* scores, int64_t batch,
+                              int64_t length, int64_t k, int32_t key_dtype, int64_t* out_indices,
+                              float* out_values, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+  if (int st = dsa_score_hist(queries, weights, keys, key_scales, scores, batch, length, key_dtype,
+                              workspace, workspace_bytes, stream))
+    return st;
+  return dsa_select_topk(scores, batch, length, k, out_indices, out_values, workspace,
+                         workspace_bytes, stream);
 }
 
 extern "C" int dsa_h8_block_max(const void* queries, const float* weights, const void* keys,

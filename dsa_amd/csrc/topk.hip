@@ -3,11 +3,10 @@
 //
 // One 1024-thread workgroup per (virtual) row.  Thread t owns the contiguous
 // slice [t * EPT, t * EPT + EPT) of the row in registers, so a single
-// exclusive scan over threads enumerates elements in index order.  Selection is
-// a 3-pass MSD radix select (11 + 11 + 10 bits) over order-preserving uint32
-// keys with a 2048-bin LDS histogram per pass; it yields the exact k-th value
-// v* and the number of elements equal to v* that still have to be taken.  The
-// chosen elements are then written in index order, or bitonic-sorted in LDS by
+// exclusive scan over threads enumerates elements in index order.  The k-th
+// largest (value, index) pair is found by a value-linear bucket select whose
+// crowded-bucket or degenerate cases fall back to an exact radix select; the
+// chosen elements are written in index order, or bitonic-sorted in LDS by
 // (value desc, index asc) when a sorted result is requested.
 #include "common.hpp"
 #include "status.hpp"
@@ -37,9 +36,12 @@ struct TopkArgs {
 struct TopkShared {
   uint32_t hist[kBins];
   uint32_t wave_sums[kTopkWaves];
+  float wave_lo[kTopkWaves];
+  float wave_hi[kTopkWaves];
   uint32_t digit;
   uint32_t krem;
-  uint64_t sort_keys[kMaxK];
+  uint64_t cstar;
+  uint64_t sort_keys[kMaxK + 1];  // slot kMaxK is a write sink for unchosen lanes
 };
 
 // Exclusive prefix sum over the workgroup in thread order; returns the total
@@ -52,7 +54,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const uint32_t y = __shfl_up(x, off, kWave);
-    if (lane >= off) x += y;
+    x += lane >= off ? y : 0u;
   }
   if (lane == 63) wave_sums[wave] = x;
   __syncthreads();
@@ -69,10 +71,83 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   return before + x - v;
 }
 
+// Bitonic sort of keys[0, width) in descending order (width a power of two).
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t* keys, int width) {
+  const int tid = threadIdx.x;
+  for (int size = 2; size <= width; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < (width >> 1); i += kTopkThreads) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const uint64_t x = keys[lo];
+        const uint64_t y = keys[hi];
+        const bool desc = (lo & size) == 0;
+        const bool swap = desc ? (x < y) : (x > y);
+        keys[lo] = swap ? y : x;
+        keys[hi] = swap ? x : y;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ void lds_add(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Rank key of an element: (ordered value, ~position).  Larger is better; all
+// composites of a row are distinct.
+__device__ __forceinline__ uint64_t composite(uint32_t key, int pos) {
+  return (uint64_t(key) << 32) | (uint64_t)(~(uint32_t)pos);
+}
+
+// Value-linear bucket of an ordered key: monotone non-decreasing in the value
+// (the subtraction, the positive scaling and the truncation are all monotone
+// in IEEE arithmetic), so equal values share a bucket and a larger bucket
+// always holds strictly larger values.
+__device__ __forceinline__ int value_bucket(uint32_t key, float lo, float scale) {
+  const float f = ordered_to_float(key);
+  const float x = (f - lo) * scale;  // -inf -> -inf, finite >= 0
+  return (int)fminf(fmaxf(x, 0.f), (float)(kBins - 1));
+}
+
+// Finds the bin holding the want-th largest element of the histogram in
+// sh.hist; leaves it in sh.digit and the remaining rank inside it in sh.krem.
+__device__ __forceinline__ void locate_bin(TopkShared& sh, uint32_t want) {
+  const int tid = threadIdx.x;
+  const uint32_t c0 = sh.hist[2 * tid];
+  const uint32_t c1 = sh.hist[2 * tid + 1];
+  uint32_t total;
+  const uint32_t before = block_exclusive_scan(c0 + c1, sh.wave_sums, total);
+  const uint32_t above1 = total - before - c0 - c1;  // elements in bins > 2t+1
+  const uint32_t above0 = above1 + c1;               // elements in bins > 2t
+  if (c1 && above1 < want && want <= above1 + c1) {
+    sh.digit = 2 * tid + 1;
+    sh.krem = want - above1;
+  }
+  if (c0 && above0 < want && want <= above0 + c0) {
+    sh.digit = 2 * tid;
+    sh.krem = want - above0;
+  }
+  __syncthreads();
+}
+
+// The k largest of a row, ties at the cut-off to the lower position.  Every
+// element is ranked by its composite; the chosen set is exactly the composites
+// >= cstar, the k-th largest composite, which is found by
+//   1. a bucket select: value-linear buckets between the row's finite min and
+//      max; the bucket T holding the k-th largest is read off a histogram, its
+//      (few) candidates are sorted in LDS and cstar is the need-th of them; or
+//   2. when the row has no finite spread or bucket T is too crowded: an
+//      11+11+10-bit radix select over the ordered keys for the k-th value,
+//      whose ties are ranked by position with a prefix scan.
+// All per-element work is branch-free (predicated adds and sink-slot writes).
 template <int EPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
   __shared__ TopkShared sh;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int64_t v = blockIdx.x;
   const int64_t row = v / a.chunks;
   const int chunk = (int)(v % a.chunks);
@@ -84,106 +159,153 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
   const int k = a.k;
   const int64_t out_base = v * (int64_t)k;
 
-  // Load this thread's slice as ordered keys; 0 marks an invalid slot.
+  // Load this thread's slice as ordered keys; 0 marks an invalid slot.  The
+  // buffer bounds check turns reads past n into zeros, which are masked.
   uint32_t key[EPT];
   const int e0 = tid * EPT;
+  {
+    const BufferRsrc rsrc = make_buffer(a.scores + base, (uint32_t)n * 4u);
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int pos = e0 + e;
-    uint32_t kv = 0;
-    if (pos < n) {
-      bool ok = true;
-      if (a.in_idx) ok = a.in_idx[base + pos] >= 0;
-      if (ok) kv = float_to_ordered(a.scores[base + pos]);
+    for (int c = 0; c < EPT / 4; ++c) {
+      const uint4 raw = buffer_load_16(rsrc, (uint32_t)(e0 + 4 * c) * 4u);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        key[4 * c + i] = e0 + 4 * c + i < n ? float_to_ordered(__uint_as_float(w4[i])) : 0u;
     }
-    key[e] = kv;
-  }
-
-  // Chosen: key > threshold, or key == threshold within the first krem ties.
-  // With threshold 1 and unlimited krem every valid slot is chosen (n <= k).
-  uint32_t threshold = 1;
-  uint32_t krem = 0xffffffffu;
-  if (n > k) {
-    uint32_t prefix = 0;
-    uint32_t prefix_mask = 0;
-    uint32_t want = (uint32_t)k;
-#pragma unroll 1
-    for (int pass = 0; pass < 3; ++pass) {
-      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-      for (int i = tid; i < kBins; i += kTopkThreads) sh.hist[i] = 0;
-      if (tid == 0) {
-        sh.digit = 0;
-        sh.krem = 1;
-      }
-      __syncthreads();
+    if (a.in_idx) {
+      const int64_t* ids = a.in_idx + base;
 #pragma unroll
       for (int e = 0; e < EPT; ++e)
-        if (key[e] != 0 && (key[e] & prefix_mask) == prefix)
-          atomicAdd(&sh.hist[(key[e] >> shift) & dmask], 1u);
-      __syncthreads();
-      // Thread t owns bins 2t and 2t+1; find the digit holding the want-th
-      // largest via a suffix count (total minus inclusive prefix).
-      const uint32_t c0 = sh.hist[2 * tid];
-      const uint32_t c1 = sh.hist[2 * tid + 1];
-      uint32_t total;
-      const uint32_t before = block_exclusive_scan(c0 + c1, sh.wave_sums, total);
-      const uint32_t above1 = total - before - c0 - c1;  // count in bins > 2t+1
-      const uint32_t above0 = above1 + c1;               // count in bins > 2t
-      if (c1 && above1 < want && want <= above1 + c1) {
-        sh.digit = 2 * tid + 1;
-        sh.krem = want - above1;
-      }
-      if (c0 && above0 < want && want <= above0 + c0) {
-        sh.digit = 2 * tid;
-        sh.krem = want - above0;
-      }
-      __syncthreads();
-      prefix |= sh.digit << shift;
-      prefix_mask |= dmask << shift;
-      want = sh.krem;
-      __syncthreads();
+        if (e0 + e < n && ids[e0 + e] < 0) key[e] = 0;
     }
-    threshold = prefix;  // exact key of the k-th largest
-    krem = want;         // elements equal to it that are taken (lowest index first)
   }
 
-  // Selection in index order: rank the ties, count the chosen elements per
-  // thread, then walk the slice again placing (key, ~position) of each chosen
-  // element at its rank in LDS.  threshold >= 1, so invalid slots (key 0) are
-  // never chosen.
-  uint32_t n_eq = 0;
+  // cstar = composite of the k-th largest; with at most k valid slots every
+  // valid slot (key >= 1) is chosen.
+  uint64_t cstar = uint64_t(1) << 32;
+  uint32_t n_valid = 0;
+  if (n > k) {
+    uint32_t mine = 0;
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) n_eq += key[e] == threshold ? 1u : 0u;
-  uint32_t eq_total;
-  const uint32_t eq_rank0 = block_exclusive_scan(n_eq, sh.wave_sums, eq_total);
-  uint32_t n_sel = 0;
-  {
-    uint32_t eq_rank = eq_rank0;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const bool eq = key[e] == threshold;
-      n_sel += (key[e] > threshold || (eq && eq_rank < krem)) ? 1u : 0u;
-      eq_rank += eq ? 1u : 0u;
-    }
+    for (int e = 0; e < EPT; ++e) mine += key[e] != 0 ? 1u : 0u;
+    block_exclusive_scan(mine, sh.wave_sums, n_valid);
   }
-  uint32_t sel_total;
-  const uint32_t pos0 = block_exclusive_scan(n_sel, sh.wave_sums, sel_total);
-  // The selection yields exactly min(n, k) elements; the clamp only guards the
-  // buffers should that invariant ever break.
-  sel_total = min(sel_total, (uint32_t)k);
-  {
-    uint32_t eq_rank = eq_rank0;
-    uint32_t p = pos0;
+  if (n_valid > (uint32_t)k) {
+    bool resolved = false;
+    float lo = __builtin_inff();
+    float hi = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const bool eq = key[e] == threshold;
-      if (key[e] > threshold || (eq && eq_rank < krem)) {
-        if (p < sel_total) sh.sort_keys[p] = (uint64_t(key[e]) << 32) | (uint64_t)(~(uint32_t)(e0 + e));
-        ++p;
-      }
-      eq_rank += eq ? 1u : 0u;
+      const float f = ordered_to_float(key[e]);
+      const bool fin = key[e] != 0 && __builtin_isfinite(f);
+      lo = fminf(lo, fin ? f : __builtin_inff());
+      hi = fmaxf(hi, fin ? f : -__builtin_inff());
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo = fminf(lo, __shfl_xor(lo, off, kWave));
+      hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+    }
+    if (lane == 0) {
+      sh.wave_lo[wave] = lo;
+      sh.wave_hi[wave] = hi;
+    }
+    for (int i = tid; i < kBins; i += kTopkThreads) sh.hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTopkWaves; ++i) {
+      lo = fminf(lo, sh.wave_lo[i]);
+      hi = fmaxf(hi, sh.wave_hi[i]);
+    }
+    const float scale = (float)kBins / (hi - lo);
+    if (lo < hi && __builtin_isfinite(scale) && scale > 0.f) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        lds_add(&sh.hist[value_bucket(key[e], lo, scale)], key[e] != 0 ? 1u : 0u);
+      __syncthreads();
+      locate_bin(sh, (uint32_t)k);
+      const int bucket = (int)sh.digit;
+      const uint32_t need = sh.krem;
+      const uint32_t crowd = sh.hist[bucket];
+      if (crowd <= (uint32_t)kMaxK) {
+        // Gather bucket T's composites at scan-assigned slots, sort them and
+        // read the need-th largest.
+        uint32_t mine = 0;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          mine += (key[e] != 0 && value_bucket(key[e], lo, scale) == bucket) ? 1u : 0u;
+        uint32_t total;
+        uint32_t slot = block_exclusive_scan(mine, sh.wave_sums, total);
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const bool in_t = key[e] != 0 && value_bucket(key[e], lo, scale) == bucket;
+          sh.sort_keys[in_t ? slot : kMaxK] = composite(key[e], e0 + e);
+          slot += in_t ? 1u : 0u;
+        }
+        int width = 1;
+        while (width < (int)crowd) width <<= 1;
+        for (int i = (int)crowd + tid; i < width; i += kTopkThreads) sh.sort_keys[i] = 0;
+        __syncthreads();
+        bitonic_sort_desc(sh.sort_keys, width);
+        cstar = sh.sort_keys[need - 1];
+        resolved = true;
+      }
+    }
+    if (!resolved) {
+      // Radix select of the k-th value, then the krem-th tie in index order.
+      uint32_t prefix = 0;
+      uint32_t prefix_mask = 0;
+      uint32_t want = (uint32_t)k;
+#pragma unroll 1
+      for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+        const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
+        __syncthreads();
+        for (int i = tid; i < kBins; i += kTopkThreads) sh.hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          lds_add(&sh.hist[(key[e] >> shift) & dmask],
+                  (key[e] != 0 && (key[e] & prefix_mask) == prefix) ? 1u : 0u);
+        __syncthreads();
+        locate_bin(sh, want);
+        prefix |= sh.digit << shift;
+        prefix_mask |= dmask << shift;
+        want = sh.krem;
+      }
+      const uint32_t threshold = prefix;
+      uint32_t mine = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) mine += key[e] == threshold ? 1u : 0u;
+      uint32_t ties;
+      uint32_t rank = block_exclusive_scan(mine, sh.wave_sums, ties);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const bool tie = key[e] == threshold;
+        if (tie && rank + 1 == want) sh.cstar = composite(threshold, e0 + e);
+        rank += tie ? 1u : 0u;
+      }
+      __syncthreads();
+      cstar = sh.cstar;
+    }
+    __syncthreads();
+  }
+
+  // Chosen elements (composite >= cstar) in index order.
+  uint32_t n_sel = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) n_sel += composite(key[e], e0 + e) >= cstar ? 1u : 0u;
+  uint32_t sel_total;
+  uint32_t p = block_exclusive_scan(n_sel, sh.wave_sums, sel_total);
+  // Exactly min(valid, k) elements are chosen; the clamp only guards buffers.
+  sel_total = min(sel_total, (uint32_t)k);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = composite(key[e], e0 + e);
+    const bool chosen = c >= cstar;
+    sh.sort_keys[(chosen && p < sel_total) ? p : kMaxK] = c;
+    p += chosen ? 1u : 0u;
   }
   __syncthreads();
 
@@ -192,23 +314,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     while (width < (int)sel_total) width <<= 1;
     for (int i = (int)sel_total + tid; i < width; i += kTopkThreads) sh.sort_keys[i] = 0;
     __syncthreads();
-    // Bitonic sort, descending on (key, ~position).
-    for (int size = 2; size <= width; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < (width >> 1); i += kTopkThreads) {
-          const int lo = 2 * i - (i & (stride - 1));
-          const int hi = lo + stride;
-          const uint64_t x = sh.sort_keys[lo];
-          const uint64_t y = sh.sort_keys[hi];
-          const bool desc = (lo & size) == 0;
-          if (desc ? (x < y) : (x > y)) {
-            sh.sort_keys[lo] = y;
-            sh.sort_keys[hi] = x;
-          }
-        }
-        __syncthreads();
-      }
-    }
+    bitonic_sort_desc(sh.sort_keys, width);
   }
   for (int i = tid; i < (int)sel_total; i += kTopkThreads) {
     const uint32_t pos = ~(uint32_t)(sh.sort_keys[i] & 0xffffffffu);

@@ -182,6 +182,41 @@ int dsa_topk_long(const float* scores, int64_t rows, int64_t length, int64_t k, 
                   int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused decode step: dense scores of `batch` sequences (as dsa_full_scores)
+ * plus the exact top-k of every sequence with the stable_topk rule.
+ * Replaces the reference benchmark's full-score launch followed by
+ * torch.topk (scripts/benchmark_progressive_dsa.py:117-123) with the
+ * selection semantics of metrics.py:9-22.
+ *
+ *   scores      [batch, length] fp32, written (materialised scores)
+ *   out_indices [batch, k] int64 in ascending index order (-1 padding when
+ *               length < k); out_values [batch, k] fp32 or NULL
+ *   workspace   dsa_score_topk_workspace_bytes(batch, length) bytes, 256-byte
+ *               aligned, zero-filled before its first use; every call leaves
+ *               it ready for the next one.  Calls that share a workspace must
+ *               be ordered (same stream); length <= 524288.
+ * Three launches: scoring (+ per-row score histogram), candidate gather and
+ * exact resolve, each spread over the whole GPU.
+ * ------------------------------------------------------------------------ */
+int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length);
+
+/* The two halves of dsa_score_topk, for callers that time or overlap them:
+ * dsa_score_hist writes the scores and the per-row score histogram into the
+ * workspace; dsa_select_topk turns scores + histogram into the top-k and
+ * leaves the workspace ready for the next dsa_score_hist. */
+int dsa_score_hist(const void* queries, const float* weights, const void* keys,
+                   const float* key_scales, float* scores, int64_t batch, int64_t length,
+                   int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t k,
+                    int64_t* out_indices, float* out_values, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+int dsa_score_topk(const void* queries, const float* weights, const void* keys,
+                   const float* key_scales, float* scores, int64_t batch, int64_t length,
+                   int64_t k, int32_t key_dtype, int64_t* out_indices, float* out_values,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Per-block maxima of score rows (replay.py:149-150 _block_max,
  * approx.py:53-55): out[r, b] = max(scores[r, b*bs : min(len, (b+1)*bs)]).
  * block_size is any positive value.
