@@ -89,7 +89,10 @@ def stable_topk(values: np.ndarray | torch.Tensor, k: int) -> np.ndarray | torch
     """Descending top-k indices with the index as deterministic tie-breaker.
 
     Reference: metrics.py:9-22 (same validation and messages).  A GPU tensor
-    yields a GPU int64 tensor; anything else yields a numpy int64 array.
+    yields a GPU int64 tensor; anything else is copied to the GPU and yields a
+    numpy int64 array.  The kernel compares float32 values, so inputs that
+    float32 cannot represent exactly are rejected with ValueError rather than
+    silently narrowed.
     """
 
     on_gpu = isinstance(values, torch.Tensor) and values.is_cuda
@@ -105,11 +108,20 @@ def stable_topk(values: np.ndarray | torch.Tensor, k: int) -> np.ndarray | torch
     if not 0 < k <= size:
         raise ValueError(f"k={k} is invalid for {size} values")
     if on_gpu:
+        if values.dtype != torch.float32:
+            narrowed = values.float()
+            if not torch.equal(narrowed.to(values.dtype), values):
+                raise ValueError("stable_topk on the GPU compares float32 values; these do not fit float32 exactly")
+            values = narrowed
         return topk(values, k, sorted=True)
-    device = _device()
     host = values.detach().cpu().numpy() if isinstance(values, torch.Tensor) else array
-    tensor = torch.from_numpy(np.ascontiguousarray(host, dtype=np.float32)).to(device)
-    return topk(tensor, k, sorted=True).cpu().numpy()
+    narrowed = np.ascontiguousarray(host, dtype=np.float32)
+    # The kernel orders float32 keys: a value that float32 cannot hold exactly
+    # could tie with a neighbour and change the selection.
+    if not np.array_equal(narrowed.astype(host.dtype, copy=False), host):
+        raise ValueError("stable_topk on the GPU compares float32 values; these do not fit float32 exactly")
+    device = _device()
+    return topk(torch.from_numpy(narrowed).to(device), k, sorted=True).cpu().numpy()
 
 
 def topk_recall(predicted, target) -> float:

@@ -195,8 +195,11 @@ int dsa_topk_long(const float* scores, int64_t rows, int64_t length, int64_t k, 
  *               aligned, zero-filled before its first use; every call leaves
  *               it ready for the next one.  Calls that share a workspace must
  *               be ordered (same stream); length <= 524288.
- * Three launches: scoring (+ per-row score histogram), candidate gather and
- * exact resolve, each spread over the whole GPU.
+ * Two launches for rows of up to 32768 keys with k <= 4096: scoring (+ a
+ * per-row 4096-bin score histogram) over the whole GPU, then one workgroup
+ * per row that finds the exact cut from the histogram.  Longer rows or larger
+ * k take a candidate-gather and an exact-resolve launch instead of the
+ * second one.
  * ------------------------------------------------------------------------ */
 int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length);
 

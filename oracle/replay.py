@@ -211,8 +211,13 @@ def replay_transition(
     previous_topk: np.ndarray | None = None,
     true_topk: np.ndarray | None = None,
     return_trace: bool = False,
+    sigma: float | None = None,
 ):
-    """Replay one decode transition.  Reference: replay.py:225-400."""
+    """Replay one decode transition.  Reference: replay.py:225-400.
+
+    ``sigma`` overrides the score-drift estimate, as the trace sweep's block
+    cache does (replay.py:482-483 computes it on the trace's float32 rows).
+    """
 
     previous = np.asarray(previous, dtype=np.float64)
     current = np.asarray(current, dtype=np.float64)
@@ -220,7 +225,8 @@ def replay_transition(
         raise ValueError("expected 1-D scores with previous length <= current length")
     if not 0 < k <= previous.size:
         raise ValueError("k must fit the previous step so it can seed replay")
-    current_max, previous_max, sigma = transition_setup(previous, current, block_size)
+    current_max, previous_max, own_sigma = transition_setup(previous, current, block_size)
+    sigma = own_sigma if sigma is None else float(sigma)
     gamma = gamma_sigma * sigma if absolute_gamma is None else float(absolute_gamma)
     upper = upper_bounds(previous_max, gamma, previous.size, current.size, block_size)
     seed = stable_topk(previous, k) if previous_topk is None else np.asarray(previous_topk)
@@ -315,6 +321,9 @@ def replay_trace_rows(
     for step in range(1, len(rows)):
         previous = np.asarray(rows[step - 1], dtype=np.float64)
         current = np.asarray(rows[step], dtype=np.float64)
+        # The drift is taken in the rows' own precision (float32 for a trace).
+        row_prev = np.asarray(rows[step - 1])
+        sigma = float(np.std(np.asarray(rows[step])[: row_prev.size] - row_prev))
         for k in k_values:
             if k > previous.size:
                 continue
@@ -324,7 +333,7 @@ def replay_trace_rows(
                 common = dict(
                     k=k, block_size=bs, step=step, layer=layer, workload=workload, prompt_id=prompt_id,
                     key_bytes=key_bytes, metadata_bytes_per_block=metadata_bytes_per_block,
-                    previous_topk=seed, true_topk=truth, wave=wave,
+                    previous_topk=seed, true_topk=truth, wave=wave, sigma=sigma,
                 )
                 for method, order in (("full", "address"), ("oracle", "oracle_current")):
                     out.append(asdict(replay_transition(previous, current, gamma_sigma=0.0, method=method, scan_order=order, **common)))

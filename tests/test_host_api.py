@@ -78,3 +78,10 @@ def test_reference_names_are_aliases() -> None:
     assert P.progressive_scores_triton is P.progressive_scores_hip
     assert P.two_pass_scores_triton is P.two_pass_scores_hip
     assert math.ceil(65 / 64) == 2
+
+
+def test_stable_topk_rejects_values_float32_cannot_hold() -> None:
+    # 1 + 2**-30 and 1.0 are distinct in float64 but equal in float32: narrowing
+    # them would create a tie the reference does not have.
+    with pytest.raises(ValueError, match="float32"):
+        metrics.stable_topk(np.array([1.0 + 2.0**-30, 1.0, 0.5]), 1)
