@@ -7,10 +7,13 @@ semantics).  One step = dense scores of all 16 x 32768 keys + the top-K of
 every sequence, inputs resident in HBM.  Four distinct key sets (4 x 128 MiB)
 are rotated so that the 256 MB last-level cache cannot hold the step's keys.
 
-Prints one JSON line (see the driver contract) with a `roofline` object for
-the dominant kernel (the scoring kernel, timed with HIP events on the stream
-it runs on) and a `cpu_baseline` object (the oracle's CPU restatement of the
-reference path timed on this host on a bounded sample).
+The timed region replays a HIP graph of 4 consecutive steps (one per key
+set): the step is three kernel launches and Python issues them slower than the
+GPU runs them.  Prints one JSON line (see the driver contract) with a
+`roofline` object for the dominant kernel (the scoring kernel, timed with HIP
+events around each launch on the stream it runs on) and a `cpu_baseline`
+object (the oracle's CPU restatement of the reference path timed on this host
+on a bounded sample).
 """
 
 from __future__ import annotations
@@ -113,21 +116,19 @@ def main() -> None:
     out_idx = torch.empty(BATCH, TOPK, device=device, dtype=torch.int64)
     ws_bytes = int(_lib.query("dsa_score_topk_workspace_bytes", BATCH, LENGTH))
     workspace = torch.zeros(ws_bytes, device=device, dtype=torch.uint8)
-    stream = torch.cuda.current_stream(device)
-    s_ptr = stream.cuda_stream
-
     # The decode step = dsa_score_topk, issued as its two halves so that the
-    # scoring kernel (the dominant one) can be timed on its own.
+    # scoring kernel (the dominant one) can be timed on its own.  Launches go
+    # to torch's current stream (the capture stream while a graph records).
     def score(keys):
         _lib.call(
             "dsa_score_hist", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(),
-            BATCH, LENGTH, _lib.DTYPE_BF16, workspace.data_ptr(), ws_bytes, s_ptr,
+            BATCH, LENGTH, _lib.DTYPE_BF16, workspace.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream,
         )
 
     def select():
         _lib.call(
             "dsa_select_topk", scores.data_ptr(), BATCH, LENGTH, TOPK, out_idx.data_ptr(), None,
-            workspace.data_ptr(), ws_bytes, s_ptr,
+            workspace.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream,
         )
 
     for i in range(args.warmup):
@@ -135,26 +136,54 @@ def main() -> None:
         select()
     torch.cuda.synchronize()
 
-    marks = [torch.cuda.Event(enable_timing=True) for _ in range(3 * args.steps)]
-    wall0 = time.perf_counter()
+    # The step is launch-bound from Python (three kernels, ~40 us of GPU work),
+    # so the timed region replays a HIP graph of ROTATIONS consecutive steps
+    # (one per key set); every launch in it is one of the library's kernels.
+    graph = torch.cuda.CUDAGraph()
+    capture = torch.cuda.Stream(device)
+    capture.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(capture):
+        for r in range(ROTATIONS):  # warm the capture stream
+            score(key_sets[r])
+            select()
+    torch.cuda.current_stream(device).wait_stream(capture)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for r in range(ROTATIONS):
+            score(key_sets[r])
+            select()
+    replays = max(1, -(-args.steps // ROTATIONS))
+    steps = replays * ROTATIONS
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
     t0.record(stream)
-    for i in range(args.steps):
+    for _ in range(replays):
+        graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_time(t1)
+    ms_per_step = total_ms / steps
+    keys_per_step = BATCH * LENGTH
+    value = keys_per_step / (ms_per_step / 1e3) / 1e9
+
+    # Per-kernel durations: HIP events around each launch, eagerly, on the
+    # stream the kernels run on.
+    timed = max(20, min(args.steps, 100))
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(3 * timed)]
+    for i in range(timed):
         marks[3 * i].record(stream)
         score(key_sets[i % ROTATIONS])
         marks[3 * i + 1].record(stream)
         select()
         marks[3 * i + 2].record(stream)
-    t1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    total_ms = t0.elapsed_time(t1)
-    score_ms = [marks[3 * i].elapsed_time(marks[3 * i + 1]) for i in range(args.steps)]
-    topk_ms = [marks[3 * i + 1].elapsed_time(marks[3 * i + 2]) for i in range(args.steps)]
-    ms_per_step = total_ms / args.steps
-    keys_per_step = BATCH * LENGTH
-    value = keys_per_step / (ms_per_step / 1e3) / 1e9
+    score_ms = [marks[3 * i].elapsed_time(marks[3 * i + 1]) for i in range(timed)]
+    topk_ms = [marks[3 * i + 1].elapsed_time(marks[3 * i + 2]) for i in range(timed)]
 
     # Algorithmic bytes of the scoring kernel per launch: every key row once
     # (256 B), one fp32 score written per key, the query block and weights once
@@ -180,7 +209,7 @@ def main() -> None:
         "value": round(value, 3),
         "unit": "G keys/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
@@ -211,6 +240,8 @@ def main() -> None:
             "algorithmic_bytes": step_bytes,
             "hbm_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "wall_s": round(wall, 3),
+            "timing": f"value: HIP events around {replays} replays of a graph of {ROTATIONS} steps; "
+            f"score_us/topk_us: HIP events around each launch over {timed} eager steps",
         },
         "recall_at_k": recall,
         "cpu_baseline": baseline,

@@ -1,35 +1,39 @@
-// Distributed exact top-k for the batched decode step (scores + selection).
+// Exact top-k for the batched decode step (scores + selection).
 //
 // The scoring kernel, run with a histogram workspace, also counts every score
 // of a row into 4096 bins given by the top 12 bits of its order-preserving key
-// (a bin's values are all larger than every value of a lower bin).  Two
-// kernels then select the k largest per row with the stable_topk rule (ties at
-// the cut-off to the lower index, reference metrics.py:9-22), each spread over
-// ceil(L / 2048) workgroups per row:
-//   gather:  find the bin T holding the k-th largest, count each chunk's
-//            elements in bins above T, and append T's elements (as composites
-//            (key << 32 | ~index)) to the row's candidate list;
-//   resolve: radix-select the exact cut-off composite among the candidates,
-//            derive every chunk's output offset, write the chosen indices of
-//            the chunk in ascending index order, and clear the histogram.
-// Kernel boundaries order the phases, so no workgroup ever waits on another.
+// (a bin's values are all larger than every value of a lower bin).  The k
+// largest per row are then selected with the stable_topk rule (ties at the
+// cut-off to the lower index, reference metrics.py:9-22), indices written in
+// ascending order, by two launches over the whole GPU, one 256-thread
+// workgroup per 2048-score chunk of a row:
+//   gather:  locate the bin T holding the k-th largest score, count the
+//            chunk's scores above T, and write the chunk's scores inside T
+//            (as composites key << 32 | ~index) to the chunk's candidate slice;
+//   resolve: fetch the row's counts and candidates in one round trip,
+//            radix-select the exact cut among the candidates, derive the
+//            chunk's output offset, write its chosen indices, and clear the
+//            chunk's share of the histogram for the next call.
+// The kernel boundary is the only synchronisation between workgroups.  A
+// one-workgroup-per-row kernel (rows up to 32768, k <= 4096) is kept as an
+// alternative path (DSA_SELECT_PATH=row).
 #include "common.hpp"
 #include "select.hpp"
 #include "status.hpp"
+
+#include <cstdlib>
+#include <cstring>
 
 namespace dsa {
 namespace {
 
 constexpr int kSelThreads = 256;
 constexpr int kSelWaves = kSelThreads / kWave;
-constexpr int kSelEpt = kSelectChunk / kSelThreads;  // 8
+constexpr int kSelEpt = kSelectChunk / kSelThreads;  // 8 scores per thread
 constexpr int kDigitBins = 2048;
-constexpr int kCandCapacity = 4096;  // candidates staged in LDS (else read in place)
+constexpr int kCandCapacity = 4096;  // row candidates staged in LDS (else read in place)
+constexpr int kSpecSlots = 1024;     // candidate slots fetched with the counts
 constexpr uint32_t kNoBin = 0xffffffffu;
-// Buffer stores aimed here fall outside every descriptor's range and are
-// dropped; small enough that offset + size cannot wrap.
-constexpr uint32_t kSinkOffset = 0x7ffffff0u;
-constexpr uint32_t kSinkSlot = 0x0ffffffeu;  // * 8 stays below 2^31
 
 struct SelectArgs {
   const float* scores;  // [rows, length]
@@ -46,320 +50,15 @@ __device__ __forceinline__ uint64_t composite(uint32_t key, int pos) {
   return (uint64_t(key) << 32) | (uint64_t)(~(uint32_t)pos);
 }
 
-// Exclusive scan over the 256 threads; two barriers.
-__device__ __forceinline__ uint32_t sel_scan(uint32_t v, uint32_t* wave_sums, uint32_t& total) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(x, off, kWave);
-    x += lane >= off ? y : 0u;
-  }
-  if (lane == 63) wave_sums[wave] = x;
-  __syncthreads();
-  uint32_t before = 0;
-  uint32_t all = 0;
-#pragma unroll
-  for (int i = 0; i < kSelWaves; ++i) {
-    const uint32_t s = wave_sums[i];
-    before += i < wave ? s : 0u;
-    all += s;
-  }
-  __syncthreads();
-  total = all;
-  return before + x - v;
+// Same XCD-aware renumbering as the scoring kernel: with a grid that is a
+// multiple of 8, a row's chunks run on one XCD, whose L2 holds its scores.
+__device__ __forceinline__ uint32_t logical_block() {
+  const uint32_t grid = gridDim.x;
+  const uint32_t b = blockIdx.x;
+  return (grid % 8u == 0u) ? (b % 8u) * (grid / 8u) + b / 8u : b;
 }
 
-// Loads this thread's 8 ordered keys of chunk c (0 = past the row end).
-__device__ __forceinline__ void load_chunk(const float* row_scores, int length, int c,
-                                           uint32_t (&key)[kSelEpt], int& e0) {
-  e0 = c * kSelectChunk + threadIdx.x * kSelEpt;
-  const BufferRsrc rsrc = make_buffer(row_scores, (uint32_t)length * 4u);
-#pragma unroll
-  for (int h = 0; h < kSelEpt / 4; ++h) {
-    const uint4 raw = buffer_load_16(rsrc, (uint32_t)(e0 + 4 * h) * 4u);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      key[4 * h + i] = e0 + 4 * h + i < length ? float_to_ordered(__uint_as_float(w4[i])) : 0u;
-  }
-}
-
-__global__ __launch_bounds__(kSelThreads) void select_gather_kernel(SelectArgs a) {
-  __shared__ uint32_t wave_sums[kSelWaves];
-  __shared__ uint32_t s_bin;
-  __shared__ uint32_t s_need;
-  const int tid = threadIdx.x;
-  const int row = blockIdx.x / a.chunks;
-  const int c = blockIdx.x % a.chunks;
-
-  // Issue the chunk's scores and the row histogram together.
-  uint32_t key[kSelEpt];
-  int e0;
-  load_chunk(a.scores + (size_t)row * a.length, a.length, c, key, e0);
-  uint32_t h[16];  // thread t owns bins [16t, 16t + 16)
-  {
-    const uint4* p = reinterpret_cast<const uint4*>(a.ws.hist + (size_t)row * kSelectBins + tid * 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 v = p[i];
-      h[4 * i] = v.x;
-      h[4 * i + 1] = v.y;
-      h[4 * i + 2] = v.z;
-      h[4 * i + 3] = v.w;
-    }
-  }
-  uint32_t mine = 0;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) mine += h[i];
-  if (tid == 0) {
-    s_bin = kNoBin;
-    s_need = 0;
-  }
-  uint32_t total;
-  const uint32_t before = sel_scan(mine, wave_sums, total);
-  const uint32_t want = (uint32_t)a.k;
-  uint32_t above = total - before - mine;  // elements in bins past this thread's
-#pragma unroll
-  for (int i = 15; i >= 0; --i) {
-    if (total > want && h[i] && above < want && want <= above + h[i]) {
-      s_bin = tid * 16 + i;
-      s_need = want - above;
-    }
-    above += h[i];
-  }
-  __syncthreads();
-  const uint32_t bin = s_bin;
-  if (c == 0 && tid == 0) {
-    uint32_t* meta = a.ws.meta + (size_t)row * 4;
-    meta[0] = bin;
-    meta[1] = s_need;
-    meta[2] = total;
-  }
-
-  // This chunk: elements above T are chosen outright, T's are candidates and
-  // go to the chunk's own slice of the candidate buffer.
-  uint32_t n_above = 0;
-  uint32_t n_cand = 0;
-#pragma unroll
-  for (int e = 0; e < kSelEpt; ++e) {
-    const uint32_t b = key[e] >> 20;
-    const bool valid = key[e] != 0;
-    n_above += (valid && (bin == kNoBin || b > bin)) ? 1u : 0u;
-    n_cand += (valid && bin != kNoBin && b == bin) ? 1u : 0u;
-  }
-  uint32_t above_total;
-  sel_scan(n_above, wave_sums, above_total);
-  uint32_t cand_total;
-  uint32_t rank = sel_scan(n_cand, wave_sums, cand_total);
-  if (tid == 0) {
-    a.ws.above[(size_t)row * a.chunks + c] = above_total;
-    a.ws.cand_count[(size_t)row * a.chunks + c] = cand_total;
-  }
-  const BufferRsrc cand = make_buffer(a.ws.cand + (size_t)row * a.length + (size_t)c * kSelectChunk,
-                                      kSelectChunk * 8u);
-#pragma unroll
-  for (int e = 0; e < kSelEpt; ++e) {
-    const bool is_cand = key[e] != 0 && bin != kNoBin && (key[e] >> 20) == bin;
-    buffer_store_u64(cand, is_cand ? rank * 8u : kSinkOffset, composite(key[e], e0 + e));
-    rank += is_cand ? 1u : 0u;
-  }
-}
-
-__global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs a) {
-  __shared__ uint32_t wave_sums[kSelWaves];
-  __shared__ uint32_t hist[kDigitBins];
-  __shared__ uint32_t chunk_above[kMaxSelectChunks];
-  __shared__ uint32_t chunk_count[kMaxSelectChunks];
-  __shared__ uint32_t chunk_first[kMaxSelectChunks + 1];
-  __shared__ uint32_t chunk_chosen[kMaxSelectChunks];
-  __shared__ uint64_t cands[kCandCapacity];
-  __shared__ uint32_t s_digit;
-  __shared__ uint32_t s_krem;
-  __shared__ uint64_t s_cstar;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int row = blockIdx.x / a.chunks;
-  const int c = blockIdx.x % a.chunks;
-  const int chunks = a.chunks;
-
-  // Issue this chunk's scores, the row's meta and per-chunk counts together.
-  uint32_t key[kSelEpt];
-  int e0;
-  load_chunk(a.scores + (size_t)row * a.length, a.length, c, key, e0);
-  const uint32_t* meta = a.ws.meta + (size_t)row * 4;
-  const uint32_t bin = meta[0];
-  const uint32_t need = meta[1];
-  const uint32_t total = meta[2];
-  for (int j = tid; j < chunks; j += kSelThreads) {
-    chunk_above[j] = a.ws.above[(size_t)row * chunks + j];
-    chunk_count[j] = a.ws.cand_count[(size_t)row * chunks + j];
-    chunk_chosen[j] = 0;
-  }
-  __syncthreads();
-  if (tid < kWave) {  // exclusive prefix of the candidate counts
-    uint32_t carry = 0;
-    for (int j0 = 0; j0 < chunks; j0 += kWave) {
-      const int j = j0 + lane;
-      const uint32_t v = j < chunks ? chunk_count[j] : 0u;
-      uint32_t x = v;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, kWave);
-        x += lane >= off ? y : 0u;
-      }
-      if (j < chunks) chunk_first[j] = carry + x - v;
-      carry += __shfl(x, 63, kWave);
-    }
-    if (lane == 0) chunk_first[chunks] = carry;
-  }
-  __syncthreads();
-  const uint32_t crowd = chunk_first[chunks];
-  const bool in_lds = crowd <= (uint32_t)kCandCapacity;
-  const uint64_t* row_cands = a.ws.cand + (size_t)row * a.length;
-
-  // Cut-off composite: with no threshold bin every valid element is chosen.
-  uint64_t cstar = uint64_t(1) << 32;
-  if (bin != kNoBin) {
-    // Candidate i of the row in chunk-major order lives in the slice of the
-    // chunk j with chunk_first[j] <= i < chunk_first[j + 1].
-    auto cand_global = [&](uint32_t i) -> uint64_t {
-      int lo = 0;
-      int hi = chunks - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (chunk_first[mid] <= i) lo = mid;
-        else hi = mid - 1;
-      }
-      return row_cands[(size_t)lo * kSelectChunk + (i - chunk_first[lo])];
-    };
-    if (in_lds) {
-      for (uint32_t i = tid; i < crowd; i += kSelThreads) cands[i] = cand_global(i);
-      __syncthreads();
-    }
-    auto cand_at = [&](uint32_t i) -> uint64_t { return in_lds ? cands[i] : cand_global(i); };
-    // Radix select of the need-th largest composite below the 12 bits the
-    // candidates share; stops as soon as the cut-off digit holds one of them.
-    uint64_t prefix = uint64_t(bin) << 52;
-    uint64_t mask = uint64_t(0xfff) << 52;
-    uint32_t want = need;
-    bool done = false;
-#pragma unroll 1
-    for (int shift = 41; shift > -11 && !done; shift -= 11) {
-      const int sh = shift < 0 ? 0 : shift;
-      const uint32_t width = shift < 0 ? (uint32_t)(11 + shift) : 11u;
-      const uint64_t dmask = (uint64_t(1) << width) - 1;
-      __syncthreads();
-      for (int i = tid; i < kDigitBins; i += kSelThreads) hist[i] = 0;
-      if (tid == 0) {
-        s_digit = 0;
-        s_krem = 1;
-      }
-      __syncthreads();
-      for (uint32_t i = tid; i < crowd; i += kSelThreads) {
-        const uint64_t x = cand_at(i);
-        __hip_atomic_fetch_add(&hist[(x >> sh) & dmask], (x & mask) == prefix ? 1u : 0u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-      __syncthreads();
-      // Thread t owns digits [8t, 8t + 8).
-      uint32_t hv[8];
-      uint32_t mine = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        hv[i] = hist[tid * 8 + i];
-        mine += hv[i];
-      }
-      uint32_t all;
-      const uint32_t before = sel_scan(mine, wave_sums, all);
-      uint32_t above = all - before - mine;
-#pragma unroll
-      for (int i = 7; i >= 0; --i) {
-        if (hv[i] && above < want && want <= above + hv[i]) {
-          s_digit = tid * 8 + i;
-          s_krem = want - above;
-        }
-        above += hv[i];
-      }
-      __syncthreads();
-      const uint32_t digit = s_digit;
-      prefix |= uint64_t(digit) << sh;
-      mask |= dmask << sh;
-      want = s_krem;
-      done = hist[digit] == 1 || sh == 0;
-    }
-    // The unique candidate matching the prefix is the cut-off.
-    for (uint32_t i = tid; i < crowd; i += kSelThreads) {
-      const uint64_t x = cand_at(i);
-      if ((x & mask) == prefix) s_cstar = x;
-    }
-    __syncthreads();
-    cstar = s_cstar;
-    // Chosen candidates per chunk (a candidate's chunk follows from its index).
-    for (uint32_t i = tid; i < crowd; i += kSelThreads) {
-      const uint64_t x = cand_at(i);
-      const uint32_t pos = ~(uint32_t)(x & 0xffffffffu);
-      __hip_atomic_fetch_add(&chunk_chosen[pos / kSelectChunk], x >= cstar ? 1u : 0u,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-  }
-  __syncthreads();
-  // Output offset of this chunk: everything chosen in the chunks before it.
-  uint32_t offset = 0;
-  for (int j = 0; j < c; ++j) offset += chunk_above[j] + chunk_chosen[j];
-
-  uint32_t n_sel = 0;
-#pragma unroll
-  for (int e = 0; e < kSelEpt; ++e) n_sel += composite(key[e], e0 + e) >= cstar ? 1u : 0u;
-  uint32_t sel_total;
-  uint32_t rank = offset + sel_scan(n_sel, wave_sums, sel_total);
-  const uint32_t kk = (uint32_t)a.k;
-  const BufferRsrc oidx = make_buffer(a.out_idx + (size_t)row * kk, kk * 8u);
-  const BufferRsrc oval = make_buffer(a.out_val ? a.out_val + (size_t)row * kk : nullptr,
-                                      a.out_val ? kk * 4u : 0u);
-#pragma unroll
-  for (int e = 0; e < kSelEpt; ++e) {
-    const bool chosen = composite(key[e], e0 + e) >= cstar;
-    const uint32_t slot = chosen ? rank : kSinkSlot;  // dropped past the row
-    buffer_store_u64(oidx, slot * 8u, (uint64_t)(int64_t)(e0 + e));
-    if (a.out_val)
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ordered_to_float(key[e])), oval,
-                                            (int)(slot * 4u), 0, 0);
-    rank += chosen ? 1u : 0u;
-  }
-  // Rows with fewer than k scores: pad with index -1 / value -inf.
-  if (c == 0) {
-    for (uint32_t i = min(total, kk) + tid; i < kk; i += kSelThreads) {
-      a.out_idx[(size_t)row * kk + i] = -1;
-      if (a.out_val) a.out_val[(size_t)row * kk + i] = -__builtin_inff();
-    }
-  }
-  // Leave the histogram zeroed for the next call (its readers are done).
-  const int per = (kSelectBins + chunks - 1) / chunks;
-  uint32_t* hrow = a.ws.hist + (size_t)row * kSelectBins;
-  for (int i = c * per + tid; i < min(kSelectBins, (c + 1) * per); i += kSelThreads) hrow[i] = 0;
-}
-
-// Rows of up to 32768 scores with k <= 4096: one 1024-thread workgroup per
-// row.  Wave w holds positions [2048w, 2048w + 2048) in registers, lane l the
-// eight 4-position groups 2048w + 256g + 4l (g = 0..7), so that a wave's
-// positions in (g, lane, i) order are in index order.  Wave 0 alone locates
-// the threshold bin in the histogram the scoring kernel built, and later the
-// radix digits; the bin's keys are compacted into LDS with ballots, the exact
-// k-th key is radix-selected among them (bits 19..9, then 8..0), ties at that
-// key are ranked by position, and the chosen positions are staged in LDS in
-// index order and written out coalesced.  The kernel runs once per row, so
-// its time is set by latency: it avoids block-wide scans on the common path
-// (one barrier per phase, wave-level ballot and DPP scans otherwise).
-constexpr int kRowThreads = 1024;
-constexpr int kRowWaves = kRowThreads / kWave;
-constexpr int kRowLength = 32768;
-constexpr int kRowGroups = 8;      // 4-position groups per lane
-constexpr int kRowMaxK = 4096;
-constexpr int kRowCand = 4096;     // threshold-bin keys compacted into LDS
-constexpr int kRowDigits1 = 2048;  // bits 19..9
-constexpr int kRowDigits2 = 512;   // bits 8..0
+constexpr int kRowWaves = 1024 / kWave;
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (kWave - 1); }
 
@@ -379,7 +78,9 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
 
 // Exclusive scan over the workgroup: one barrier; `ws` (16 words) must not be
 // rewritten until every thread has passed a later barrier.
+template <int kWaves>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* ws, uint32_t& total) {
+  static_assert(kWaves % 4 == 0, "wave sums are read 4 at a time");
   const uint32_t lane = lane_id();
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t incl = wave_incl_scan(v);
@@ -388,7 +89,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* ws, ui
   uint32_t before = 0;
   uint32_t all = 0;
 #pragma unroll
-  for (int q = 0; q < kRowWaves / 4; ++q) {
+  for (int q = 0; q < kWaves / 4; ++q) {
     const uint4 s4 = reinterpret_cast<const uint4*>(ws)[q];
     const uint32_t sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
@@ -409,6 +110,7 @@ struct Locate {
   uint32_t digit;  // kNoBin when the want-th largest is not in these bins
   uint32_t rem;    // its rank among the keys of that digit (1-based)
   uint32_t count;  // keys in that digit
+  uint32_t total;  // keys in all bins
 };
 
 // One wave finds the bin holding the want-th largest key among 64*N LDS
@@ -432,7 +134,7 @@ __device__ __forceinline__ Locate wave_locate(const uint32_t* bins, uint32_t wan
   const uint32_t total = __builtin_amdgcn_readlane(incl, kWave - 1);
   const uint32_t above = total - incl;  // keys in the bins of higher lanes
   const uint64_t m = __ballot(above < want && want <= above + sum);
-  if (m == 0 || (none_if_fits && total <= want)) return Locate{kNoBin, 0u, 0u};
+  if (m == 0 || (none_if_fits && total <= want)) return Locate{kNoBin, 0u, 0u, total};
   const uint32_t owner = (uint32_t)__builtin_ctzll(m);
   const uint32_t above_owner = __builtin_amdgcn_readlane(above, owner);
   const uint32_t c = lane < (uint32_t)N ? bins[N * owner + lane] : 0u;
@@ -441,8 +143,342 @@ __device__ __forceinline__ Locate wave_locate(const uint32_t* bins, uint32_t wan
   const uint64_t m2 = __ballot(above2 < want && want <= above2 + c);
   const uint32_t j = (uint32_t)__builtin_ctzll(m2);
   return Locate{N * owner + j, want - (uint32_t)__builtin_amdgcn_readlane(above2, j),
-                (uint32_t)__builtin_amdgcn_readlane(c, j)};
+                (uint32_t)__builtin_amdgcn_readlane(c, j), total};
 }
+
+
+// ---------------------------------------------------------------------------
+// gather: one workgroup per (row, chunk).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kSelThreads) void select_gather_kernel(SelectArgs a) {
+  __shared__ __align__(16) uint32_t hist[kSelectBins];
+  __shared__ __align__(16) uint32_t wsum[kSelWaves];
+  __shared__ uint32_t s_bin, s_want, s_total;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = lane_id();
+  const uint32_t wave = tid / kWave;
+  const uint32_t chunks = (uint32_t)a.chunks;
+  const uint32_t logical = logical_block();
+  const uint32_t row = logical / chunks;
+  const uint32_t c = logical % chunks;
+  const uint32_t n = (uint32_t)a.length;
+  const uint32_t kk = (uint32_t)a.k;
+  const uint32_t p0 = c * kSelectChunk + tid * kSelEpt;
+
+  // This thread's 8 scores and 16 bins of the row's histogram, issued together.
+  const BufferRsrc srs = make_buffer(a.scores + (size_t)row * n, n * 4u);
+  const uint4 s0 = buffer_load_16(srs, p0 * 4u);
+  const uint4 s1 = buffer_load_16(srs, (p0 + 4u) * 4u);
+  {
+    const BufferRsrc hr = make_buffer(a.ws.hist + (size_t)row * kSelectBins, kSelectBins * 4u);
+#pragma unroll
+    for (int q = 0; q < kSelectBins / (4 * kSelThreads); ++q)
+      reinterpret_cast<uint4*>(hist)[tid + q * kSelThreads] = buffer_load_16(hr, (tid + q * kSelThreads) * 16u);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const Locate t = wave_locate<kSelectBins / kWave>(hist, kk, true);
+    if (lane == 0) {
+      s_bin = t.digit;
+      s_want = t.rem;
+      s_total = t.total;
+    }
+  }
+  __syncthreads();
+  const uint32_t bin = s_bin;
+
+  uint32_t key[kSelEpt];
+  {
+    const uint32_t w8[kSelEpt] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < kSelEpt; ++i) key[i] = p0 + i < n ? float_to_ordered(__uint_as_float(w8[i])) : 0u;
+  }
+  uint32_t n_above = 0;
+  uint32_t n_cand = 0;
+#pragma unroll
+  for (int i = 0; i < kSelEpt; ++i) {
+    const uint32_t kb = key[i] >> 20;
+    n_above += (key[i] != 0 && (bin == kNoBin || kb > bin)) ? 1u : 0u;
+    n_cand += (key[i] != 0 && bin != kNoBin && kb == bin) ? 1u : 0u;
+  }
+  uint32_t packed_total;
+  const uint32_t packed = block_excl_scan<kSelWaves>((n_cand << 16) | n_above, wsum, packed_total);
+  if (n_cand) {
+    uint64_t* slice = a.ws.cand + (size_t)row * n + (size_t)c * kSelectChunk;
+    uint32_t slot = packed >> 16;
+#pragma unroll
+    for (int i = 0; i < kSelEpt; ++i)
+      if (key[i] != 0 && (key[i] >> 20) == bin) slice[slot++] = composite(key[i], (int)(p0 + i));
+  }
+  if (tid == 0) {
+    a.ws.above[(size_t)row * chunks + c] = packed_total & 0xffffu;
+    a.ws.cand_count[(size_t)row * chunks + c] = packed_total >> 16;
+    if (c == 0) {
+      a.ws.meta[row * 4 + 0] = bin;
+      a.ws.meta[row * 4 + 1] = s_want;
+      a.ws.meta[row * 4 + 2] = s_total;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// resolve: one workgroup per (row, chunk).
+//
+// One round trip fetches this chunk's scores, the row's meta, the per-chunk
+// counts (wave 0 scans them) and the first slots of every chunk's candidate
+// slice; the candidates are staged in LDS.  The exact cut is a radix select
+// over (key, ~position) composites: all waves count 11-bit digits, wave 0
+// locates the digit holding the cut, and a digit with a single candidate ends
+// it (that candidate was recorded while counting).  The candidates of the
+// earlier chunks at or above the cut and this chunk's chosen scores share one
+// block scan.  Five barriers in the common case.
+// ---------------------------------------------------------------------------
+struct ResolveShared {
+  uint64_t cands[kCandCapacity];
+  uint64_t last[kDigitBins];            // a candidate of each digit (the only one when its count is 1)
+  uint32_t digits[2][kDigitBins];
+  uint32_t base[kMaxSelectChunks + 1];  // candidate prefix over the row's chunks
+  uint32_t wsum[2][kSelWaves];
+  uint32_t digit, rem, count, offset, crowd, overflow;
+};
+
+__global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs a) {
+  __shared__ ResolveShared sh;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = lane_id();
+  const uint32_t wave = tid / kWave;
+  const uint32_t chunks = (uint32_t)a.chunks;
+  const uint32_t logical = logical_block();
+  const uint32_t row = logical / chunks;
+  const uint32_t c = logical % chunks;
+  const uint32_t n = (uint32_t)a.length;
+  const uint32_t kk = (uint32_t)a.k;
+  const uint32_t p0 = c * kSelectChunk + tid * kSelEpt;
+  const uint64_t* row_cands = a.ws.cand + (size_t)row * n;
+
+  // One round trip: this chunk's scores, the row's meta, the per-chunk counts
+  // (wave 0, up to 4 chunks per lane) and the first `spec` candidate slots of
+  // every chunk (valid below a chunk's count, stale above it).
+  const BufferRsrc srs = make_buffer(a.scores + (size_t)row * n, n * 4u);
+  const uint4 s0 = buffer_load_16(srs, p0 * 4u);
+  const uint4 s1 = buffer_load_16(srs, (p0 + 4u) * 4u);
+  const uint32_t bin = a.ws.meta[row * 4 + 0];
+  const uint32_t want = a.ws.meta[row * 4 + 1];
+  const uint32_t total = a.ws.meta[row * 4 + 2];
+  constexpr int kPerLane = kMaxSelectChunks / kWave;  // 4
+  uint32_t above_q[kPerLane];
+  uint32_t cand_q[kPerLane];
+  if (wave == 0) {
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      const uint32_t j = lane * kPerLane + q;
+      above_q[q] = j < chunks ? a.ws.above[(size_t)row * chunks + j] : 0u;
+      cand_q[q] = j < chunks ? a.ws.cand_count[(size_t)row * chunks + j] : 0u;
+    }
+  }
+  const uint32_t spec = kSpecSlots / chunks;  // >= 4
+  uint64_t pre[kSpecSlots / kSelThreads];
+  if (bin != kNoBin) {
+#pragma unroll
+    for (int i = 0; i < kSpecSlots / kSelThreads; ++i) {
+      const uint32_t p = tid + i * kSelThreads;
+      const uint32_t j = p / spec;
+      const uint32_t at = j * kSelectChunk + p % spec;  // stays inside the row's candidate area
+      pre[i] = (j < chunks && at < n) ? row_cands[at] : 0u;
+    }
+  }
+  if (wave == 0) {
+    // Exclusive prefix of both counts over the chunks, lane-major.
+    uint32_t a_sum = 0;
+    uint32_t c_sum = 0;
+    uint32_t widest = 0;
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      a_sum += above_q[q];
+      c_sum += cand_q[q];
+      widest = max(widest, cand_q[q]);
+    }
+    const uint32_t a_incl = wave_incl_scan(a_sum);
+    const uint32_t c_incl = wave_incl_scan(c_sum);
+    uint32_t a_run = a_incl - a_sum;
+    uint32_t c_run = c_incl - c_sum;
+#pragma unroll
+    for (int q = 0; q < kPerLane; ++q) {
+      const uint32_t j = lane * kPerLane + q;
+      if (j < chunks) sh.base[j] = c_run;
+      if (j == c) sh.offset = a_run;  // chosen scores above the bin in earlier chunks
+      a_run += above_q[q];
+      c_run += cand_q[q];
+    }
+    const bool overflow = __ballot(widest > spec) != 0;
+    if (lane == kWave - 1) {
+      sh.base[chunks] = c_incl;
+      sh.crowd = c_incl;
+      sh.overflow = overflow ? 1u : 0u;
+    }
+  } else {
+    for (uint32_t i = tid - kWave; i < 2u * kDigitBins; i += kSelThreads - kWave) (&sh.digits[0][0])[i] = 0;
+  }
+  __syncthreads();
+  const uint32_t crowd = sh.crowd;
+  const bool in_lds = crowd <= (uint32_t)kCandCapacity;
+  auto chunk_of = [&](uint32_t i) -> uint32_t {  // last chunk whose base is <= i
+    uint32_t lo = 0;
+    uint32_t hi = chunks - 1;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (sh.base[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
+  auto cand_at = [&](uint32_t i) -> uint64_t {
+    if (in_lds) return sh.cands[i];
+    const uint32_t j = chunk_of(i);
+    return row_cands[(size_t)j * kSelectChunk + (i - sh.base[j])];
+  };
+
+  uint64_t cstar = uint64_t(1) << 32;  // every valid score when the row has <= k
+  if (bin != kNoBin) {
+    if (in_lds) {
+#pragma unroll
+      for (int i = 0; i < kSpecSlots / kSelThreads; ++i) {
+        const uint32_t p = tid + i * kSelThreads;
+        const uint32_t j = p / spec;
+        const uint32_t s = p % spec;
+        if (j < chunks && sh.base[j] + s < sh.base[j + 1]) sh.cands[sh.base[j] + s] = pre[i];
+      }
+      if (sh.overflow) {
+        // Some chunk holds more candidates than its prefetched slots: the rest.
+        for (uint32_t i = tid; i < crowd; i += kSelThreads) {
+          const uint32_t j = chunk_of(i);
+          const uint32_t s = i - sh.base[j];
+          if (s >= spec) sh.cands[i] = row_cands[(size_t)j * kSelectChunk + s];
+        }
+      }
+      __syncthreads();
+    }
+    // Radix select of the want-th largest composite: the top 12 bits are the
+    // bin; 11-bit digits of bits 51..8, then bits 7..0.
+    uint64_t prefix = uint64_t(bin) << 52;
+    uint64_t mask = uint64_t(0xfff) << 52;
+    uint32_t rem = want;
+    bool done = false;
+#pragma unroll 1
+    for (int pass = 0; pass < 5; ++pass) {
+      const int shift = pass < 4 ? 41 - 11 * pass : 0;
+      const uint32_t dmask = pass < 4 ? 0x7ffu : 0xffu;
+      uint32_t* dig = sh.digits[pass & 1];
+      for (uint32_t i = tid; i < crowd; i += kSelThreads) {
+        const uint64_t x = cand_at(i);
+        if ((x & mask) == prefix) {
+          const uint32_t d = (uint32_t)(x >> shift) & dmask;
+          __hip_atomic_fetch_add(&dig[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          sh.last[d] = x;
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const Locate t = wave_locate<kDigitBins / kWave>(dig, rem, false);
+        if (lane == 0) {
+          sh.digit = t.digit;
+          sh.rem = t.rem;
+          sh.count = t.count;
+        }
+      } else {
+        // Meanwhile clear the other buffer for the next pass.
+        uint32_t* next = sh.digits[(pass + 1) & 1];
+        for (uint32_t i = tid - kWave; i < (uint32_t)kDigitBins; i += kSelThreads - kWave) next[i] = 0;
+      }
+      __syncthreads();
+      if (sh.digit == kNoBin) break;  // unreachable for consistent counts
+      prefix |= uint64_t(sh.digit) << shift;
+      mask |= uint64_t(dmask) << shift;
+      rem = sh.rem;
+      if (sh.count == 1) {
+        cstar = sh.last[sh.digit];  // the one candidate carrying the prefix
+        done = true;
+        break;
+      }
+      // sh.digit / sh.rem / sh.last are rewritten only after the next pass's
+      // first barrier, which every thread reaches after reading them here.
+    }
+    if (!done) cstar = prefix;  // all 64 bits fixed
+  }
+
+  // This chunk's chosen scores in index order, after the chosen scores of the
+  // earlier chunks: those above the bin (sh.offset) and the candidates at or
+  // above the cut, counted here and summed by the same block scan.
+  uint32_t key[kSelEpt];
+  {
+    const uint32_t w8[kSelEpt] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < kSelEpt; ++i) key[i] = p0 + i < n ? float_to_ordered(__uint_as_float(w8[i])) : 0u;
+  }
+  uint32_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < kSelEpt; ++i) mine += composite(key[i], (int)(p0 + i)) >= cstar ? 1u : 0u;
+  uint32_t before = 0;
+  if (bin != kNoBin)
+    for (uint32_t i = tid; i < sh.base[c]; i += kSelThreads) before += cand_at(i) >= cstar ? 1u : 0u;
+  const uint32_t offset = sh.offset;
+  uint32_t slot;
+  if (crowd < 65536u) {
+    uint32_t packed_total;
+    const uint32_t packed = block_excl_scan<kSelWaves>((before << 16) | mine, sh.wsum[0], packed_total);
+    slot = offset + (packed_total >> 16) + (packed & 0xffffu);
+  } else {
+    uint32_t before_all;
+    block_excl_scan<kSelWaves>(before, sh.wsum[0], before_all);
+    uint32_t chunk_total;
+    slot = offset + before_all + block_excl_scan<kSelWaves>(mine, sh.wsum[1], chunk_total);
+  }
+  int64_t* oidx = a.out_idx + (size_t)row * kk;
+  float* oval = a.out_val ? a.out_val + (size_t)row * kk : nullptr;
+  if (mine) {
+#pragma unroll
+    for (int i = 0; i < kSelEpt; ++i) {
+      if (composite(key[i], (int)(p0 + i)) >= cstar) {
+        if (slot < kk) {  // always true for consistent counts; keeps writes in the row
+          oidx[slot] = (int64_t)(p0 + i);
+          if (oval) oval[slot] = ordered_to_float(key[i]);
+        }
+        ++slot;
+      }
+    }
+  }
+  if (c == 0) {
+    for (uint32_t i = min(total, kk) + tid; i < kk; i += kSelThreads) {
+      oidx[i] = -1;
+      if (oval) oval[i] = -__builtin_inff();
+    }
+  }
+  // No reader of the row's histogram is left: clear this chunk's share.
+  {
+    uint32_t* hrow = a.ws.hist + (size_t)row * kSelectBins;
+    const uint32_t per = (kSelectBins + chunks - 1) / chunks;
+    for (uint32_t i = tid; i < per; i += kSelThreads)
+      if (c * per + i < (uint32_t)kSelectBins) hrow[c * per + i] = 0;
+  }
+}
+
+// Rows of up to 32768 scores with k <= 4096: one 1024-thread workgroup per
+// row.  Wave w holds positions [2048w, 2048w + 2048) in registers, lane l the
+// eight 4-position groups 2048w + 256g + 4l (g = 0..7), so that a wave's
+// positions in (g, lane, i) order are in index order.  Wave 0 alone locates
+// the threshold bin in the histogram the scoring kernel built, and later the
+// radix digits; the bin's keys are compacted into LDS with ballots, the exact
+// k-th key is radix-selected among them (bits 19..9, then 8..0), ties at that
+// key are ranked by position, and the chosen positions are staged in LDS in
+// index order and written out coalesced.  The kernel runs once per row, so
+// its time is set by latency: it avoids block-wide scans on the common path
+// (one barrier per phase, wave-level ballot and DPP scans otherwise).
+constexpr int kRowThreads = 1024;
+constexpr int kRowLength = 32768;
+constexpr int kRowGroups = 8;      // 4-position groups per lane
+constexpr int kRowMaxK = 4096;
+constexpr int kRowCand = 4096;     // threshold-bin keys compacted into LDS
+constexpr int kRowDigits1 = 2048;  // bits 19..9
+constexpr int kRowDigits2 = 512;   // bits 8..0
 
 __global__ __launch_bounds__(kRowThreads) void select_row_kernel(SelectArgs a) {
   __shared__ uint32_t cand[kRowCand];       // bin keys (low 20 bits), then staged positions
@@ -592,7 +628,7 @@ __global__ __launch_bounds__(kRowThreads) void select_row_kernel(SelectArgs a) {
         wrun += __builtin_amdgcn_readlane(incl, kWave - 1);
       }
       uint32_t all_t;
-      const uint32_t wbase = block_excl_scan(lane == 0 ? wrun : 0u, wsum[0], all_t);
+      const uint32_t wbase = block_excl_scan<kRowWaves>(lane == 0 ? wrun : 0u, wsum[0], all_t);
       const uint32_t first = __builtin_amdgcn_readfirstlane(wbase);
 #pragma unroll
       for (int g = 0; g < kRowGroups; ++g) {
@@ -696,8 +732,11 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
   a.ws = ws;
   a.out_idx = out_idx;
   a.out_val = out_val;
-  if (length <= kRowLength && k <= kRowMaxK) {
-    hipLaunchKernelGGL(select_row_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0, stream, a);
+  // DSA_SELECT_PATH=row selects the one-workgroup-per-row kernel where it
+  // applies (diagnostics and tests); gather + resolve otherwise.
+  const char* forced = getenv("DSA_SELECT_PATH");
+  if (forced && strcmp(forced, "row") == 0 && length <= kRowLength && k <= kRowMaxK) {
+    hipLaunchKernelGGL(select_row_kernel, dim3((unsigned)rows), dim3(1024), 0, stream, a);
     return check_launch("select_row_kernel");
   }
   const dim3 grid((unsigned)(rows * a.chunks));

@@ -23,7 +23,7 @@ struct SelectWorkspace {
 // Carves the workspace out of `base` (base == nullptr only measures it).
 SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length);
 
-// Launches gather + resolve on scores [rows, length] whose histogram is in ws.
+// Selects the top-k of scores [rows, length] whose histogram is in ws.
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,
                   hipStream_t stream);

@@ -17,6 +17,17 @@ from oracle import topk as T
 
 pytestmark = pytest.mark.gpu
 
+# The library picks its selection path itself; DSA_SELECT_PATH forces one so
+# that every path is checked (a forced path that does not apply falls through
+# to the default choice).
+PATHS = ["chunks", "row"]
+
+
+@pytest.fixture(params=PATHS)
+def select_path(request, monkeypatch):
+    monkeypatch.setenv("DSA_SELECT_PATH", request.param)
+    return request.param
+
 
 def inputs(batch, length, seed, hot=0.0, ties=False):
     gen = torch.Generator().manual_seed(seed)
@@ -27,7 +38,9 @@ def inputs(batch, length, seed, hot=0.0, ties=False):
         n = max(1, round(hot * length))
         for b in range(batch):
             k[b, torch.randperm(length, generator=gen)[:n]] *= 4
-    if ties:
+    if ties == "all":
+        k[:] = k[:, :1]  # every score equal: the threshold bin holds the whole row
+    elif ties:
         k[:, ::3] = k[:, :1]  # many identical keys -> identical scores
     return q, w, k.to(torch.bfloat16)
 
@@ -42,10 +55,11 @@ def inputs(batch, length, seed, hot=0.0, ties=False):
         (2, 6001, 500, 0.0, True),
         (2, 1000, 1000, 0.0, False),
         (2, 700, 2048, 0.0, False),
+        (2, 20000, 3000, 0.0, "all"),
     ],
 )
-def test_indexer_topk_matches_stable_topk(device, batch, length, k, hot, ties) -> None:
-    print(f"indexer_topk B={batch} L={length} k={k} hot={hot} ties={ties}", flush=True)
+def test_indexer_topk_matches_stable_topk(device, select_path, batch, length, k, hot, ties) -> None:
+    print(f"indexer_topk path={select_path} B={batch} L={length} k={k} hot={hot} ties={ties}", flush=True)
     q, w, keys = inputs(batch, length, seed=length + k, hot=hot, ties=ties)
     idx, scores, vals = decode.indexer_topk(q.to(device), w.to(device), keys.to(device), k, return_scores=True, return_values=True)
     idx = idx.cpu().numpy()
@@ -62,15 +76,17 @@ def test_indexer_topk_matches_stable_topk(device, batch, length, k, hot, ties) -
         assert np.isneginf(vals[b][~chosen]).all()
 
 
-def test_workspace_is_reused_across_calls_and_shapes(device) -> None:
-    for seed in range(3):
+def test_workspace_is_reused_across_calls_and_paths(device, monkeypatch) -> None:
+    # Alternating paths on one workspace: each leaves the histogram zeroed.
+    for seed in range(6):
+        monkeypatch.setenv("DSA_SELECT_PATH", PATHS[seed % len(PATHS)])
         q, w, keys = inputs(2, 3000, seed=seed)
         idx, scores = decode.indexer_topk(q.to(device), w.to(device), keys.to(device), 300, return_scores=True)
         for b in range(2):
             assert idx[b].cpu().tolist() == T.topk_index_order(scores[b].cpu().numpy(), 300).tolist()
 
 
-def test_fp8_keys(device) -> None:
+def test_fp8_keys(device, select_path) -> None:
     gen = torch.Generator().manual_seed(21)
     batch, length, k = 2, 9000, 512
     q = (torch.randn(batch, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
@@ -102,3 +118,39 @@ def test_recall_against_float64_oracle(device) -> None:
             assert sorted(idx[b].tolist()) == sorted(truth.tolist())
         else:
             assert T.topk_recall(idx[b], truth) >= 0.999
+
+
+def test_graph_replays_match_eager(device) -> None:
+    # The decode step captured in a HIP graph: every replay (with eager work
+    # and synchronisations in between) equals the eager result.
+    from dsa_amd import _lib
+
+    batch, length, k = 4, 32768, 2048
+    q, w, keys = inputs(batch, length, seed=77, hot=0.01)
+    q, w, keys = q.to(device), w.to(device).float(), keys.to(device)
+    eager_idx = decode.indexer_topk(q, w, keys, k)
+    scores = torch.empty(batch, length, device=device)
+    idx = torch.empty(batch, k, device=device, dtype=torch.int64)
+    ws = torch.zeros(int(_lib.query("dsa_score_topk_workspace_bytes", batch, length)), device=device, dtype=torch.uint8)
+
+    def step():
+        _lib.call("dsa_score_topk", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(),
+                  batch, length, k, _lib.DTYPE_BF16, idx.data_ptr(), None, ws.data_ptr(), ws.numel(),
+                  torch.cuda.current_stream().cuda_stream)
+
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for r in range(4):
+        idx.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(idx, eager_idx), f"replay {r}"
+        decode.indexer_topk(q, w, keys, 300)  # unrelated eager work between replays
+        torch.cuda.synchronize()
