@@ -20,17 +20,20 @@ struct KeysB16 {  // bf16 or fp16 rows, 256 B
   static constexpr int kRowBytes = 256;
   static constexpr int kRaw = 4;
   static constexpr bool kScaled = false;
+  // Natural k order: k-step j of lane group g is dims 32j + 8g .. +8, so one
+  // load instruction reads 64 contiguous bytes of each of the tile's 16 rows.
+  static constexpr bool kNaturalK = true;
   __device__ static __forceinline__ void load(const uint8_t* base, int key, int g,
                                               uint4 (&raw)[kRaw]) {
-    const uint4* p = reinterpret_cast<const uint4*>(base + (size_t)key * kRowBytes + g * 64);
+    const uint8_t* row = base + (size_t)key * kRowBytes + g * 16;
 #pragma unroll
-    for (int c = 0; c < kRaw; ++c) raw[c] = p[c];
+    for (int c = 0; c < kRaw; ++c) raw[c] = *reinterpret_cast<const uint4*>(row + 64 * c);
   }
   __device__ static __forceinline__ void load_buf(BufferRsrc rsrc, int key, int g,
                                                   uint4 (&raw)[kRaw]) {
-    const uint32_t off = (uint32_t)key * kRowBytes + g * 64;
+    const uint32_t off = (uint32_t)key * kRowBytes + g * 16;
 #pragma unroll
-    for (int c = 0; c < kRaw; ++c) raw[c] = buffer_load_16(rsrc, off + 16 * c);
+    for (int c = 0; c < kRaw; ++c) raw[c] = buffer_load_16(rsrc, off + 64 * c);
   }
   __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) { return raw[j]; }
 };
@@ -39,6 +42,9 @@ struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
   static constexpr int kRowBytes = 128;
   static constexpr int kRaw = 2;
   static constexpr bool kScaled = true;
+  // Permuted k order: k-step j of lane group g is dims 32g + 8j .. +8; a lane
+  // reads 32 contiguous bytes, and two instructions cover each 128-byte row.
+  static constexpr bool kNaturalK = false;
   __device__ static __forceinline__ void load(const uint8_t* base, int key, int g,
                                               uint4 (&raw)[kRaw]) {
     const uint4* p = reinterpret_cast<const uint4*>(base + (size_t)key * kRowBytes + g * 32);
@@ -78,15 +84,22 @@ __device__ __forceinline__ float tile_contrib(const uint4 (&qa)[M][4], const flo
   return v;
 }
 
+// Element offset of k-step j's 8 dims for lane group g, in the key format's
+// k order (the A and B fragments must use the same one).
+template <bool kNaturalK>
+__device__ __forceinline__ int kstep_dims(int g, int j) {
+  return kNaturalK ? 32 * j + 8 * g : 32 * g + 8 * j;
+}
+
 // A fragments of heads 16m .. 16m+15 for m < M (no gather, no padding).
-template <int M>
+template <int M, bool kNaturalK>
 __device__ __forceinline__ void load_dense_head_tiles(const uint16_t* q, const float* w, int r, int g,
                                                       uint4 (&qa)[M][4], float (&wr)[M][4]) {
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const uint4* row = reinterpret_cast<const uint4*>(q + (16 * m + r) * kHeadDim + 32 * g);
+    const uint16_t* row = q + (16 * m + r) * kHeadDim;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qa[m][j] = row[j];
+    for (int j = 0; j < 4; ++j) qa[m][j] = *reinterpret_cast<const uint4*>(row + kstep_dims<kNaturalK>(g, j));
 #pragma unroll
     for (int i = 0; i < 4; ++i) wr[m][i] = w[16 * m + 4 * g + i];
   }
@@ -94,7 +107,7 @@ __device__ __forceinline__ void load_dense_head_tiles(const uint16_t* q, const f
 
 // Loads the A fragments of M head tiles.  Row slot s of the stacked tiles is
 // head ids[s] (or head s when ids == nullptr) for s < count, else a zero row.
-template <int M>
+template <int M, bool kNaturalK>
 __device__ __forceinline__ void load_head_tiles(const uint16_t* q, const float* w,
                                                 const int32_t* ids, int count, int r, int g,
                                                 uint4 (&qa)[M][4], float (&wr)[M][4]) {
@@ -104,7 +117,7 @@ __device__ __forceinline__ void load_head_tiles(const uint16_t* q, const float* 
     const int head = slot < count ? (ids ? ids[slot] : slot) : -1;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      qa[m][j] = head >= 0 ? *reinterpret_cast<const uint4*>(q + head * kHeadDim + 32 * g + 8 * j)
+      qa[m][j] = head >= 0 ? *reinterpret_cast<const uint4*>(q + head * kHeadDim + kstep_dims<kNaturalK>(g, j))
                            : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -194,35 +207,35 @@ __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], cons
 // The streaming part of dense_scores_kernel: query block into registers, then
 // the two-buffer unit loop.
 template <class Tag, class KF, int M, bool kGather, bool kHist>
-__device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int u_first, int64_t seq,
-                                             int valid, int L, int lane, int r, int g,
+__device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int u_first, int u_stride,
+                                             int64_t seq, int valid, int L, int lane, int r, int g,
                                              BufferRsrc keys, BufferRsrc out, const float* scales,
                                              uint32_t* hist) {
   uint4 qa[M][4];
   float wr[M][4];
   if constexpr (kGather) {
     const int32_t* ids = a.head_ids ? a.head_ids + seq * a.ids_stride : nullptr;
-    load_head_tiles<M>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, ids, a.head_count, r, g, qa,
+    load_head_tiles<M, KF::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, ids, a.head_count, r, g, qa,
                        wr);
   } else {
-    load_dense_head_tiles<M>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa, wr);
+    load_dense_head_tiles<M, KF::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa, wr);
   }
 
   // Two register buffers.  The next unit's loads are always issued before the
   // current unit is computed; past the wave's last unit the prefetch re-reads
   // that last unit (an L2 hit), so no load is conditional and the compiler's
   // vmcnt waits cover exactly the buffer being consumed.
-  const int u_last = u_first + 4 * (count - 1);
+  const int u_last = u_first + u_stride * (count - 1);
   uint4 buf0[4][KF::kRaw];
   uint4 buf1[4][KF::kRaw];
   dense_load_unit<KF>(keys, u_first, r, g, buf0);
   for (int i = 0; i < count; i += 2) {
-    const int u = u_first + 4 * i;
-    dense_load_unit<KF>(keys, min(u + 4, u_last), r, g, buf1);
+    const int u = u_first + u_stride * i;
+    dense_load_unit<KF>(keys, min(u + u_stride, u_last), r, g, buf1);
     dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf0, u, valid, L, lane, g, scales, out, hist);
     if (i + 1 >= count) break;
-    dense_load_unit<KF>(keys, min(u + 8, u_last), r, g, buf0);
-    dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf1, u + 4, valid, L, lane, g, scales, out, hist);
+    dense_load_unit<KF>(keys, min(u + 2 * u_stride, u_last), r, g, buf0);
+    dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf1, u + u_stride, valid, L, lane, g, scales, out, hist);
   }
 }
 
@@ -255,21 +268,24 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
   const BufferRsrc out = make_buffer(out_ptr, (uint32_t)L * 4u);
   const float* scales = KF::kScaled ? a.scales + keyset * a.scale_stride : nullptr;
 
-  // This wave owns units u_first, u_first + 4, ... below u_end; those at or
-  // past u_compute_end lie wholly beyond the causal limit and only get -inf.
+  // The sequence's waves sweep its units together: wave k of the sequence
+  // owns units k, k + W, k + 2W, ... (W = its wave count), so at any time the
+  // GPU reads a few contiguous fronts rather than one stream per workgroup.
+  // Units at or past u_compute_end lie wholly beyond the causal limit and
+  // only get -inf.
   const int n_units = (L + 63) >> 6;
-  const int u_end = min(n_units, (chunk + 1) * a.units_per_wg);
-  const int u_first = chunk * a.units_per_wg + wave;
-  const int u_compute_end = min(u_end, (valid + 63) >> 6);
-  const int count = u_compute_end > u_first ? (u_compute_end - u_first + 3) >> 2 : 0;
-  for (int uu = u_first + 4 * count; uu < u_end; uu += 4)
+  const int u_stride = a.wgs_per_seq * 4;
+  const int u_first = chunk * 4 + wave;
+  const int u_compute_end = min(n_units, (valid + 63) >> 6);
+  const int count = u_compute_end > u_first ? (u_compute_end - u_first + u_stride - 1) / u_stride : 0;
+  for (int uu = u_first + u_stride * count; uu < n_units; uu += u_stride)
     buffer_store_f32(out, (uint32_t)(uu * 64 + lane) * 4, -__builtin_inff());
   if constexpr (kHist) {
     for (int i = threadIdx.x; i < kSelectBins; i += 256) hist[i] = 0;
     __syncthreads();
     if (count > 0)
-      dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, seq, valid, L, lane, r, g, keys, out,
-                                               scales, hist);
+      dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
+                                               out, scales, hist);
     __syncthreads();
     uint32_t* ghist = a.hist + seq * kSelectBins;
     for (int i = threadIdx.x; i < kSelectBins; i += 256) {
@@ -279,8 +295,8 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
     return;
   }
   if (count == 0) return;
-  dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, seq, valid, L, lane, r, g, keys, out,
-                                           scales, hist);
+  dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
+                                           out, scales, hist);
 }
 
 
@@ -388,7 +404,7 @@ __global__ __launch_bounds__(256) void block_kernel(BlockArgs a) {
     }
     uint4 qa[4][4];
     float wr[4][4];
-    load_head_tiles<4>(a.q, a.w, nullptr, kHeads, r, g, qa, wr);
+    load_head_tiles<4, KF::kNaturalK>(a.q, a.w, nullptr, kHeads, r, g, qa, wr);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       uint4 raw[KF::kRaw];
@@ -409,7 +425,7 @@ __global__ __launch_bounds__(256) void block_kernel(BlockArgs a) {
     }
     uint4 qa[1][4];
     float wr[1][4];
-    load_head_tiles<1>(a.q, a.w, a.selected, kVerifierHeads, r, g, qa, wr);
+    load_head_tiles<1, KF::kNaturalK>(a.q, a.w, a.selected, kVerifierHeads, r, g, qa, wr);
     float maximum = neg_inf;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -426,7 +442,7 @@ __global__ __launch_bounds__(256) void block_kernel(BlockArgs a) {
   } else {  // kModeProgressive
     uint4 qs[1][4];
     float ws[1][4];
-    load_head_tiles<1>(a.q, a.w, a.selected, kVerifierHeads, r, g, qs, ws);
+    load_head_tiles<1, KF::kNaturalK>(a.q, a.w, a.selected, kVerifierHeads, r, g, qs, ws);
     uint4 raw[T][KF::kRaw];
     float p[T];
     float maximum = neg_inf;
@@ -443,7 +459,7 @@ __global__ __launch_bounds__(256) void block_kernel(BlockArgs a) {
     if (accept) {
       uint4 qr[4][4];
       float wrr[4][4];
-      load_head_tiles<4>(a.q, a.w, a.remaining, kHeads - kVerifierHeads, r, g, qr, wrr);
+      load_head_tiles<4, KF::kNaturalK>(a.q, a.w, a.remaining, kHeads - kVerifierHeads, r, g, qr, wrr);
 #pragma unroll
       for (int t = 0; t < T; ++t) p[t] += reduce_lane_groups(tile_contrib<Tag, 4, KF>(qr, wrr, raw[t]));
     }
