@@ -14,15 +14,11 @@
 //            radix-select the exact cut among the candidates, derive the
 //            chunk's output offset, write its chosen indices, and clear the
 //            chunk's share of the histogram for the next call.
-// The kernel boundary is the only synchronisation between workgroups.  A
-// one-workgroup-per-row kernel (rows up to 32768, k <= 4096) is kept as an
-// alternative path (DSA_SELECT_PATH=row).
+// The kernel boundary is the only synchronisation between workgroups.
 #include "common.hpp"
 #include "select.hpp"
 #include "status.hpp"
 
-#include <cstdlib>
-#include <cstring>
 
 namespace dsa {
 namespace {
@@ -57,8 +53,6 @@ __device__ __forceinline__ uint32_t logical_block() {
   const uint32_t b = blockIdx.x;
   return (grid % 8u == 0u) ? (b % 8u) * (grid / 8u) + b / 8u : b;
 }
-
-constexpr int kRowWaves = 1024 / kWave;
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (kWave - 1); }
 
@@ -461,244 +455,6 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs 
   }
 }
 
-// Rows of up to 32768 scores with k <= 4096: one 1024-thread workgroup per
-// row.  Wave w holds positions [2048w, 2048w + 2048) in registers, lane l the
-// eight 4-position groups 2048w + 256g + 4l (g = 0..7), so that a wave's
-// positions in (g, lane, i) order are in index order.  Wave 0 alone locates
-// the threshold bin in the histogram the scoring kernel built, and later the
-// radix digits; the bin's keys are compacted into LDS with ballots, the exact
-// k-th key is radix-selected among them (bits 19..9, then 8..0), ties at that
-// key are ranked by position, and the chosen positions are staged in LDS in
-// index order and written out coalesced.  The kernel runs once per row, so
-// its time is set by latency: it avoids block-wide scans on the common path
-// (one barrier per phase, wave-level ballot and DPP scans otherwise).
-constexpr int kRowThreads = 1024;
-constexpr int kRowLength = 32768;
-constexpr int kRowGroups = 8;      // 4-position groups per lane
-constexpr int kRowMaxK = 4096;
-constexpr int kRowCand = 4096;     // threshold-bin keys compacted into LDS
-constexpr int kRowDigits1 = 2048;  // bits 19..9
-constexpr int kRowDigits2 = 512;   // bits 8..0
-
-__global__ __launch_bounds__(kRowThreads) void select_row_kernel(SelectArgs a) {
-  __shared__ uint32_t cand[kRowCand];       // bin keys (low 20 bits), then staged positions
-  __shared__ uint32_t stage_key[kRowMaxK];  // staged keys
-  __shared__ __align__(16) uint32_t hist[kSelectBins];
-  __shared__ __align__(16) uint32_t digits1[kRowDigits1];
-  __shared__ __align__(16) uint32_t digits2[kRowDigits2];
-  __shared__ __align__(16) uint32_t wsum[2][kRowWaves];
-  __shared__ uint32_t s_bin, s_want, s_crowd, s_fill, s_d1, s_cpos;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t lane = lane_id();
-  const uint32_t wave = tid / kWave;
-  const int row = blockIdx.x;
-  const int n = a.length;
-  const uint32_t kk = (uint32_t)a.k;
-
-  // The row's histogram (4 bins per thread) is issued first, then the scores
-  // of this lane's 32 positions.
-  const BufferRsrc hr = make_buffer(a.ws.hist + (size_t)row * kSelectBins, kSelectBins * 4u);
-  const uint4 hv = buffer_load_16(hr, tid * 16u);
-  const uint32_t base = wave * 2048u + 4u * lane;
-  uint4 raw[kRowGroups];
-  {
-    const BufferRsrc rsrc = make_buffer(a.scores + (size_t)row * n, (uint32_t)n * 4u);
-#pragma unroll
-    for (int g = 0; g < kRowGroups; ++g) raw[g] = buffer_load_16(rsrc, (base + 256u * g) * 4u);
-  }
-  for (uint32_t i = tid; i < (uint32_t)kRowDigits1; i += kRowThreads) digits1[i] = 0;
-  if (tid < (uint32_t)kRowDigits2) digits2[tid] = 0;
-  reinterpret_cast<uint4*>(hist)[tid] = hv;
-  // This workgroup is the histogram's only reader: clear it for the next call.
-  buffer_store_16(hr, tid * 16u, make_uint4(0u, 0u, 0u, 0u));
-  __syncthreads();
-  if (wave == 0) {
-    const Locate t = wave_locate<kSelectBins / kWave>(hist, kk, true);
-    if (lane == 0) {
-      s_bin = t.digit;
-      s_want = t.rem;
-      s_crowd = t.count;
-      s_fill = 0;
-    }
-  }
-  uint32_t key[4 * kRowGroups];
-#pragma unroll
-  for (int g = 0; g < kRowGroups; ++g) {
-    const uint32_t w4[4] = {raw[g].x, raw[g].y, raw[g].z, raw[g].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      key[4 * g + i] = (int)(base + 256u * g + i) < n ? float_to_ordered(__uint_as_float(w4[i])) : 0u;
-  }
-  __syncthreads();
-  const uint32_t bin = s_bin;
-  const uint32_t crowd = s_crowd;
-  uint32_t want = s_want;
-
-  // The selection is every key above (ckey, cpos) in (key desc, index asc)
-  // order; with total <= k that is every valid key (key >= 1).
-  uint32_t ckey = 1;
-  uint32_t cpos = 0xffffffffu;
-  if (bin != kNoBin) {
-    uint32_t d1;
-    uint32_t low;
-    uint32_t ties;
-    if (crowd <= (uint32_t)kRowCand) {
-      // Compact the bin's keys (low 20 bits) into LDS.
-      uint32_t wcount = 0;
-#pragma unroll
-      for (int e = 0; e < 4 * kRowGroups; ++e)
-        wcount += __popcll(__ballot(key[e] != 0 && (key[e] >> 20) == bin));
-      uint32_t at = 0;
-      if (lane == 0 && wcount) at = __hip_atomic_fetch_add(&s_fill, wcount, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      at = __builtin_amdgcn_readfirstlane(at);
-#pragma unroll
-      for (int e = 0; e < 4 * kRowGroups; ++e) {
-        const bool in = key[e] != 0 && (key[e] >> 20) == bin;
-        const uint64_t m = __ballot(in);
-        if (in) cand[at + lanes_below(m)] = key[e] & 0xfffffu;
-        at += __popcll(m);
-      }
-      __syncthreads();
-      for (uint32_t i = tid; i < crowd; i += kRowThreads)
-        __hip_atomic_fetch_add(&digits1[cand[i] >> 9], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      __syncthreads();
-      if (wave == 0) {
-        const Locate t = wave_locate<kRowDigits1 / kWave>(digits1, want, false);
-        if (lane == 0) {
-          s_d1 = t.digit;
-          s_want = t.rem;
-        }
-      }
-      __syncthreads();
-      d1 = s_d1;
-      want = s_want;
-      for (uint32_t i = tid; i < crowd; i += kRowThreads) {
-        const uint32_t v = cand[i];
-        if ((v >> 9) == d1)
-          __hip_atomic_fetch_add(&digits2[v & 0x1ffu], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-    } else {
-      // A crowded bin (many equal or near-equal scores): count in place.
-#pragma unroll
-      for (int e = 0; e < 4 * kRowGroups; ++e)
-        if (key[e] != 0 && (key[e] >> 20) == bin)
-          __hip_atomic_fetch_add(&digits1[(key[e] >> 9) & 0x7ffu], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      __syncthreads();
-      if (wave == 0) {
-        const Locate t = wave_locate<kRowDigits1 / kWave>(digits1, want, false);
-        if (lane == 0) {
-          s_d1 = t.digit;
-          s_want = t.rem;
-        }
-      }
-      __syncthreads();
-      d1 = s_d1;
-      want = s_want;
-#pragma unroll
-      for (int e = 0; e < 4 * kRowGroups; ++e)
-        if (key[e] != 0 && (key[e] >> 9) == ((bin << 11) | d1))
-          __hip_atomic_fetch_add(&digits2[key[e] & 0x1ffu], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    __syncthreads();
-    if (wave == 0) {
-      const Locate t = wave_locate<kRowDigits2 / kWave>(digits2, want, false);
-      if (lane == 0) {
-        s_d1 = t.digit;
-        s_want = t.rem;
-        s_crowd = t.count;
-      }
-    }
-    __syncthreads();
-    low = (d1 << 9) | s_d1;
-    want = s_want;
-    ties = s_crowd;
-    ckey = (bin << 20) | low;
-    if (want < ties) {
-      // Only the first `want` keys equal to ckey (in index order) are chosen:
-      // rank the ties in (wave, g, lane, i) order, which is index order.
-      uint32_t wrun = 0;
-      uint32_t off[kRowGroups];
-#pragma unroll
-      for (int g = 0; g < kRowGroups; ++g) {
-        uint32_t t = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) t += key[4 * g + i] == ckey ? 1u : 0u;
-        const uint32_t incl = wave_incl_scan(t);
-        off[g] = wrun + incl - t;
-        wrun += __builtin_amdgcn_readlane(incl, kWave - 1);
-      }
-      uint32_t all_t;
-      const uint32_t wbase = block_excl_scan<kRowWaves>(lane == 0 ? wrun : 0u, wsum[0], all_t);
-      const uint32_t first = __builtin_amdgcn_readfirstlane(wbase);
-#pragma unroll
-      for (int g = 0; g < kRowGroups; ++g) {
-        uint32_t r = first + off[g];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool tie = key[4 * g + i] == ckey;
-          if (tie && r + 1 == want) s_cpos = base + 256u * g + i;
-          r += tie ? 1u : 0u;
-        }
-      }
-      __syncthreads();
-      cpos = s_cpos;
-    }
-  }
-
-  // Chosen positions in index order: per-wave offsets from DPP scans, wave
-  // bases from one exchange, staged in LDS, then written out coalesced.
-  uint32_t wrun = 0;
-  uint32_t off[kRowGroups];
-#pragma unroll
-  for (int g = 0; g < kRowGroups; ++g) {
-    uint32_t t = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v = key[4 * g + i];
-      t += (v > ckey || (v == ckey && base + 256u * g + i <= cpos)) ? 1u : 0u;
-    }
-    const uint32_t incl = wave_incl_scan(t);
-    off[g] = wrun + incl - t;
-    wrun += __builtin_amdgcn_readlane(incl, kWave - 1);
-  }
-  if (lane == 0) wsum[1][wave] = wrun;
-  __syncthreads();
-  uint32_t wbase = 0;
-  uint32_t sel_total = 0;
-#pragma unroll
-  for (int q = 0; q < kRowWaves / 4; ++q) {
-    const uint4 s4 = reinterpret_cast<const uint4*>(wsum[1])[q];
-    const uint32_t sv[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      wbase += (uint32_t)(4 * q + j) < wave ? sv[j] : 0u;
-      sel_total += sv[j];
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < kRowGroups; ++g) {
-    uint32_t slot = wbase + off[g];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v = key[4 * g + i];
-      const uint32_t p = base + 256u * g + i;
-      if (v > ckey || (v == ckey && p <= cpos)) {
-        cand[slot] = p;
-        stage_key[slot] = v;
-        ++slot;
-      }
-    }
-  }
-  __syncthreads();
-  int64_t* oidx = a.out_idx + (size_t)row * kk;
-  float* oval = a.out_val ? a.out_val + (size_t)row * kk : nullptr;
-  for (uint32_t i = tid; i < kk; i += kRowThreads) {
-    const bool live = i < sel_total;
-    oidx[i] = live ? (int64_t)cand[i] : int64_t(-1);
-    if (oval) oval[i] = live ? ordered_to_float(stage_key[i]) : -__builtin_inff();
-  }
-}
-
 }  // namespace
 
 SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length) {
@@ -732,13 +488,6 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
   a.ws = ws;
   a.out_idx = out_idx;
   a.out_val = out_val;
-  // DSA_SELECT_PATH=row selects the one-workgroup-per-row kernel where it
-  // applies (diagnostics and tests); gather + resolve otherwise.
-  const char* forced = getenv("DSA_SELECT_PATH");
-  if (forced && strcmp(forced, "row") == 0 && length <= kRowLength && k <= kRowMaxK) {
-    hipLaunchKernelGGL(select_row_kernel, dim3((unsigned)rows), dim3(1024), 0, stream, a);
-    return check_launch("select_row_kernel");
-  }
   const dim3 grid((unsigned)(rows * a.chunks));
   hipLaunchKernelGGL(select_gather_kernel, grid, dim3(kSelThreads), 0, stream, a);
   if (int st = check_launch("select_gather_kernel")) return st;

@@ -195,18 +195,19 @@ int dsa_topk_long(const float* scores, int64_t rows, int64_t length, int64_t k, 
  *               aligned, zero-filled before its first use; every call leaves
  *               it ready for the next one.  Calls that share a workspace must
  *               be ordered (same stream); length <= 524288.
- * Two launches for rows of up to 32768 keys with k <= 4096: scoring (+ a
- * per-row 4096-bin score histogram) over the whole GPU, then one workgroup
- * per row that finds the exact cut from the histogram.  Longer rows or larger
- * k take a candidate-gather and an exact-resolve launch instead of the
- * second one.
+ * Three launches, each over the whole GPU: scoring (+ a per-row 4096-bin
+ * score histogram), candidate gather (the bin holding the k-th score, per
+ * 2048-key chunk), and exact resolve (the cut, the output offsets and the
+ * indices).
  * ------------------------------------------------------------------------ */
 int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length);
 
 /* The two halves of dsa_score_topk, for callers that time or overlap them:
  * dsa_score_hist writes the scores and the per-row score histogram into the
  * workspace; dsa_select_topk turns scores + histogram into the top-k and
- * leaves the workspace ready for the next dsa_score_hist. */
+ * leaves the workspace ready for the next dsa_score_hist.  Every
+ * dsa_score_hist on a workspace must be followed by a dsa_select_topk on it
+ * (same batch and length) before the next dsa_score_hist. */
 int dsa_score_hist(const void* queries, const float* weights, const void* keys,
                    const float* key_scales, float* scores, int64_t batch, int64_t length,
                    int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);

@@ -17,16 +17,6 @@ from oracle import topk as T
 
 pytestmark = pytest.mark.gpu
 
-# The library picks its selection path itself; DSA_SELECT_PATH forces one so
-# that every path is checked (a forced path that does not apply falls through
-# to the default choice).
-PATHS = ["chunks", "row"]
-
-
-@pytest.fixture(params=PATHS)
-def select_path(request, monkeypatch):
-    monkeypatch.setenv("DSA_SELECT_PATH", request.param)
-    return request.param
 
 
 def inputs(batch, length, seed, hot=0.0, ties=False):
@@ -58,8 +48,8 @@ def inputs(batch, length, seed, hot=0.0, ties=False):
         (2, 20000, 3000, 0.0, "all"),
     ],
 )
-def test_indexer_topk_matches_stable_topk(device, select_path, batch, length, k, hot, ties) -> None:
-    print(f"indexer_topk path={select_path} B={batch} L={length} k={k} hot={hot} ties={ties}", flush=True)
+def test_indexer_topk_matches_stable_topk(device, batch, length, k, hot, ties) -> None:
+    print(f"indexer_topk B={batch} L={length} k={k} hot={hot} ties={ties}", flush=True)
     q, w, keys = inputs(batch, length, seed=length + k, hot=hot, ties=ties)
     idx, scores, vals = decode.indexer_topk(q.to(device), w.to(device), keys.to(device), k, return_scores=True, return_values=True)
     idx = idx.cpu().numpy()
@@ -76,17 +66,17 @@ def test_indexer_topk_matches_stable_topk(device, select_path, batch, length, k,
         assert np.isneginf(vals[b][~chosen]).all()
 
 
-def test_workspace_is_reused_across_calls_and_paths(device, monkeypatch) -> None:
-    # Alternating paths on one workspace: each leaves the histogram zeroed.
+def test_workspace_is_reused_across_calls(device) -> None:
+    # One workspace, many calls: each leaves the histogram and the scoring
+    # sweep's unit counters ready for the next.
     for seed in range(6):
-        monkeypatch.setenv("DSA_SELECT_PATH", PATHS[seed % len(PATHS)])
         q, w, keys = inputs(2, 3000, seed=seed)
         idx, scores = decode.indexer_topk(q.to(device), w.to(device), keys.to(device), 300, return_scores=True)
         for b in range(2):
             assert idx[b].cpu().tolist() == T.topk_index_order(scores[b].cpu().numpy(), 300).tolist()
 
 
-def test_fp8_keys(device, select_path) -> None:
+def test_fp8_keys(device) -> None:
     gen = torch.Generator().manual_seed(21)
     batch, length, k = 2, 9000, 512
     q = (torch.randn(batch, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
