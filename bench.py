@@ -191,6 +191,12 @@ def main() -> None:
     score_bytes = keys_per_step * (256 + 4) + BATCH * (64 * 128 * 2 + 64 * 4)
     score_avg_ms = sum(score_ms) / len(score_ms)
     achieved = score_bytes / (score_avg_ms / 1e3) / 1e9
+    # HBM bytes per launch of the scoring kernel, from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel of known size).
+    traffic = None
+    traffic_file = ROOT / "profiles" / "dense_scores_c2_traffic.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("traffic_bytes")
     # Whole-step algorithmic bytes (keys + q + w + K index/score outputs).
     step_bytes = keys_per_step * 256 + BATCH * (64 * 128 * 2 + 64 * 4) + BATCH * TOPK * (4 + 4)
 
@@ -229,7 +235,7 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "dense_scores_kernel<bf16, M=4, hist>",
             "kernel_avg_us": round(score_avg_ms * 1e3, 3),
             "algorithmic_bytes": score_bytes,
