@@ -54,10 +54,15 @@ _SIGNATURES: dict[str, list] = {
     "dsa_block_max": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "dsa_block_key_norms": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p],
     "dsa_temporal_score_radius": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "dsa_temporal_step": [
+        _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p,
+        _i64, _p,
+    ],
 }
 _RESTYPES: dict[str, object] = {
     "dsa_topk_long_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "dsa_score_topk_workspace_bytes": (_i64, [_i64, _i64]),
+    "dsa_temporal_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,164 @@
+"""Temporal pruning of a decode step on the GPU (seeded, bounded block scan).
+
+The reference evaluates temporal pruning offline: ``replay_transition``
+(reference replay.py:225-400) replays a score trace through the filter of
+replay.py:172-222.  ``temporal_step`` runs the same filter as a real decode
+step: the previous step's top-k keys are scored first, every key block whose
+bound ``previous block max + gamma`` falls below the running threshold is
+skipped without loading its keys, and the top-k is taken over the keys that
+were scored.  Methods follow the reference's names:
+
+- ``static``: threshold fixed at the seeds' minimum, address order;
+- ``static_hot_first``: the same decisions, visiting the seeds' blocks first;
+- ``dynamic``: the threshold is refreshed to the k-th largest evaluated score
+  after every ``wave`` blocks of the scan (``wave=1`` is the reference's
+  per-block refresh; a GPU processes a wave of blocks per launch).
+
+``gamma`` is an absolute margin (the reference's calibrated margins,
+replay.py:562-590): a live step cannot use the current step's score drift.
+"""
+
+from __future__ import annotations
+
+import math
+import threading
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .progressive_kernel import HEAD_DIM, HEADS
+
+BLOCK_SIZES = (16, 32, 64, 128)
+SCAN_ORDERS = {"address": 0, "previous_hot": 1, "upper_hot": 2}
+METHODS = ("static", "static_hot_first", "dynamic")
+
+_workspaces: dict[tuple, torch.Tensor] = {}
+_lock = threading.Lock()
+
+
+@dataclass
+class TemporalStep:
+    """Outcome of one pruned step (per sequence of the batch)."""
+
+    topk: torch.Tensor  # int64 [B, k], ascending index order
+    scores: torch.Tensor  # fp32 [B, L], -inf for keys that were not scored
+    evaluated_blocks: torch.Tensor  # bool [B, ceil(L / block_size)]
+    qk_scored: torch.Tensor  # int32 [B]
+
+
+def _workspace(device, stream, batch, length, k, block_size) -> torch.Tensor:
+    key = (device.index, stream, batch, length, k, block_size)
+    with _lock:
+        ws = _workspaces.get(key)
+        if ws is None:
+            need = int(_lib.query("dsa_temporal_workspace_bytes", batch, length, k, block_size))
+            ws = torch.empty(need, device=device, dtype=torch.uint8)
+            _workspaces[key] = ws
+        return ws
+
+
+def temporal_step(
+    queries: torch.Tensor,
+    weights: torch.Tensor,
+    keys: torch.Tensor,
+    previous_block_max: torch.Tensor,
+    previous_length: int,
+    previous_topk: torch.Tensor,
+    gamma,
+    *,
+    block_size: int = 64,
+    method: str = "dynamic",
+    scan_order: str = "previous_hot",
+    wave: int = 32,
+    key_scales: torch.Tensor | None = None,
+) -> TemporalStep:
+    """One pruned decode step for ``B`` sequences.
+
+    queries ``[B, 64, 128]``, weights ``[B, 64]``, keys ``[B, L, 128]`` (the
+    query dtype, or fp8 e4m3fn with ``key_scales`` ``[B, ceil(L/128)]``),
+    ``previous_block_max`` ``[B, ceil(previous_length / block_size)]``,
+    ``previous_topk`` ``[B, k]`` (distinct indices below ``previous_length``),
+    ``gamma`` a float or ``[B]`` tensor.
+    """
+
+    _lib.load()
+    if queries.ndim != 3 or queries.shape[1:] != (HEADS, HEAD_DIM):
+        raise ValueError("queries must be [batch,64,128]")
+    batch = queries.shape[0]
+    if weights.shape != (batch, HEADS):
+        raise ValueError("weights must be [batch,64]")
+    if keys.ndim != 3 or keys.shape[0] != batch or keys.shape[2] != HEAD_DIM:
+        raise ValueError("keys must be [batch,L,128]")
+    if not (queries.is_cuda and weights.is_cuda and keys.is_cuda):
+        raise ValueError("HIP kernels require GPU tensors")
+    if block_size not in BLOCK_SIZES:
+        raise ValueError(f"block_size must be one of {BLOCK_SIZES}")
+    if method not in METHODS:
+        raise ValueError(f"unknown method: {method}")
+    if method == "static":
+        scan_order, wave = "address", 0
+    elif method == "static_hot_first":
+        scan_order, wave = "previous_hot", 0
+    elif wave < 1:
+        raise ValueError("dynamic pruning needs wave >= 1")
+    if scan_order not in SCAN_ORDERS:
+        raise ValueError(f"unknown scan order: {scan_order}")
+    length = keys.shape[1]
+    if not 0 < previous_length <= length:
+        raise ValueError("expected previous length <= current length")
+    prev_blocks = math.ceil(previous_length / block_size)
+    if previous_block_max.shape != (batch, prev_blocks):
+        raise ValueError(f"previous_block_max must be [batch,{prev_blocks}]")
+    if previous_topk.ndim != 2 or previous_topk.shape[0] != batch:
+        raise ValueError("previous_topk must be [batch,k]")
+    k = previous_topk.shape[1]
+    if not 0 < k <= previous_length:
+        raise ValueError("k must fit the previous step so it can seed the scan")
+    if keys.dtype == torch.float8_e4m3fn:
+        if queries.dtype != torch.bfloat16:
+            raise ValueError("fp8 keys are scored against BF16 queries")
+        if key_scales is None or key_scales.shape != (batch, math.ceil(length / 128)):
+            raise ValueError("fp8 keys need key_scales [batch, ceil(L/128)]")
+        key_scales = key_scales.to(device=keys.device, dtype=torch.float32).contiguous()
+    elif queries.dtype not in (torch.float16, torch.bfloat16) or keys.dtype != queries.dtype:
+        raise ValueError("queries and keys must share FP16/BF16 dtype")
+    device = keys.device
+    gamma_t = torch.as_tensor(gamma, dtype=torch.float32, device=device).reshape(-1)
+    if gamma_t.numel() == 1:
+        gamma_t = gamma_t.expand(batch)
+    if gamma_t.numel() != batch:
+        raise ValueError("gamma must be a float or one value per sequence")
+    queries = queries.contiguous()
+    keys = keys.contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    prev_max = previous_block_max.to(device=device, dtype=torch.float32).contiguous()
+    seeds = previous_topk.to(device=device, dtype=torch.int64).contiguous()
+    gamma_t = gamma_t.contiguous()
+    stream = _lib.stream_of(keys)
+    blocks = math.ceil(length / block_size)
+    scores = torch.empty((batch, length), device=device, dtype=torch.float32)
+    evaluated = torch.empty((batch, blocks), device=device, dtype=torch.uint8)
+    topk = torch.empty((batch, k), device=device, dtype=torch.int64)
+    qk = torch.empty(batch, device=device, dtype=torch.int32)
+    ws = _workspace(device, stream, batch, length, k, block_size)
+    _lib.call(
+        "dsa_temporal_step", _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(key_scales),
+        _lib.ptr(prev_max), previous_length, _lib.ptr(seeds), _lib.ptr(gamma_t), _lib.ptr(scores),
+        _lib.ptr(evaluated), _lib.ptr(topk), _lib.ptr(qk), batch, length, k, block_size,
+        SCAN_ORDERS[scan_order], wave, _lib.dtype_code(keys.dtype), _lib.ptr(ws), ws.numel(), stream,
+    )
+    return TemporalStep(topk, scores, evaluated.bool(), qk)
+
+
+def block_max(scores: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Per-block maxima ``[B, ceil(L / block_size)]`` of GPU score rows
+    (reference replay.py:149-150)."""
+
+    if not scores.is_cuda or scores.ndim != 2:
+        raise ValueError("block_max expects GPU score rows [B, L]")
+    scores = scores.to(torch.float32).contiguous()
+    rows, length = scores.shape
+    out = torch.empty((rows, math.ceil(length / block_size)), device=scores.device, dtype=torch.float32)
+    _lib.call("dsa_block_max", _lib.ptr(scores), rows, length, length, block_size, _lib.ptr(out), _lib.stream_of(scores))
+    return out

@@ -221,6 +221,42 @@ int dsa_score_topk(const void* queries, const float* weights, const void* keys,
                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Temporal pruning of one decode step (seeded, bounded block scan).
+ * Device counterpart of the reference's replay filter: replay.py:172-222
+ * (_run_filter) and replay.py:225-400 (replay_transition with a calibrated
+ * absolute margin, methods static / static_hot_first / dynamic).
+ *
+ *   prev_block_max [batch, ceil(prev_length / block_size)] fp32: block maxima
+ *               of the previous step's scores (dsa_block_max)
+ *   prev_topk   [batch, k] int64: the previous step's top-k (the seeds),
+ *               distinct, < prev_length
+ *   gamma       [batch] fp32: absolute margin; U_b = prev max + gamma, and
+ *               blocks holding keys past prev_length are never pruned
+ *   scan_order  0 address, 1 previous-hot (blocks of the seeds first, then
+ *               larger U, then address), 2 larger U then address
+ *   wave        0: threshold fixed at the seed minimum (static); W > 0: the
+ *               threshold becomes the k-th largest evaluated score after
+ *               every W blocks of the scan (W = 1 is the reference's dynamic
+ *               filter).  k + wave * block_size <= 8192.
+ *   scores      [batch, length] fp32 out: evaluated keys' scores, else -inf
+ *   evaluated_blocks [batch, ceil(length / block_size)] bytes out: 1 = kept
+ *   out_topk    [batch, k] int64 out: stable top-k of the evaluated keys, in
+ *               ascending index order
+ *   qk_scored   [batch] int32 out: keys scored (seeds + kept blocks, once each)
+ *   length <= 32768, block_size in {16, 32, 64, 128}, k <= 4096; keys as in
+ *   dsa_full_scores (bf16/fp16, or fp8 with key_scales).
+ * Pruned blocks load no key bytes.  A step costs 3 + 2 * ceil(blocks / W)
+ * launches (3 when static).
+ * ------------------------------------------------------------------------ */
+int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, int64_t k, int32_t block_size);
+int dsa_temporal_step(const void* queries, const float* weights, const void* keys, const float* key_scales,
+                      const float* prev_block_max, int64_t prev_length, const int64_t* prev_topk,
+                      const float* gamma, float* scores, uint8_t* evaluated_blocks, int64_t* out_topk,
+                      int32_t* qk_scored, int64_t batch, int64_t length, int64_t k, int32_t block_size,
+                      int32_t scan_order, int32_t wave, int32_t key_dtype, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Per-block maxima of score rows (replay.py:149-150 _block_max,
  * approx.py:53-55): out[r, b] = max(scores[r, b*bs : min(len, (b+1)*bs)]).
  * block_size is any positive value.

@@ -1,0 +1,129 @@
+"""GPU temporal pruning step against the oracle's replay filter.
+
+For one decode transition (previous step -> current step with a few appended
+keys and an AR(1) query drift), the GPU step's decisions must equal the
+oracle's ``run_filter`` (reference replay.py:172-222, with the ``wave``
+refresh schedule) fed the same inputs: the dense GPU scores of the current
+step, the previous step's block maxima and top-k, the absolute margin and the
+scan order.  Kept blocks and the number of keys scored must match exactly;
+evaluated keys carry the dense scores bit for bit; the top-k is the stable
+top-k over the evaluated keys.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_amd import decode, temporal
+from oracle import replay as R
+from oracle import topk as T
+
+pytestmark = pytest.mark.gpu
+
+
+def transition(batch, prev_length, length, seed, hot=0.01, rho=0.95):
+    gen = torch.Generator().manual_seed(seed)
+    q_prev = torch.randn(batch, 64, 128, generator=gen) / math.sqrt(128)
+    q_cur = rho * q_prev + math.sqrt(1 - rho * rho) * torch.randn(batch, 64, 128, generator=gen) / math.sqrt(128)
+    w = torch.randn(batch, 64, generator=gen) / 8
+    keys = torch.randn(batch, length, 128, generator=gen)
+    n_hot = max(1, round(hot * length))
+    for b in range(batch):
+        keys[b, torch.randperm(length, generator=gen)[:n_hot]] *= 4
+    return q_prev.to(torch.bfloat16), q_cur.to(torch.bfloat16), w, keys.to(torch.bfloat16)
+
+
+CASES = [
+    # block, method, scan order, wave, prev length, length, k
+    (16, "dynamic", "previous_hot", 64, 3000, 3003, 128),
+    (32, "dynamic", "upper_hot", 16, 3000, 3003, 128),
+    (64, "static", "address", 0, 4096, 4100, 256),
+    (64, "static_hot_first", "previous_hot", 0, 4096, 4100, 256),
+    (64, "dynamic", "previous_hot", 1, 2048, 2048, 128),
+    (64, "dynamic", "previous_hot", 32, 16384, 16385, 2048),
+    (128, "dynamic", "address", 8, 5000, 5001, 300),
+]
+
+
+@pytest.mark.parametrize("block,method,order,wave,prev_length,length,k", CASES)
+def test_temporal_step_matches_replay_filter(device, block, method, order, wave, prev_length, length, k) -> None:
+    print(f"temporal bs={block} {method}/{order} wave={wave} L={prev_length}->{length} k={k}", flush=True)
+    batch = 3
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=block * 7 + length)
+    q_prev, q_cur, w, keys = q_prev.to(device), q_cur.to(device), w.to(device), keys.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys[:, :prev_length].contiguous(), k, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys, k, return_scores=True)[1].cpu().numpy()
+    spread = float(prev_scores.std())
+    gamma = torch.full((batch,), 0.15 * spread, device=device)
+    step = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                  method=method, scan_order=order, wave=max(wave, 1))
+    got_scores = step.scores.cpu().numpy()
+    got_kept = step.evaluated_blocks.cpu().numpy()
+    got_qk = step.qk_scored.cpu().numpy()
+    got_topk = step.topk.cpu().numpy()
+    prev_max_h = prev_max.cpu().double().numpy()
+    seeds = prev_topk.cpu().numpy()
+    schedule, dynamic, _ = R.method_schedule(method, order)
+    blocks = math.ceil(length / block)
+    pruned_any = False
+    for b in range(batch):
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max_h.shape[1]] = prev_max_h[b]
+        upper = R.upper_bounds(previous_max, float(gamma[b]), prev_length, length, block)
+        hot = np.zeros(blocks, dtype=bool)
+        hot[seeds[b] // block] = True
+        scan = R.block_scan_order(schedule, upper, R.block_maxima(dense[b], block), hot)
+        current = dense[b].astype(np.float64)
+        tau_seed = float(current[seeds[b]].min())
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=dynamic, fixed_threshold=tau_seed,
+                             wave=wave if dynamic else 1)
+        np.testing.assert_array_equal(got_kept[b], trace.kept, err_msg=f"row {b}: kept blocks")
+        assert int(got_qk[b]) == trace.scored, (b, int(got_qk[b]), trace.scored)
+        ev = trace.evaluated
+        np.testing.assert_array_equal(got_scores[b][ev], dense[b][ev])
+        assert np.isneginf(got_scores[b][~ev]).all()
+        masked = np.where(ev, dense[b], -np.inf).astype(np.float32)
+        assert got_topk[b].tolist() == T.topk_index_order(masked, k).tolist(), b
+        pruned_any |= not trace.kept.all()
+    if block <= 32:  # small blocks' maxima sit near the cut: these cases must prune
+        assert pruned_any, "the margin pruned nothing: the case does not exercise pruning"
+
+
+def test_temporal_step_fp8(device) -> None:
+    print("temporal fp8 keys", flush=True)
+    batch, prev_length, length, k, block = 2, 8192, 8200, 512, 64
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=31)
+    raw = keys.float()
+    blocks128 = math.ceil(length / 128)
+    scales = torch.stack([torch.stack([raw[b, j * 128 : (j + 1) * 128].abs().max() / 448 for j in range(blocks128)]) for b in range(batch)])
+    keys8 = (raw / scales.repeat_interleave(128, dim=1)[:, :length, None]).to(torch.float8_e4m3fn)
+    q_prev, q_cur, w, keys8, scales = q_prev.to(device), q_cur.to(device), w.to(device), keys8.to(device), scales.to(device)
+    prev_scales = scales[:, : math.ceil(prev_length / 128)].contiguous()
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys8[:, :prev_length].contiguous(), k,
+                                                 key_scales=prev_scales, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys8, k, key_scales=scales, return_scores=True)[1].cpu().numpy()
+    gamma = 0.15 * float(prev_scores.std())
+    step = temporal.temporal_step(q_cur, w, keys8, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                  method="dynamic", scan_order="previous_hot", wave=16, key_scales=scales)
+    seeds = prev_topk.cpu().numpy()
+    for b in range(batch):
+        blocks = math.ceil(length / block)
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+        upper = R.upper_bounds(previous_max, float(np.float32(gamma)), prev_length, length, block)
+        hot = np.zeros(blocks, dtype=bool)
+        hot[seeds[b] // block] = True
+        scan = R.block_scan_order("previous_hot", upper, R.block_maxima(dense[b], block), hot)
+        current = dense[b].astype(np.float64)
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=True,
+                             fixed_threshold=float(current[seeds[b]].min()), wave=16)
+        np.testing.assert_array_equal(step.evaluated_blocks[b].cpu().numpy(), trace.kept)
+        assert int(step.qk_scored[b]) == trace.scored
+        ev = trace.evaluated
+        np.testing.assert_array_equal(step.scores[b].cpu().numpy()[ev], dense[b][ev])
