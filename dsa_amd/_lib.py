@@ -55,15 +55,41 @@ _SIGNATURES: dict[str, list] = {
     "dsa_block_key_norms": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p],
     "dsa_temporal_score_radius": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "dsa_temporal_step": [
-        _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p,
-        _i64, _p,
+        _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
+        _p, _i64, _p,
     ],
+    "dsa_approx_step": [
+        _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64,
+        _i32, _i32, _i32, _p, _i64, _p,
+    ],
+    "dsa_approx_init_state": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p],
 }
 _RESTYPES: dict[str, object] = {
     "dsa_topk_long_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "dsa_score_topk_workspace_bytes": (_i64, [_i64, _i64]),
     "dsa_temporal_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
 }
+
+
+
+class ApproxPolicyC(ctypes.Structure):
+    """``dsa_approx_policy`` of include/dsa_amd.h."""
+
+    _fields_ = [
+        ("gamma", ctypes.c_double),
+        ("age_slope", ctypes.c_double),
+        ("ema_alpha", ctypes.c_double),
+        ("volatility_lambda", ctypes.c_double),
+        ("risk_model", _i32),
+        ("order", _i32),
+        ("buckets", _i32),
+        ("cold_streak", _i32),
+        ("age_cap", _i32),
+        ("recent_window", _i32),
+        ("full_refresh", _i32),
+        ("reserved", _i32),
+    ]
+
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -13,6 +13,12 @@
 // (-inf elsewhere), which blocks were kept, the number of keys scored and the
 // stable top-k among the evaluated keys.
 //
+// The same scan runs the own-trajectory policy (approx.py:129-364): per-block
+// metadata kept on the device gives each block a risk (stale block max, or
+// EMA plus volatility, plus gamma and an age slope) that plays the bound's
+// part, some blocks are forced, and after the step the metadata of refreshed
+// blocks is advanced in place while skipped blocks keep stale values.
+//
 // Keys are scored with the tile code of the dense kernel (indexer.hpp), so
 // an evaluated key's score equals the dense score bit for bit, and pruned
 // blocks load no key bytes.
@@ -60,11 +66,24 @@ TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t length, int6
   return ws;
 }
 
+// Own-trajectory policy state (approx.py:42-50), [rows][stride] per field.
+struct ApproxDev {
+  float* last_max;
+  float* ema;
+  float* vol;
+  int16_t* age;
+  int16_t* cold;
+  int64_t stride;
+  const double* gamma_rows;  // per-row gamma, or null for p.gamma
+  dsa_approx_policy p;
+};
+
 struct TemporalArgs {
   const uint16_t* q;      // [rows][64][128]
   const float* w;         // [rows][64]
-  const uint8_t* keys;    // [rows][length] key rows
-  const float* scales;    // fp8: [rows][ceil(length / 128)]
+  const uint8_t* keys;    // [rows][key_stride] key rows (the first length are scored)
+  int64_t key_stride;     // key rows between sequences
+  const float* scales;    // fp8: [rows][ceil(key_stride / 128)]
   const float* prev_max;  // [rows][prev_blocks]
   const int64_t* seeds;   // [rows][k]
   const float* gamma;     // [rows]
@@ -74,79 +93,161 @@ struct TemporalArgs {
   int32_t rows, length, k, block_size, blocks, prev_length, prev_blocks;
   int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper
   int32_t wave_start, wave_len;
+  int32_t policy_mode;    // 0: bound prev_max + gamma (replay filter); 1: own-trajectory policy
+  ApproxDev ap;
   TemporalWorkspace ws;
 };
 
-// Bounds, scan order and a clean slate for one row (one workgroup per row).
-__global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
-  __shared__ uint64_t sort_keys[kMaxTemporalBlocks];
-  __shared__ uint8_t hot[kMaxTemporalBlocks];
+// Order-preserving double -> uint64 map (NaN as -inf, -0.0 as +0.0, so the
+// sort sees the values a float64 sort key would).
+__device__ __forceinline__ uint64_t double_to_ordered(double d) {
+  if (__builtin_isnan(d)) d = -HUGE_VAL;
+  if (d == 0.0) d = 0.0;
+  const uint64_t u = (uint64_t)__double_as_longlong(d);
+  return (u >> 63) ? ~u : (u | (1ull << 63));
+}
+
+// Risk of a block under the policy (approx.py:178-189).  The float32 product
+// volatility_lambda * volatility and the left-to-right float64 sums follow
+// numpy's evaluation of the reference expression.
+__device__ __forceinline__ double policy_risk(const dsa_approx_policy& p, double gamma, float last_max, float ema,
+                                              float vol, int age) {
+#pragma clang fp contract(off)
+  const double aged = p.age_slope * (double)age;
+  if (p.risk_model == DSA_RISK_EMA) {
+    const float spread = (float)p.volatility_lambda * vol;
+    return (((double)ema + (double)spread) + gamma) + aged;
+  }
+  return ((double)last_max + gamma) + aged;
+}
+
+// Sort entries: ascending (lo >> 31, hi, lo & 0x7fffffff).
+__device__ __forceinline__ bool sorts_before(uint64_t hi_a, uint32_t lo_a, uint64_t hi_b, uint32_t lo_b) {
+  if ((lo_a >> 31) != (lo_b >> 31)) return (lo_a >> 31) < (lo_b >> 31);
+  if (hi_a != hi_b) return hi_a < hi_b;
+  return (lo_a & 0x7fffffffu) < (lo_b & 0x7fffffffu);
+}
+
+// Bitonic sort of n (a power of two) entries in LDS by one 1024-thread
+// workgroup.
+__device__ void block_bitonic_sort(uint64_t* hi, uint32_t* lo, int n) {
   const int tid = threadIdx.x;
-  const int row = blockIdx.x;
-  const int L = a.length;
-  const int nb = a.blocks;
-  float* srow = a.scores + (size_t)row * L;
-  for (int i = tid; i < L; i += 1024) srow[i] = -__builtin_inff();
-  const int words = (L + 31) / 32;
-  for (int i = tid; i < words; i += 1024) a.ws.seed_mask[(size_t)row * words + i] = 0;
-  for (int i = tid; i < nb; i += 1024) a.evaluated[(size_t)row * nb + i] = 0;
-  if (tid == 0) a.ws.tau[row] = 0xffffffffu;
-  const int first_new = a.prev_length / a.block_size;
-  const bool grown = a.prev_length < L;
-  const double gamma = (double)a.gamma[row];
-  for (int b = tid; b < nb; b += 1024) {
-    const bool fresh = grown && b >= first_new;
-    const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
-    a.ws.upper[(size_t)row * nb + b] = fresh ? HUGE_VAL : (double)pm + gamma;
-  }
-  if (a.scan_order == 0) {
-    for (int b = tid; b < nb; b += 1024) a.ws.order[(size_t)row * nb + b] = b;
-    return;
-  }
-  for (int b = tid; b < nb; b += 1024) hot[b] = 0;
-  __syncthreads();
-  if (a.scan_order == 1) {
-    for (int i = tid; i < a.k; i += 1024) {
-      const int64_t key = a.seeds[(size_t)row * a.k + i];
-      if (key >= 0 && key < L) hot[min((int)(key / a.block_size), nb - 1)] = 1;
-    }
-  }
-  __syncthreads();
-  // Descending sort of (hot, U, -address).  For a fixed gamma, U orders the
-  // blocks as the previous block maxima do, so the 32-bit ordered key of the
-  // maximum (+inf for blocks with new keys) stands for U.
-  int n = 1;
-  while (n < nb) n <<= 1;
-  for (int b = tid; b < n; b += 1024) {
-    uint64_t key = 0;
-    if (b < nb) {
-      const bool fresh = grown && b >= first_new;
-      const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
-      key = (uint64_t(hot[b]) << 63) | (uint64_t(float_to_ordered(fresh ? __builtin_inff() : pm)) << 31) |
-            (uint64_t)(~(uint32_t)b & 0x7fffffffu);
-    }
-    sort_keys[b] = key;
-  }
-  __syncthreads();
   for (int size = 2; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int i = tid; i < n; i += 1024) {
         const int j = i ^ stride;
         if (j > i) {
-          const uint64_t x = sort_keys[i];
-          const uint64_t y = sort_keys[j];
-          const bool descending = (i & size) == 0;
-          if (descending ? x < y : x > y) {
-            sort_keys[i] = y;
-            sort_keys[j] = x;
+          const bool ascending = (i & size) == 0;
+          const bool swap = ascending ? sorts_before(hi[j], lo[j], hi[i], lo[i])
+                                      : sorts_before(hi[i], lo[i], hi[j], lo[j]);
+          if (swap) {
+            const uint64_t th = hi[i];
+            const uint32_t tl = lo[i];
+            hi[i] = hi[j];
+            lo[i] = lo[j];
+            hi[j] = th;
+            lo[j] = tl;
           }
         }
       }
       __syncthreads();
     }
   }
-  for (int p = tid; p < nb; p += 1024)
-    a.ws.order[(size_t)row * nb + p] = ~(uint32_t)sort_keys[p] & 0x7fffffffu;
+}
+
+// Bounds, scan order and a clean slate for one row (one workgroup per row).
+// Replay filter: U_b = prev max + gamma, +inf for blocks with new keys, order
+// (previous-hot first,) larger U, lower address.  Policy: U_b = risk, or +inf
+// for a forced block, order by risk (approx.py:93-109: address, larger risk
+// then lower address, or buckets of that rank in address order).
+__global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
+  __shared__ uint64_t sort_hi[kMaxTemporalBlocks];
+  __shared__ uint32_t sort_lo[kMaxTemporalBlocks];
+  __shared__ uint8_t hot[kMaxTemporalBlocks];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const int L = a.length;
+  const int nb = a.blocks;
+  const int bs = a.block_size;
+  float* srow = a.scores + (size_t)row * L;
+  for (int i = tid; i < L; i += 1024) srow[i] = -__builtin_inff();
+  const int words = (L + 31) / 32;
+  for (int i = tid; i < words; i += 1024) a.ws.seed_mask[(size_t)row * words + i] = 0;
+  for (int i = tid; i < nb; i += 1024) a.evaluated[(size_t)row * nb + i] = 0;
+  if (tid == 0) a.ws.tau[row] = 0xffffffffu;
+  const int first_new = a.prev_length / bs;
+  const bool grown = a.prev_length < L;
+  const bool policy = a.policy_mode != 0;
+  const bool sorted = policy ? a.ap.p.order != DSA_ORDER_ADDRESS : a.scan_order != 0;
+  const bool hot_first = !policy && a.scan_order == 1;
+  if (hot_first) {
+    for (int b = tid; b < nb; b += 1024) hot[b] = 0;
+    __syncthreads();
+    for (int i = tid; i < a.k; i += 1024) {
+      const int64_t key = a.seeds[(size_t)row * a.k + i];
+      if (key >= 0 && key < L) hot[key / bs] = 1;
+    }
+    __syncthreads();
+  }
+  if (policy) {
+    const dsa_approx_policy& p = a.ap.p;
+    const double gamma = a.ap.gamma_rows ? a.ap.gamma_rows[row] : p.gamma;
+    const int state_blocks = a.prev_blocks;
+    const int recent_first = p.recent_window > 0 ? max(0, L - p.recent_window) / bs : nb;
+    for (int b = tid; b < nb; b += 1024) {
+      const size_t at = (size_t)row * a.ap.stride + b;
+      const bool stored = b < state_blocks;
+      const float last = stored ? a.ap.last_max[at] : -__builtin_inff();
+      const float ema = stored ? a.ap.ema[at] : -__builtin_inff();
+      const float vol = stored ? a.ap.vol[at] : 0.f;
+      const int age = stored ? a.ap.age[at] : 0;
+      const int cold = stored ? a.ap.cold[at] : 1;
+      const double risk = policy_risk(p, gamma, last, ema, vol, age);
+      const bool forced = p.full_refresh || (grown && b >= first_new) || b >= recent_first ||
+                          (p.age_cap >= 0 && age >= p.age_cap) || cold < p.cold_streak;
+      a.ws.upper[(size_t)row * nb + b] = forced ? HUGE_VAL : risk;
+      if (sorted) {
+        sort_hi[b] = ~double_to_ordered(risk);
+        sort_lo[b] = (uint32_t)b;
+      }
+    }
+  } else {
+    const double gamma = (double)a.gamma[row];
+    for (int b = tid; b < nb; b += 1024) {
+      const bool fresh = grown && b >= first_new;
+      const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
+      const double upper = fresh ? HUGE_VAL : (double)pm + gamma;
+      a.ws.upper[(size_t)row * nb + b] = upper;
+      if (sorted) {
+        sort_hi[b] = ~double_to_ordered(upper);
+        sort_lo[b] = (hot_first && !hot[b] ? 0x80000000u : 0u) | (uint32_t)b;
+      }
+    }
+  }
+  if (!sorted) {
+    for (int b = tid; b < nb; b += 1024) a.ws.order[(size_t)row * nb + b] = b;
+    return;
+  }
+  int n = 1;
+  while (n < nb) n <<= 1;
+  for (int b = nb + tid; b < n; b += 1024) {  // padding sorts last
+    sort_hi[b] = ~0ull;
+    sort_lo[b] = 0xffffffffu;
+  }
+  __syncthreads();
+  block_bitonic_sort(sort_hi, sort_lo, n);
+  if (policy && a.ap.p.order == DSA_ORDER_BUCKET) {
+    // Rank r in the risk order -> bucket min(N - 1, r * N / nb); then address
+    // order within each bucket.
+    const int64_t buckets = a.ap.p.buckets;
+    for (int r = tid; r < nb; r += 1024) {
+      sort_hi[r] = (uint64_t)min<int64_t>(buckets - 1, (int64_t)r * buckets / nb);
+      sort_lo[r] &= 0x7fffffffu;
+    }
+    __syncthreads();
+    block_bitonic_sort(sort_hi, sort_lo, n);
+  }
+  for (int r = tid; r < nb; r += 1024) a.ws.order[(size_t)row * nb + r] = sort_lo[r] & 0x7fffffffu;
 }
 
 // Scores 64 keys of one row with the dense kernel's unit code: lane (r, g)
@@ -160,7 +261,7 @@ __device__ __forceinline__ float score_unit(const TemporalArgs& a, int row, cons
   float wr[4][4];
   load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads,
                                           r, g, qa, wr);
-  const BufferRsrc keys = make_buffer(a.keys + (size_t)row * a.length * KF::kRowBytes,
+  const BufferRsrc keys = make_buffer(a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
                                       (uint32_t)a.length * KF::kRowBytes);
   uint4 buf[4][KF::kRaw];
 #pragma unroll
@@ -198,7 +299,7 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
     a.ws.run[(size_t)row * a.k + i] = 0;  // below every score
     return;
   }
-  if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.length + 127) / 128) + (key >> 7)];
+  if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
   a.scores[(size_t)row * a.length + key] = v;
   const int words = (a.length + 31) / 32;
   __hip_atomic_fetch_or(a.ws.seed_mask + (size_t)row * words + (key >> 5), 1u << (key & 31), __ATOMIC_RELAXED,
@@ -238,7 +339,7 @@ __global__ __launch_bounds__(256) void temporal_block_kernel(TemporalArgs a) {
     float v = score_unit<Tag, KF>(a, row, tile_key, r, g);
     const int key = u * 64 + lane;
     if (key >= first && key < end) {
-      if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.length + 127) / 128) + (key >> 7)];
+      if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
       a.scores[(size_t)row * a.length + key] = v;
     }
   }
@@ -340,6 +441,80 @@ __global__ __launch_bounds__(256) void temporal_count_kernel(TemporalArgs a) {
   if (tid == 0) a.qk_scored[row] = (int32_t)total;
 }
 
+struct StateArgs {
+  const float* scores;     // [rows][score_stride]
+  int64_t score_stride;
+  const int64_t* topk;     // [rows][k]: the step's top-k (hot blocks)
+  const uint8_t* evaluated;  // [rows][blocks]: refreshed blocks (update only)
+  ApproxDev ap;
+  int32_t length, blocks, block_size, k, state_blocks;
+};
+
+// kInit: initialize_state (approx.py:112-126) from a dense step.  Otherwise
+// the own-mode update after a step (approx.py:253-287): refreshed blocks take
+// the block max of the current scores (all of their keys were scored), EMA
+// and volatility move by ema_alpha (float64, stored as float32; the
+// volatility's second term and sum are float32, as numpy evaluates
+// `float * float32 scalar`), every other block keeps stale values and ages;
+// the cold streak restarts at blocks holding a top-k key.  In place: each
+// thread reads and writes only its own blocks.
+template <bool kInit>
+__global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
+#pragma clang fp contract(off)
+  __shared__ uint8_t hot[kMaxTemporalBlocks];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const int nb = s.blocks;
+  const int bs = s.block_size;
+  for (int b = tid; b < nb; b += 1024) hot[b] = 0;
+  __syncthreads();
+  for (int i = tid; i < s.k; i += 1024) {
+    const int64_t key = s.topk[(size_t)row * s.k + i];
+    if (key >= 0 && key < s.length) hot[key / bs] = 1;
+  }
+  __syncthreads();
+  const float* srow = s.scores + (size_t)row * s.score_stride;
+  const dsa_approx_policy& p = s.ap.p;
+  for (int b = tid; b < nb; b += 1024) {
+    const size_t at = (size_t)row * s.ap.stride + b;
+    const bool refresh = kInit || s.evaluated[(size_t)row * nb + b];
+    float seen = -__builtin_inff();
+    if (refresh) {
+      const int end = min(s.length, (b + 1) * bs);
+      for (int key = b * bs; key < end; ++key) seen = fmaxf(seen, srow[key]);
+    }
+    if constexpr (kInit) {
+      s.ap.last_max[at] = seen;
+      s.ap.ema[at] = seen;
+      s.ap.vol[at] = 0.f;
+      s.ap.age[at] = 0;
+      s.ap.cold[at] = hot[b] ? 0 : 1;
+    } else {
+      const bool stored = b < s.state_blocks;
+      float last = stored ? s.ap.last_max[at] : -__builtin_inff();
+      float ema = stored ? s.ap.ema[at] : -__builtin_inff();
+      float vol = stored ? s.ap.vol[at] : 0.f;
+      int age = min((stored ? (int)s.ap.age[at] : 0) + 1, 32767);
+      const int cold = stored ? (int)s.ap.cold[at] : 1;
+      if (refresh) {
+        const double observed = (double)seen;
+        const double mean = __builtin_isfinite(ema) ? (double)ema : observed;
+        const double alpha = p.ema_alpha;
+        last = seen;
+        ema = (float)(alpha * observed + (1.0 - alpha) * mean);
+        const float carried = (float)(1.0 - alpha) * vol;
+        vol = (float)(alpha * fabs(observed - mean)) + carried;
+        age = 0;
+      }
+      s.ap.last_max[at] = last;
+      s.ap.ema[at] = ema;
+      s.ap.vol[at] = vol;
+      s.ap.age[at] = (int16_t)age;
+      s.ap.cold[at] = (int16_t)(hot[b] ? 0 : min(cold + 1, 32767));
+    }
+  }
+}
+
 template <class Tag, class KF>
 int launch_temporal(TemporalArgs a, int32_t wave, int64_t* out_topk, hipStream_t stream) {
   hipLaunchKernelGGL(temporal_prep_kernel, dim3(a.rows), dim3(1024), 0, stream, a);
@@ -360,7 +535,57 @@ int launch_temporal(TemporalArgs a, int32_t wave, int64_t* out_topk, hipStream_t
   }
   hipLaunchKernelGGL(temporal_count_kernel, dim3(a.rows), dim3(256), 0, stream, a);
   if (int st = check_launch("temporal_count_kernel")) return st;
-  return dsa_topk(a.scores, nullptr, a.rows, a.length, a.length, nullptr, a.k, 0, out_topk, nullptr, stream);
+  if (int st = dsa_topk(a.scores, nullptr, a.rows, a.length, a.length, nullptr, a.k, 0, out_topk, nullptr, stream))
+    return st;
+  if (a.policy_mode == 0) return DSA_STATUS_OK;
+  StateArgs s = {};
+  s.scores = a.scores;
+  s.score_stride = a.length;
+  s.topk = out_topk;
+  s.evaluated = a.evaluated;
+  s.ap = a.ap;
+  s.length = a.length;
+  s.blocks = a.blocks;
+  s.block_size = a.block_size;
+  s.k = a.k;
+  s.state_blocks = a.prev_blocks;
+  hipLaunchKernelGGL(approx_state_kernel<false>, dim3(a.rows), dim3(1024), 0, stream, s);
+  return check_launch("approx_state_kernel");
+}
+
+// Shared argument checks of the two step entry points.
+int check_step(const void* queries, const void* keys, int64_t key_stride, const float* key_scales,
+               int64_t prev_length, int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
+               int32_t key_dtype, const void* workspace) {
+  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
+  DSA_REQUIRE(block_size == 16 || block_size == 32 || block_size == 64 || block_size == 128,
+              "block_size %d not in {16, 32, 64, 128}", block_size);
+  DSA_REQUIRE(length > 0 && length <= 32768, "length %lld outside [1, 32768]", (long long)length);
+  DSA_REQUIRE(key_stride >= length, "key_stride < length");
+  DSA_REQUIRE(prev_length > 0 && prev_length <= length, "prev_length %lld outside [1, length]",
+              (long long)prev_length);
+  DSA_REQUIRE(k > 0 && k <= 4096 && k <= prev_length, "k=%lld must be in [1, min(4096, prev_length)]",
+              (long long)k);
+  DSA_REQUIRE(wave >= 0, "wave must be >= 0");
+  DSA_REQUIRE(k + int64_t(wave) * block_size <= kMaxMerge, "k + wave * block_size exceeds %d", kMaxMerge);
+  DSA_REQUIRE(key_dtype == DSA_DTYPE_BF16 || key_dtype == DSA_DTYPE_F16 || key_dtype == DSA_DTYPE_FP8_E4M3,
+              "the temporal step takes fp16/bf16/fp8 keys (got %d)", key_dtype);
+  DSA_REQUIRE(key_dtype != DSA_DTYPE_FP8_E4M3 || key_scales, "fp8 keys need key_scales");
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(queries) % 16 == 0 && reinterpret_cast<uintptr_t>(keys) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+              "queries, keys (16 B) and workspace (256 B) must be aligned");
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  DSA_REQUIRE(blocks <= kMaxTemporalBlocks, "%lld blocks exceed %d", (long long)blocks, kMaxTemporalBlocks);
+  return DSA_STATUS_OK;
+}
+
+int run_step(TemporalArgs& a, int32_t wave, int32_t key_dtype, int64_t* out_topk, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (key_dtype) {
+    case DSA_DTYPE_BF16: return launch_temporal<Bf16Tag, KeysB16>(a, wave, out_topk, s);
+    case DSA_DTYPE_F16: return launch_temporal<F16Tag, KeysB16>(a, wave, out_topk, s);
+    default: return launch_temporal<Bf16Tag, KeysFP8>(a, wave, out_topk, s);
+  }
 }
 
 }  // namespace
@@ -374,7 +599,8 @@ extern "C" int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, i
 }
 
 extern "C" int dsa_temporal_step(const void* queries, const float* weights, const void* keys,
-                                 const float* key_scales, const float* prev_block_max, int64_t prev_length,
+                                 int64_t key_stride, const float* key_scales, const float* prev_block_max,
+                                 int64_t prev_length,
                                  const int64_t* prev_topk, const float* gamma, float* scores,
                                  uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
                                  int64_t batch, int64_t length, int64_t k, int32_t block_size,
@@ -383,25 +609,11 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
   DSA_REQUIRE(queries && weights && keys && prev_block_max && prev_topk && gamma && scores && evaluated_blocks &&
                   out_topk && qk_scored,
               "null pointer argument");
-  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
-  DSA_REQUIRE(block_size == 16 || block_size == 32 || block_size == 64 || block_size == 128,
-              "block_size %d not in {16, 32, 64, 128}", block_size);
-  DSA_REQUIRE(length > 0 && length <= 32768, "length %lld outside [1, 32768]", (long long)length);
-  DSA_REQUIRE(prev_length > 0 && prev_length <= length, "prev_length %lld outside [1, length]",
-              (long long)prev_length);
-  DSA_REQUIRE(k > 0 && k <= 4096 && k <= prev_length, "k=%lld must be in [1, min(4096, prev_length)]",
-              (long long)k);
+  if (int st = check_step(queries, keys, key_stride, key_scales, prev_length, batch, length, k, block_size, wave,
+                          key_dtype, workspace))
+    return st;
   DSA_REQUIRE(scan_order >= 0 && scan_order <= 2, "scan_order %d not in {0, 1, 2}", scan_order);
-  DSA_REQUIRE(wave >= 0, "wave must be >= 0");
-  DSA_REQUIRE(k + int64_t(wave) * block_size <= kMaxMerge, "k + wave * block_size exceeds %d", kMaxMerge);
-  DSA_REQUIRE(key_dtype == DSA_DTYPE_BF16 || key_dtype == DSA_DTYPE_F16 || key_dtype == DSA_DTYPE_FP8_E4M3,
-              "dsa_temporal_step takes fp16/bf16/fp8 keys (got %d)", key_dtype);
-  DSA_REQUIRE(key_dtype != DSA_DTYPE_FP8_E4M3 || key_scales, "fp8 keys need key_scales");
-  DSA_REQUIRE(reinterpret_cast<uintptr_t>(queries) % 16 == 0 && reinterpret_cast<uintptr_t>(keys) % 16 == 0 &&
-                  reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
-              "queries, keys (16 B) and workspace (256 B) must be aligned");
   const int64_t blocks = (length + block_size - 1) / block_size;
-  DSA_REQUIRE(blocks <= kMaxTemporalBlocks, "%lld blocks exceed %d", (long long)blocks, kMaxTemporalBlocks);
   const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
   if (!workspace || workspace_bytes < ws.bytes)
     return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the temporal step needs %lld workspace bytes", (long long)ws.bytes);
@@ -409,6 +621,7 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
   a.q = static_cast<const uint16_t*>(queries);
   a.w = weights;
   a.keys = static_cast<const uint8_t*>(keys);
+  a.key_stride = key_stride;
   a.scales = key_scales;
   a.prev_max = prev_block_max;
   a.seeds = prev_topk;
@@ -425,10 +638,80 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
   a.prev_blocks = (int32_t)((prev_length + block_size - 1) / block_size);
   a.scan_order = scan_order;
   a.ws = ws;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (key_dtype) {
-    case DSA_DTYPE_BF16: return launch_temporal<Bf16Tag, KeysB16>(a, wave, out_topk, s);
-    case DSA_DTYPE_F16: return launch_temporal<F16Tag, KeysB16>(a, wave, out_topk, s);
-    default: return launch_temporal<Bf16Tag, KeysFP8>(a, wave, out_topk, s);
-  }
+  return run_step(a, wave, key_dtype, out_topk, stream);
+}
+
+extern "C" int dsa_approx_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
+                               const float* key_scales, const dsa_approx_policy* policy, const double* gamma_rows,
+                               int64_t prev_length, const int64_t* prev_topk, float* last_max, float* ema,
+                               float* volatility, int16_t* age, int16_t* cold_streak, int64_t state_stride,
+                               float* scores, uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
+                               int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
+                               int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  DSA_REQUIRE(queries && weights && keys && policy && prev_topk && last_max && ema && volatility && age &&
+                  cold_streak && scores && evaluated_blocks && out_topk && qk_scored,
+              "null pointer argument");
+  if (int st = check_step(queries, keys, key_stride, key_scales, prev_length, batch, length, k, block_size, wave,
+                          key_dtype, workspace))
+    return st;
+  DSA_REQUIRE(policy->risk_model == DSA_RISK_LAST_MAX || policy->risk_model == DSA_RISK_EMA,
+              "risk_model %d unknown", policy->risk_model);
+  DSA_REQUIRE(policy->order >= DSA_ORDER_ADDRESS && policy->order <= DSA_ORDER_BUCKET, "order %d unknown",
+              policy->order);
+  DSA_REQUIRE(policy->order != DSA_ORDER_BUCKET || policy->buckets >= 1, "bucket order needs buckets >= 1");
+  DSA_REQUIRE(policy->recent_window >= 0, "recent_window must be >= 0");
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  DSA_REQUIRE(state_stride >= blocks, "state_stride %lld < %lld blocks", (long long)state_stride, (long long)blocks);
+  const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the approximate step needs %lld workspace bytes",
+                (long long)ws.bytes);
+  TemporalArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.w = weights;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.key_stride = key_stride;
+  a.scales = key_scales;
+  a.seeds = prev_topk;
+  a.scores = scores;
+  a.evaluated = evaluated_blocks;
+  a.qk_scored = qk_scored;
+  a.rows = (int32_t)batch;
+  a.length = (int32_t)length;
+  a.k = (int32_t)k;
+  a.block_size = block_size;
+  a.blocks = (int32_t)blocks;
+  a.prev_length = (int32_t)prev_length;
+  a.prev_blocks = (int32_t)((prev_length + block_size - 1) / block_size);
+  a.policy_mode = 1;
+  a.ap = ApproxDev{last_max, ema, volatility, age, cold_streak, state_stride, gamma_rows, *policy};
+  a.ws = ws;
+  return run_step(a, wave, key_dtype, out_topk, stream);
+}
+
+extern "C" int dsa_approx_init_state(const float* scores, int64_t score_stride, const int64_t* topk,
+                                     float* last_max, float* ema, float* volatility, int16_t* age,
+                                     int16_t* cold_streak, int64_t state_stride, int64_t batch, int64_t length,
+                                     int64_t k, int32_t block_size, void* stream) {
+  DSA_REQUIRE(scores && topk && last_max && ema && volatility && age && cold_streak, "null pointer argument");
+  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
+  DSA_REQUIRE(length > 0 && score_stride >= length, "length %lld / score_stride %lld invalid", (long long)length,
+              (long long)score_stride);
+  DSA_REQUIRE(k > 0 && k <= length, "k=%lld outside [1, length]", (long long)k);
+  DSA_REQUIRE(block_size > 0, "block_size must be positive");
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  DSA_REQUIRE(blocks <= kMaxTemporalBlocks, "%lld blocks exceed %d", (long long)blocks, kMaxTemporalBlocks);
+  DSA_REQUIRE(state_stride >= blocks, "state_stride %lld < %lld blocks", (long long)state_stride, (long long)blocks);
+  StateArgs s = {};
+  s.scores = scores;
+  s.score_stride = score_stride;
+  s.topk = topk;
+  s.ap = ApproxDev{last_max, ema, volatility, age, cold_streak, state_stride, nullptr, {}};
+  s.length = (int32_t)length;
+  s.blocks = (int32_t)blocks;
+  s.block_size = block_size;
+  s.k = (int32_t)k;
+  s.state_blocks = (int32_t)blocks;
+  hipLaunchKernelGGL(approx_state_kernel<true>, dim3(batch), dim3(1024), 0, static_cast<hipStream_t>(stream), s);
+  return check_launch("approx_state_kernel");
 }

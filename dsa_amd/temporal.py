@@ -76,7 +76,9 @@ def temporal_step(
     """One pruned decode step for ``B`` sequences.
 
     queries ``[B, 64, 128]``, weights ``[B, 64]``, keys ``[B, L, 128]`` (the
-    query dtype, or fp8 e4m3fn with ``key_scales`` ``[B, ceil(L/128)]``),
+    query dtype, or fp8 e4m3fn with ``key_scales`` ``[B, ceil(C/128)]`` for a
+    key buffer of capacity C; a view ``cache[:, :L]`` of a ``[B, C, 128]``
+    cache is read in place),
     ``previous_block_max`` ``[B, ceil(previous_length / block_size)]``,
     ``previous_topk`` ``[B, k]`` (distinct indices below ``previous_length``),
     ``gamma`` a float or ``[B]`` tensor.
@@ -115,11 +117,14 @@ def temporal_step(
     k = previous_topk.shape[1]
     if not 0 < k <= previous_length:
         raise ValueError("k must fit the previous step so it can seed the scan")
+    if keys.stride(2) != 1 or keys.stride(1) != HEAD_DIM:
+        keys = keys.contiguous()
+    key_stride = keys.stride(0) // HEAD_DIM
     if keys.dtype == torch.float8_e4m3fn:
         if queries.dtype != torch.bfloat16:
             raise ValueError("fp8 keys are scored against BF16 queries")
-        if key_scales is None or key_scales.shape != (batch, math.ceil(length / 128)):
-            raise ValueError("fp8 keys need key_scales [batch, ceil(L/128)]")
+        if key_scales is None or key_scales.shape != (batch, math.ceil(key_stride / 128)):
+            raise ValueError("fp8 keys need key_scales [batch, ceil(capacity/128)]")
         key_scales = key_scales.to(device=keys.device, dtype=torch.float32).contiguous()
     elif queries.dtype not in (torch.float16, torch.bfloat16) or keys.dtype != queries.dtype:
         raise ValueError("queries and keys must share FP16/BF16 dtype")
@@ -130,7 +135,6 @@ def temporal_step(
     if gamma_t.numel() != batch:
         raise ValueError("gamma must be a float or one value per sequence")
     queries = queries.contiguous()
-    keys = keys.contiguous()
     weights = weights.to(torch.float32).contiguous()
     prev_max = previous_block_max.to(device=device, dtype=torch.float32).contiguous()
     seeds = previous_topk.to(device=device, dtype=torch.int64).contiguous()
@@ -143,7 +147,7 @@ def temporal_step(
     qk = torch.empty(batch, device=device, dtype=torch.int32)
     ws = _workspace(device, stream, batch, length, k, block_size)
     _lib.call(
-        "dsa_temporal_step", _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(key_scales),
+        "dsa_temporal_step", _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), key_stride, _lib.ptr(key_scales),
         _lib.ptr(prev_max), previous_length, _lib.ptr(seeds), _lib.ptr(gamma_t), _lib.ptr(scores),
         _lib.ptr(evaluated), _lib.ptr(topk), _lib.ptr(qk), batch, length, k, block_size,
         SCAN_ORDERS[scan_order], wave, _lib.dtype_code(keys.dtype), _lib.ptr(ws), ws.numel(), stream,

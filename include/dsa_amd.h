@@ -243,18 +243,93 @@ int dsa_score_topk(const void* queries, const float* weights, const void* keys,
  *   out_topk    [batch, k] int64 out: stable top-k of the evaluated keys, in
  *               ascending index order
  *   qk_scored   [batch] int32 out: keys scored (seeds + kept blocks, once each)
+ *   keys        [batch, key_stride, 128]: the first `length` rows of each
+ *               sequence are scored (a KV cache with spare capacity needs no
+ *               copy); fp8 key_scales are [batch, ceil(key_stride / 128)]
  *   length <= 32768, block_size in {16, 32, 64, 128}, k <= 4096; keys as in
  *   dsa_full_scores (bf16/fp16, or fp8 with key_scales).
  * Pruned blocks load no key bytes.  A step costs 3 + 2 * ceil(blocks / W)
  * launches (3 when static).
  * ------------------------------------------------------------------------ */
 int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, int64_t k, int32_t block_size);
-int dsa_temporal_step(const void* queries, const float* weights, const void* keys, const float* key_scales,
-                      const float* prev_block_max, int64_t prev_length, const int64_t* prev_topk,
+int dsa_temporal_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
+                      const float* key_scales, const float* prev_block_max, int64_t prev_length,
+                      const int64_t* prev_topk,
                       const float* gamma, float* scores, uint8_t* evaluated_blocks, int64_t* out_topk,
                       int32_t* qk_scored, int64_t batch, int64_t length, int64_t k, int32_t block_size,
                       int32_t scan_order, int32_t wave, int32_t key_dtype, void* workspace,
                       int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Own-trajectory pruned decode step (approx.py:129-364 replay_step with
+ * history_mode="own"; policy fields approx.py:15-39 ApproxPolicy).
+ *
+ * The per-block metadata of the policy lives on the device, one row per
+ * sequence with a fixed capacity (state_stride blocks):
+ *   last_max, ema, volatility  fp32  [batch, state_stride]
+ *   age, cold_streak           int16 [batch, state_stride]
+ * It describes the first ceil(prev_length / block_size) blocks; blocks past
+ * those are read as the reference's extension (-inf, -inf, 0, 0, 1).
+ *
+ * dsa_approx_step scores the seeds (prev_topk, the previous approximate
+ * top-k), then scans blocks in the policy's order.  A block is forced when
+ * full_refresh is set, it holds keys the previous step did not have, it lies
+ * in the recent window, its age reached age_cap (>= 0), or its cold streak is
+ * below cold_streak.  Any other block is skipped iff
+ *   risk = last_max + gamma + age_slope * age                    (risk_model 0)
+ *   risk = ema + volatility_lambda * volatility + gamma + age_slope * age (1)
+ * is below the threshold in force (float64 arithmetic, as the reference).
+ * wave = 0 keeps the seed threshold (static policy); wave >= 1 refreshes it to
+ * the k-th largest evaluated score after every `wave` blocks of the scan
+ * (wave = 1 is the reference's per-block refresh).
+ * Outputs are those of dsa_temporal_step (out_topk is the approximate top-k in
+ * ascending index order).  On return, the metadata of every block of the
+ * current length has been advanced in place: refreshed blocks take the
+ * current block max (EMA and volatility updated with ema_alpha, age 0),
+ * others keep stale values with age + 1 (saturating at 32767); the cold
+ * streak is 0 for blocks holding an approximate top-k key, else + 1.
+ * gamma_rows (nullable) overrides policy->gamma per sequence.
+ * history_mode="teacher" needs the dense step and is not a device path;
+ * order "oracle_current" reads the current scores and is rejected.
+ * Limits as dsa_temporal_step; state_stride >= ceil(length / block_size).
+ * ------------------------------------------------------------------------ */
+#define DSA_RISK_LAST_MAX 0
+#define DSA_RISK_EMA 1
+#define DSA_ORDER_ADDRESS 0
+#define DSA_ORDER_PREVIOUS_MAX 1 /* also "predicted_risk" */
+#define DSA_ORDER_BUCKET 2
+
+typedef struct dsa_approx_policy {
+  double gamma;
+  double age_slope;
+  double ema_alpha;
+  double volatility_lambda;
+  int32_t risk_model;    /* DSA_RISK_* */
+  int32_t order;         /* DSA_ORDER_* */
+  int32_t buckets;       /* bucket count of DSA_ORDER_BUCKET ("bucket8" -> 8) */
+  int32_t cold_streak;
+  int32_t age_cap;       /* < 0: no cap */
+  int32_t recent_window; /* keys; 0: none */
+  int32_t full_refresh;  /* policy "full", refresh interval or fallback hit */
+  int32_t reserved;
+} dsa_approx_policy;
+
+int dsa_approx_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
+                    const float* key_scales, const dsa_approx_policy* policy, const double* gamma_rows,
+                    int64_t prev_length, const int64_t* prev_topk, float* last_max, float* ema,
+                    float* volatility, int16_t* age, int16_t* cold_streak, int64_t state_stride,
+                    float* scores, uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
+                    int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
+                    int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* initialize_state (approx.py:112-126) from dense score rows [batch, length]
+ * (row stride score_stride) and their top-k (any order): last_max = ema =
+ * block max, volatility = 0, age = 0, cold_streak = 0 for blocks holding a
+ * top-k key, else 1. */
+int dsa_approx_init_state(const float* scores, int64_t score_stride, const int64_t* topk, float* last_max,
+                          float* ema, float* volatility, int16_t* age, int16_t* cold_streak,
+                          int64_t state_stride, int64_t batch, int64_t length, int64_t k, int32_t block_size,
+                          void* stream);
 
 /* ------------------------------------------------------------------------
  * Per-block maxima of score rows (replay.py:149-150 _block_max,

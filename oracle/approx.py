@@ -4,6 +4,13 @@ Reference: approx.py:15-364 (ApproxPolicy, ApproxState, initialize_state,
 replay_step).  Per-block metadata (last max, EMA, volatility, age, cold
 streak) is updated only for blocks that were refreshed, so skipped blocks keep
 stale values and never see the current step's scores.
+
+One extension, as in the replay oracle: ``wave``.  The reference refreshes the
+running top-K threshold after every kept block; with ``wave = W`` the scan
+order is cut into consecutive groups of W blocks, every block of a group is
+skipped or refreshed against the threshold in force at the start of the
+group, and the running top-K takes the group's new keys after it.  ``wave = 1``
+is the reference schedule.
 """
 
 from __future__ import annotations
@@ -140,6 +147,7 @@ def replay_step(
     history_mode: str = "own",
     previous_length: int | None = None,
     fallback_value: float | None = None,
+    wave: int = 1,
 ) -> tuple[ApproxState, dict[str, Any], dict[str, np.ndarray]]:
     """One own-trajectory transition.  Reference: approx.py:129-364."""
 
@@ -194,23 +202,30 @@ def replay_step(
     recent = np.zeros(blocks, dtype=bool)
     if policy.recent_window:
         recent[max(0, length - policy.recent_window) // block_size :] = True
-    for b in order:
-        b = int(b)
-        lo, hi = b * block_size, min(length, (b + 1) * block_size)
-        forced = (
-            full_refresh
-            or new_block[b]
-            or recent[b]
-            or (policy.age_cap is not None and age[b] >= policy.age_cap)
-            or cold[b] < policy.cold_streak
-        )
-        if not forced and risk[b] < threshold:
-            skipped[b] = True
-            continue
-        unseen = lo + np.flatnonzero(~evaluated[lo:hi])
-        evaluated[lo:hi] = True
-        refreshed[b] = True
-        if heap is not None and unseen.size:
+    if wave < 1:
+        raise ValueError("wave must be >= 1")
+    for start in range(0, order.size, wave):
+        fresh_keys = []
+        for b in order[start : start + wave]:
+            b = int(b)
+            lo, hi = b * block_size, min(length, (b + 1) * block_size)
+            forced = (
+                full_refresh
+                or new_block[b]
+                or recent[b]
+                or (policy.age_cap is not None and age[b] >= policy.age_cap)
+                or cold[b] < policy.cold_streak
+            )
+            if not forced and risk[b] < threshold:
+                skipped[b] = True
+                continue
+            unseen = lo + np.flatnonzero(~evaluated[lo:hi])
+            evaluated[lo:hi] = True
+            refreshed[b] = True
+            if unseen.size:
+                fresh_keys.append(unseen)
+        if heap is not None and fresh_keys:
+            unseen = np.concatenate(fresh_keys)
             floor = heap[0][0]
             for key in unseen[scores[unseen] >= floor]:
                 item = (float(scores[key]), -int(key))

@@ -50,3 +50,27 @@ def test_invalid_arguments_are_rejected_without_a_device() -> None:
 def test_call_raises_runtime_error_with_message() -> None:
     with pytest.raises(RuntimeError, match="dsa_topk failed"):
         _lib.call("dsa_topk", None, None, 1, 16, 16, None, 4, 1, None, None, None)
+
+
+def test_approx_policy_struct_matches_the_header() -> None:
+    # four doubles, then eight int32 fields, no padding: 64 bytes
+    assert ctypes.sizeof(_lib.ApproxPolicyC) == 64
+    assert _lib.ApproxPolicyC.risk_model.offset == 32
+    assert _lib.ApproxPolicyC.reserved.offset == 60
+
+
+def test_approx_step_rejects_bad_policies_without_a_device() -> None:
+    lib = _lib.load()
+    fake = ctypes.c_void_p(256)
+    policy = _lib.ApproxPolicyC(ema_alpha=0.9, risk_model=0, order=2, buckets=0, cold_streak=1, age_cap=-1)
+    args = [fake, fake, fake, 4096, None, ctypes.addressof(policy), None, 4096, fake, fake, fake, fake, fake, fake, 64,
+            fake, fake, fake, fake, 2, 4096, 512, 64, 1, 2, fake, 1 << 20, None]
+    assert lib.dsa_approx_step(*args) == 1
+    assert b"bucket" in lib.dsa_last_error()
+    policy.order, policy.risk_model = 1, 5
+    assert lib.dsa_approx_step(*args) == 1
+    assert b"risk_model" in lib.dsa_last_error()
+    policy.risk_model = 1
+    args[14] = 63  # state rows shorter than the 64 blocks of L=4096 at block 64
+    assert lib.dsa_approx_step(*args) == 1
+    assert b"state_stride" in lib.dsa_last_error()

@@ -127,3 +127,32 @@ def test_block_key_norms_closed_form() -> None:
     keys[1, 1] = [1, 0]
     out = block_key_norms(keys, 2)
     assert out.tolist() == [[5.0, 1.0], [10.0, 0.0], [0.0, 0.0]]
+
+
+def test_approx_wave_covering_every_block_is_the_static_policy() -> None:
+    # A threshold refreshed only after the whole scan never prunes anything
+    # the seed threshold would not: the dynamic policy with one wave over all
+    # blocks makes the static policy's decisions in the same order.
+    rng = np.random.default_rng(9)
+    previous = rng.normal(size=600).astype(np.float32)
+    current = (0.9 * np.pad(previous, (0, 3)) + 0.3 * rng.normal(size=603)).astype(np.float32)
+    for order, gamma in (("address", -0.4), ("previous_max", -0.2), ("bucket4", -0.6)):
+        static = ApproxPolicy(name="s", gamma=gamma, order=order, cold_streak=0)
+        dynamic = ApproxPolicy(name="d", gamma=gamma, order=order, cold_streak=0, dynamic_threshold=True)
+        results = []
+        for policy, wave in ((static, 1), (dynamic, 1000)):
+            state = initialize_state(previous, k=32, block_size=16)
+            state, metrics, details = replay_step(state, current, policy=policy, k=32, block_size=16, step=1,
+                                                  previous_length=600, wave=wave)
+            results.append((state, metrics, details))
+        (s0, m0, d0), (s1, m1, d1) = results
+        assert m0["blocks_skipped"] > 0, order
+        np.testing.assert_array_equal(d0["refreshed_blocks"], d1["refreshed_blocks"])
+        assert m0["qk_scored"] == m1["qk_scored"]
+        assert sorted(d0["approximate"].tolist()) == sorted(d1["approximate"].tolist())
+        for field in ("last_max", "ema", "volatility", "age", "cold_streak"):
+            np.testing.assert_array_equal(getattr(s0, field), getattr(s1, field))
+        # and a per-block refresh prunes at least as much as the seed threshold
+        state = initialize_state(previous, k=32, block_size=16)
+        _, m2, _ = replay_step(state, current, policy=dynamic, k=32, block_size=16, step=1, previous_length=600)
+        assert m2["qk_scored"] <= m0["qk_scored"], order
