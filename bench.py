@@ -45,6 +45,13 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--config", choices=("c2", "c3"), default="c2",
+                        help="c2: the headline decode step (default); c3: temporal replay over 256 decode steps")
+    parser.add_argument("--c3-out", default=None, help="c3: also write the per-variant table (JSON) here")
+    parser.add_argument("--c3-blocks", default=",".join(map(str, C3_BLOCKS)), help="c3: block sizes to replay")
+    parser.add_argument("--c3-gamma", default=",".join(map(str, C3_GAMMA_SIGMA)), help="c3: gamma_sigma values")
+    parser.add_argument("--c3-refreshes", type=int, default=32,
+                        help="c3: threshold refreshes per dynamic scan (the reference refreshes after every block)")
     return parser.parse_args()
 
 
@@ -104,6 +111,9 @@ def main() -> None:
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build (the path shards by sequence, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    if args.config == "c3":
+        run_c3(args)
+        return
     import torch
 
     from dsa_amd import _lib, metrics
@@ -253,6 +263,220 @@ def main() -> None:
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)
+
+# --------------------------------------------------------------------------
+# C3: temporal replay over a decode trajectory
+# --------------------------------------------------------------------------
+C3_BATCH = 4
+C3_LENGTH = 16384
+C3_STEPS = 256
+C3_TOPK = 2048
+C3_RHO = 0.95
+C3_BLOCKS = (16, 32, 64, 128)
+C3_GAMMA_SIGMA = (0.0, 0.25, 0.5, 1.0)
+# replay variants (reference replay.py:533-541, without the oracle order)
+C3_REPLAY = (("static", "address"), ("static_hot_first", "previous_hot"), ("dynamic", "address"),
+             ("dynamic", "previous_hot"), ("dynamic", "upper_hot"))
+C3_HEADLINE_RECALL = 0.999  # headline: most bytes skipped among variants at this mean Recall@K or better
+
+
+def c3_wave(blocks: int, block_size: int, refreshes: int) -> int:
+    """Blocks per threshold refresh: about `refreshes` refreshes per scan,
+    within the step's merge limit (k + wave * block_size <= 8192)."""
+
+    return max(1, min(-(-blocks // refreshes), (8192 - C3_TOPK) // block_size))
+
+
+def c3_inputs(device):
+    """B=4 sequences: keys ~ N(0,1) bf16 for the final context, AR(1) queries
+    q_t = rho q_{t-1} + sqrt(1 - rho^2) eps (eps ~ N(0,1)/sqrt(128)), fixed
+    weights ~ N(0, 1/64); seeded CPU generator."""
+
+    import torch
+
+    gen = torch.Generator().manual_seed(SEED)
+    total = C3_LENGTH + C3_STEPS - 1
+    keys = torch.randn(C3_BATCH, total, 128, generator=gen).to(torch.bfloat16).to(device)
+    w = (torch.randn(C3_BATCH, 64, generator=gen) / 8.0).to(device)
+    q = torch.randn(C3_BATCH, 64, 128, generator=gen) / math.sqrt(128)
+    queries = []
+    for _ in range(C3_STEPS):
+        queries.append(q.to(torch.bfloat16).to(device))
+        q = C3_RHO * q + math.sqrt(1 - C3_RHO * C3_RHO) * torch.randn(C3_BATCH, 64, 128, generator=gen) / math.sqrt(128)
+    return keys, w, queries
+
+
+def c3_summary(rows: list[dict]) -> dict:
+    """Aggregates as the reference's replay_trace (replay.py:592-627):
+    medians of reductions, means of recall and exact match."""
+
+    import numpy as np
+
+    col = lambda name: np.asarray([r[name] for r in rows], dtype=np.float64)  # noqa: E731
+    return {
+        "transitions": len(rows),
+        "qk_reduction": float(np.median(col("qk_reduction"))),
+        "qk_reduction_p5": float(np.quantile(col("qk_reduction"), 0.05)),
+        "net_byte_reduction": float(np.median(col("net_byte_reduction"))),
+        "recall": float(np.mean(col("recall"))),
+        "recall_min": float(np.min(col("recall"))),
+        "exact_match": float(np.mean(col("exact_match"))),
+        "false_cold_blocks": int(np.sum(col("false_cold_blocks"))),
+        "us_per_step": float(np.median(col("us"))),
+    }
+
+
+def run_c3(args) -> None:
+    """BASELINE config 3 on one GPU: 256 decode steps of B=4 sequences whose
+    context grows from 16384 keys by one key per step, K=2048.
+
+    Every step is run dense (scores + exact top-k: the truth) and pruned.
+    Replay variants are teacher-forced as the reference's replay_trace
+    (replay.py:476-590): step t's pruned scan is seeded with the dense top-k
+    of step t-1 and bounded by its block maxima + gamma_sigma * sigma_t
+    (sigma_t = std of the score drift over the common keys).  Own-trajectory
+    variants (approx.py:129-364) carry their own device state from step 0 with
+    an absolute gamma fixed at gamma_sigma * sigma_1.  Bytes read per pruned
+    step = keys scored x 256 + blocks x 8 (replay.py:369-371).
+    """
+
+    import numpy as np
+    import torch
+
+    from dsa_amd import _lib, approx, decode, temporal
+
+    _lib.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    keys, w, queries = c3_inputs(device)
+    stream = torch.cuda.current_stream(device)
+    lengths = [C3_LENGTH + t for t in range(C3_STEPS)]
+
+    # Dense trajectory: scores and exact top-k of every step, timed per step.
+    dense_scores, dense_topk, dense_us = [], [], []
+    for t, length in enumerate(lengths):
+        view = keys[:, :length].contiguous()
+        for _ in range(2 if t == 0 else 1):  # the first call warms the workspace
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            top, sc = decode.indexer_topk(queries[t], w, view, C3_TOPK, return_scores=True)
+            e1.record(stream)
+        dense_scores.append(sc)
+        dense_topk.append(top)
+        torch.cuda.synchronize()
+        dense_us.append(e0.elapsed_time(e1) * 1e3)
+        del view
+    sigma = [None] + [
+        (dense_scores[t][:, : lengths[t - 1]] - dense_scores[t - 1]).std(dim=1, unbiased=False) for t in range(1, C3_STEPS)
+    ]
+
+    def true_mask(t):
+        mask = torch.zeros(C3_BATCH, lengths[t], dtype=torch.bool, device=device)
+        mask.scatter_(1, dense_topk[t], True)
+        return mask
+
+    truth = [true_mask(t) for t in range(C3_STEPS)]
+
+    def record(rows, t, bs, step, us):
+        length = lengths[t]
+        nb = -(-length // bs)
+        hits = truth[t].gather(1, step.topk).sum(dim=1)
+        true_blocks = torch.zeros(C3_BATCH, nb, dtype=torch.bool, device=device)
+        true_blocks.scatter_(1, dense_topk[t] // bs, True)
+        false_cold = (true_blocks & ~step.evaluated_blocks).sum(dim=1)
+        qk = step.qk_scored.to(torch.float64)
+        hits, false_cold, qk = hits.cpu().numpy(), false_cold.cpu().numpy(), qk.cpu().numpy()
+        for b in range(C3_BATCH):
+            rows.append({
+                "qk_reduction": 1.0 - qk[b] / length,
+                "net_byte_reduction": 1.0 - (qk[b] * 256 + nb * 8) / (length * 256),
+                "recall": hits[b] / C3_TOPK,
+                "exact_match": float(hits[b] == C3_TOPK),
+                "false_cold_blocks": int(false_cold[b]),
+                "us": us,
+            })
+
+    def timed(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        out = fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return out, e0.elapsed_time(e1) * 1e3
+
+    variants = []
+    wall0 = time.perf_counter()
+    blocks_run = [int(x) for x in args.c3_blocks.split(",")]
+    gammas_run = [float(x) for x in args.c3_gamma.split(",")]
+    for bs in blocks_run:
+        prev_max = [temporal.block_max(sc, bs) for sc in dense_scores[:-1]]
+        wave = c3_wave(-(-lengths[-1] // bs), bs, args.c3_refreshes)
+        for gamma_sigma in gammas_run:
+            for method, order in C3_REPLAY:
+                rows = []
+                for t in range(1, C3_STEPS):
+                    gamma = gamma_sigma * sigma[t]
+                    step, us = timed(lambda: temporal.temporal_step(
+                        queries[t], w, keys[:, : lengths[t]], prev_max[t - 1], lengths[t - 1], dense_topk[t - 1], gamma,
+                        block_size=bs, method=method, scan_order=order, wave=wave))
+                    record(rows, t, bs, step, us)
+                variants.append({"kind": "replay", "block_size": bs, "method": method, "scan_order": order,
+                                 "gamma_sigma": gamma_sigma, "wave": wave if method == "dynamic" else 0,
+                                 **c3_summary(rows)})
+        # Own trajectory: the policy state is initialised from the dense step 0
+        # and then only sees what its own pruned steps scored.
+        own = (
+            approx.ApproxPolicy("dynamic_previous_max", dynamic_threshold=True, order="previous_max"),
+            approx.ApproxPolicy("dynamic_previous_max_streak0", dynamic_threshold=True, order="previous_max",
+                                cold_streak=0),
+        )
+        for policy in own:
+            for gamma_sigma in gammas_run:
+                state = approx.initialize_state(dense_scores[0], k=C3_TOPK, block_size=bs,
+                                                capacity=lengths[-1])
+                gamma = (gamma_sigma * sigma[1]).to(torch.float64)
+                rows = []
+                for t in range(1, C3_STEPS):
+                    step, us = timed(lambda: approx.approx_step(
+                        state, queries[t], w, keys[:, : lengths[t]], policy=policy, step=t, wave=wave, gamma=gamma))
+                    record(rows, t, bs, step, us)
+                variants.append({"kind": "own", "block_size": bs, "method": policy.name, "scan_order": policy.order,
+                                 "gamma_sigma": gamma_sigma, "wave": wave, **c3_summary(rows)})
+        print(f"c3: block {bs} done ({time.perf_counter() - wall0:.1f} s)", file=sys.stderr, flush=True)
+
+    eligible = [v for v in variants if v["recall"] >= C3_HEADLINE_RECALL]
+    head = max(eligible, key=lambda v: (v["net_byte_reduction"], v["recall"]))
+    dense_bytes = sum(C3_BATCH * length * 256 for length in lengths[1:])
+    line = {
+        "metric": "C3 temporal replay: key bytes skipped vs dense + Recall@K, B=4, 256 steps, L 16384->16639, K=2048",
+        "value": round(head["net_byte_reduction"], 4),
+        "unit": "fraction of dense key bytes skipped (median over transitions)",
+        "n_gpus": 1,
+        "steps": C3_STEPS,
+        "warmup": 0,
+        "ms_per_step": round(head["us_per_step"] / 1e3, 5),
+        "recall_at_k": round(head["recall"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C3 temporal replay: B=4 x 256 decode steps, keys N(0,1) bf16, AR(1) queries rho=0.95, "
+            "K=2048, blocks 16/32/64/128, gamma_sigma 0/0.25/0.5/1",
+            "headline_rule": f"largest median net byte reduction among variants with mean Recall@K >= {C3_HEADLINE_RECALL}",
+            "refreshes_per_scan": args.c3_refreshes,
+        },
+        "headline": head,
+        "dense": {"us_per_step": float(np.median(dense_us)), "bytes_equivalent": dense_bytes},
+        "variants": len(variants),
+        "wall_s": round(time.perf_counter() - wall0, 1),
+    }
+    if args.c3_out:
+        Path(args.c3_out).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.c3_out).write_text(json.dumps({"line": line, "variants": variants}, indent=1))
+    print(json.dumps(line), flush=True)
+
 
 
 if __name__ == "__main__":

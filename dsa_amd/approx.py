@@ -262,4 +262,4 @@ def approx_step(
     )
     state.topk = topk
     state.length = length
-    return TemporalStep(topk, scores, evaluated.bool(), qk)
+    return TemporalStep(topk, scores, evaluated.view(torch.bool), qk)

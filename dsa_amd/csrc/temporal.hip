@@ -25,6 +25,7 @@
 #include "common.hpp"
 #include "dsa_amd.h"
 #include "indexer.hpp"
+#include "select.hpp"
 #include "status.hpp"
 #include "waveops.hpp"
 
@@ -44,6 +45,7 @@ struct TemporalWorkspace {
   uint32_t* order;      // [rows][blocks] block ids in scan order
   double* upper;        // [rows][blocks] U_b, in double like the float64 reference
   uint32_t* seed_mask;  // [rows][ceil(L / 32)] keys evaluated as seeds
+  SelectWorkspace select;  // final top-k over the evaluated keys
   int64_t bytes;
 };
 
@@ -55,9 +57,11 @@ TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t length, int6
   const int64_t order_off = run_off + round(rows * k * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
   const int64_t mask_off = upper_off + round(rows * blocks * 8);
+  const int64_t select_off = mask_off + round(rows * ((length + 31) / 32) * 4);
   TemporalWorkspace ws;
-  ws.bytes = mask_off + round(rows * ((length + 31) / 32) * 4);
   const uintptr_t p = reinterpret_cast<uintptr_t>(base);
+  ws.select = select_workspace_layout(base ? reinterpret_cast<void*>(p + select_off) : nullptr, rows, length);
+  ws.bytes = select_off + round(ws.select.bytes);
   ws.tau = base ? reinterpret_cast<uint32_t*>(p + tau_off) : nullptr;
   ws.run = base ? reinterpret_cast<uint32_t*>(p + run_off) : nullptr;
   ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
@@ -121,36 +125,86 @@ __device__ __forceinline__ double policy_risk(const dsa_approx_policy& p, double
   return ((double)last_max + gamma) + aged;
 }
 
-// Sort entries: ascending (lo >> 31, hi, lo & 0x7fffffff).
+// Sort entries: ascending (lo >> 31, hi, lo & 0x7fffffff).  Branch-free: the
+// sort is VALU-bound on one CU, so each compare is a handful of v_cmp with
+// the masks combined on the scalar unit.
 __device__ __forceinline__ bool sorts_before(uint64_t hi_a, uint32_t lo_a, uint64_t hi_b, uint32_t lo_b) {
-  if ((lo_a >> 31) != (lo_b >> 31)) return (lo_a >> 31) < (lo_b >> 31);
-  if (hi_a != hi_b) return hi_a < hi_b;
-  return (lo_a & 0x7fffffffu) < (lo_b & 0x7fffffffu);
+  const uint32_t ga = lo_a >> 31;
+  const uint32_t gb = lo_b >> 31;
+  const uint32_t aa = lo_a & 0x7fffffffu;
+  const uint32_t ab = lo_b & 0x7fffffffu;
+  return (ga < gb) | ((ga == gb) & ((hi_a < hi_b) | ((hi_a == hi_b) & (aa < ab))));
 }
 
-// Bitonic sort of n (a power of two) entries in LDS by one 1024-thread
-// workgroup.
-__device__ void block_bitonic_sort(uint64_t* hi, uint32_t* lo, int n) {
-  const int tid = threadIdx.x;
+constexpr int kSortN = kMaxTemporalBlocks;  // most entries one 1024-thread workgroup sorts
+
+// Bitonic sort of n entries (a power of two, 2 <= n <= kSortN) held two per
+// thread (entries 2t and 2t+1 of thread t; threads with 2t >= n only join
+// the barriers).  Compare-exchange partners at distance 1 are in the same
+// thread, at distance 2..64 in the same wave (lane shuffles, no barrier), and
+// further apart they meet through LDS (xh, xl: kSortN entries).  Partners of
+// an active entry are active: e ^ stride < n for every e < n.
+__device__ void block_sort(uint64_t (&h)[2], uint32_t (&l)[2], uint64_t* xh, uint32_t* xl, int n) {
+  const int t = threadIdx.x;
+  const bool active = 2 * t < n;
   for (int size = 2; size <= n; size <<= 1) {
+    const bool up = ((2 * t) & size) == 0;
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < n; i += 1024) {
-        const int j = i ^ stride;
-        if (j > i) {
-          const bool ascending = (i & size) == 0;
-          const bool swap = ascending ? sorts_before(hi[j], lo[j], hi[i], lo[i])
-                                      : sorts_before(hi[i], lo[i], hi[j], lo[j]);
-          if (swap) {
-            const uint64_t th = hi[i];
-            const uint32_t tl = lo[i];
-            hi[i] = hi[j];
-            lo[i] = lo[j];
-            hi[j] = th;
-            lo[j] = tl;
+      if (stride == 1) {
+        const bool second_first = sorts_before(h[1], l[1], h[0], l[0]);
+        const bool same = (h[0] == h[1]) & (l[0] == l[1]);
+        const bool swap = up ? second_first : !(second_first | same);
+        const uint64_t h0 = swap ? h[1] : h[0];
+        const uint64_t h1 = swap ? h[0] : h[1];
+        const uint32_t l0 = swap ? l[1] : l[0];
+        const uint32_t l1 = swap ? l[0] : l[1];
+        h[0] = h0;
+        h[1] = h1;
+        l[0] = l0;
+        l[1] = l1;
+        continue;
+      }
+      const int mask = stride >> 1;  // partner thread t ^ mask
+      const bool lower = (t & mask) == 0;
+      uint64_t oh[2];
+      uint32_t ol[2];
+      if (stride <= 64) {
+        if (!active) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          oh[j] = __shfl_xor(h[j], mask, kWave);
+          ol[j] = __shfl_xor(l[j], mask, kWave);
+        }
+      } else {
+        if (active) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            xh[2 * t + j] = h[j];
+            xl[2 * t + j] = l[j];
           }
         }
+        __syncthreads();
+        if (active) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            oh[j] = xh[(2 * t + j) ^ stride];
+            ol[j] = xl[(2 * t + j) ^ stride];
+          }
+        }
+        __syncthreads();
+        if (!active) continue;
       }
-      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // other-first decides for the lower entry of an ascending pair and the
+        // upper entry of a descending one; the rest take the other entry iff
+        // it is strictly later (equal entries are padding).
+        const bool other_first = sorts_before(oh[j], ol[j], h[j], l[j]);
+        const bool same = (oh[j] == h[j]) & (ol[j] == l[j]);
+        const bool take = (up == lower) ? other_first : !(other_first | same);
+        h[j] = take ? oh[j] : h[j];
+        l[j] = take ? ol[j] : l[j];
+      }
     }
   }
 }
@@ -161,8 +215,8 @@ __device__ void block_bitonic_sort(uint64_t* hi, uint32_t* lo, int n) {
 // for a forced block, order by risk (approx.py:93-109: address, larger risk
 // then lower address, or buckets of that rank in address order).
 __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
-  __shared__ uint64_t sort_hi[kMaxTemporalBlocks];
-  __shared__ uint32_t sort_lo[kMaxTemporalBlocks];
+  __shared__ uint64_t xh[kSortN];
+  __shared__ uint32_t xl[kSortN];
   __shared__ uint8_t hot[kMaxTemporalBlocks];
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
@@ -174,7 +228,11 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   const int words = (L + 31) / 32;
   for (int i = tid; i < words; i += 1024) a.ws.seed_mask[(size_t)row * words + i] = 0;
   for (int i = tid; i < nb; i += 1024) a.evaluated[(size_t)row * nb + i] = 0;
-  if (tid == 0) a.ws.tau[row] = 0xffffffffu;
+  for (int i = tid; i < kSelectBins; i += 1024) a.ws.select.hist[(size_t)row * kSelectBins + i] = 0;
+  if (tid == 0) {
+    a.ws.tau[row] = 0xffffffffu;
+    a.qk_scored[row] = 0;
+  }
   const int first_new = a.prev_length / bs;
   const bool grown = a.prev_length < L;
   const bool policy = a.policy_mode != 0;
@@ -189,65 +247,66 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     }
     __syncthreads();
   }
-  if (policy) {
-    const dsa_approx_policy& p = a.ap.p;
-    const double gamma = a.ap.gamma_rows ? a.ap.gamma_rows[row] : p.gamma;
-    const int state_blocks = a.prev_blocks;
-    const int recent_first = p.recent_window > 0 ? max(0, L - p.recent_window) / bs : nb;
-    for (int b = tid; b < nb; b += 1024) {
+  // Thread t owns blocks 2t and 2t + 1 (nb <= kSortN); entries past nb are
+  // padding that sorts last.
+  uint64_t h[2] = {~0ull, ~0ull};
+  uint32_t l[2] = {0xffffffffu, 0xffffffffu};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = 2 * tid + j;
+    if (b >= nb) continue;
+    double upper, rank_value;
+    uint32_t group = 0;
+    if (policy) {
+      const dsa_approx_policy& p = a.ap.p;
+      const double gamma = a.ap.gamma_rows ? a.ap.gamma_rows[row] : p.gamma;
       const size_t at = (size_t)row * a.ap.stride + b;
-      const bool stored = b < state_blocks;
+      const bool stored = b < a.prev_blocks;
       const float last = stored ? a.ap.last_max[at] : -__builtin_inff();
       const float ema = stored ? a.ap.ema[at] : -__builtin_inff();
       const float vol = stored ? a.ap.vol[at] : 0.f;
       const int age = stored ? a.ap.age[at] : 0;
       const int cold = stored ? a.ap.cold[at] : 1;
-      const double risk = policy_risk(p, gamma, last, ema, vol, age);
+      const int recent_first = p.recent_window > 0 ? max(0, L - p.recent_window) / bs : nb;
+      rank_value = policy_risk(p, gamma, last, ema, vol, age);
       const bool forced = p.full_refresh || (grown && b >= first_new) || b >= recent_first ||
                           (p.age_cap >= 0 && age >= p.age_cap) || cold < p.cold_streak;
-      a.ws.upper[(size_t)row * nb + b] = forced ? HUGE_VAL : risk;
-      if (sorted) {
-        sort_hi[b] = ~double_to_ordered(risk);
-        sort_lo[b] = (uint32_t)b;
-      }
-    }
-  } else {
-    const double gamma = (double)a.gamma[row];
-    for (int b = tid; b < nb; b += 1024) {
+      upper = forced ? HUGE_VAL : rank_value;
+    } else {
       const bool fresh = grown && b >= first_new;
       const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
-      const double upper = fresh ? HUGE_VAL : (double)pm + gamma;
-      a.ws.upper[(size_t)row * nb + b] = upper;
-      if (sorted) {
-        sort_hi[b] = ~double_to_ordered(upper);
-        sort_lo[b] = (hot_first && !hot[b] ? 0x80000000u : 0u) | (uint32_t)b;
-      }
+      upper = fresh ? HUGE_VAL : (double)pm + (double)a.gamma[row];
+      rank_value = upper;
+      group = hot_first && !hot[b] ? 0x80000000u : 0u;
     }
+    a.ws.upper[(size_t)row * nb + b] = upper;
+    h[j] = ~double_to_ordered(rank_value);
+    l[j] = group | (uint32_t)b;
   }
   if (!sorted) {
     for (int b = tid; b < nb; b += 1024) a.ws.order[(size_t)row * nb + b] = b;
     return;
   }
-  int n = 1;
+  int n = 2;
   while (n < nb) n <<= 1;
-  for (int b = nb + tid; b < n; b += 1024) {  // padding sorts last
-    sort_hi[b] = ~0ull;
-    sort_lo[b] = 0xffffffffu;
-  }
-  __syncthreads();
-  block_bitonic_sort(sort_hi, sort_lo, n);
+  block_sort(h, l, xh, xl, n);
   if (policy && a.ap.p.order == DSA_ORDER_BUCKET) {
     // Rank r in the risk order -> bucket min(N - 1, r * N / nb); then address
     // order within each bucket.
     const int64_t buckets = a.ap.p.buckets;
-    for (int r = tid; r < nb; r += 1024) {
-      sort_hi[r] = (uint64_t)min<int64_t>(buckets - 1, (int64_t)r * buckets / nb);
-      sort_lo[r] &= 0x7fffffffu;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 2 * tid + j;
+      if (r < nb) {
+        h[j] = (uint64_t)min<int64_t>(buckets - 1, (int64_t)r * buckets / nb);
+        l[j] &= 0x7fffffffu;
+      }
     }
-    __syncthreads();
-    block_bitonic_sort(sort_hi, sort_lo, n);
+    block_sort(h, l, xh, xl, n);
   }
-  for (int r = tid; r < nb; r += 1024) a.ws.order[(size_t)row * nb + r] = sort_lo[r] & 0x7fffffffu;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (2 * tid + j < nb) a.ws.order[(size_t)row * nb + 2 * tid + j] = l[j] & 0x7fffffffu;
 }
 
 // Scores 64 keys of one row with the dense kernel's unit code: lane (r, g)
@@ -293,20 +352,25 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
   }
   float v = score_unit<Tag, KF>(a, row, tile_key, r, g);
   const int i = base + lane;
-  if (i >= a.k) return;
-  const int64_t key = seeds[i];
-  if (key < 0 || key >= a.length) {
-    a.ws.run[(size_t)row * a.k + i] = 0;  // below every score
-    return;
+  uint32_t least = 0xffffffffu;  // this lane's seed key (none: neutral for the min)
+  if (i < a.k) {
+    const int64_t key = seeds[i];
+    if (key < 0 || key >= a.length) {
+      a.ws.run[(size_t)row * a.k + i] = 0;  // below every score
+    } else {
+      if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
+      a.scores[(size_t)row * a.length + key] = v;
+      const int words = (a.length + 31) / 32;
+      __hip_atomic_fetch_or(a.ws.seed_mask + (size_t)row * words + (key >> 5), 1u << (key & 31),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      least = float_to_ordered(v);
+      a.ws.run[(size_t)row * a.k + i] = least;
+    }
   }
-  if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
-  a.scores[(size_t)row * a.length + key] = v;
-  const int words = (a.length + 31) / 32;
-  __hip_atomic_fetch_or(a.ws.seed_mask + (size_t)row * words + (key >> 5), 1u << (key & 31), __ATOMIC_RELAXED,
-                        __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t ord = float_to_ordered(v);
-  a.ws.run[(size_t)row * a.k + i] = ord;
-  __hip_atomic_fetch_min(a.ws.tau + row, ord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // One atomic per wave: the minimum of its 64 seeds.
+  for (int off = 32; off > 0; off >>= 1) least = min(least, (uint32_t)__shfl_xor((int)least, off, kWave));
+  if (lane == 0 && least != 0xffffffffu)
+    __hip_atomic_fetch_min(a.ws.tau + row, least, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One block per wave: scan positions [wave_start, wave_start + wave_len) of
@@ -418,27 +482,63 @@ __global__ __launch_bounds__(1024) void temporal_refresh_kernel(TemporalArgs a) 
   if (tid == 0) a.ws.tau[row] = prefix;
 }
 
-// Keys scored: the seeds plus every key of a kept block (each counted once).
-__global__ __launch_bounds__(256) void temporal_count_kernel(TemporalArgs a) {
-  __shared__ __align__(16) uint32_t wsum[4];
+// After the scan: the 4096-bin histogram (top 12 bits of the ordered key)
+// of the step's scores for the select kernels, keys never scored (-inf)
+// included in their own bin so that the row's count is its length, and the
+// number of keys scored (the seeds plus every key of a kept block, each
+// counted once).  One workgroup per (row, chunk of kSelectChunk keys).
+__global__ __launch_bounds__(256) void temporal_hist_kernel(TemporalArgs a) {
+  __shared__ __align__(16) uint32_t hist[kSelectBins];
   const int tid = threadIdx.x;
-  const int row = blockIdx.x;
-  const int words = (a.length + 31) / 32;
-  const int bs = a.block_size;
-  uint32_t count = 0;
-  for (int wd = tid; wd < words; wd += 256) {
-    uint32_t bits = a.ws.seed_mask[(size_t)row * words + wd];
-    for (int sub = 0; sub < 32; sub += 16) {  // blocks are multiples of 16 keys
-      const int blk = (wd * 32 + sub) / bs;
-      if (blk < a.blocks && a.evaluated[(size_t)row * a.blocks + blk]) bits |= 0xffffu << sub;
-    }
-    const int valid = min(32, a.length - wd * 32);
-    if (valid < 32) bits &= (1u << valid) - 1u;
-    count += __popc(bits);
+  const int lane = tid & 63;
+  const int L = a.length;
+  const int chunks = (L + kSelectChunk - 1) / kSelectChunk;
+  const int row = blockIdx.x / chunks;
+  const int c = blockIdx.x % chunks;
+  for (int i = tid; i < kSelectBins; i += 256) hist[i] = 0;
+  __syncthreads();
+  const float* srow = a.scores + (size_t)row * L;
+  const int p0 = c * kSelectChunk + tid * (kSelectChunk / 256);
+  uint32_t unscored = 0;
+#pragma unroll
+  for (int i = 0; i < kSelectChunk / 256; ++i) {
+    const int pos = p0 + i;
+    if (pos >= L) break;
+    const float v = srow[pos];
+    if (v == -__builtin_inff())
+      ++unscored;
+    else
+      __hip_atomic_fetch_add(&hist[float_to_ordered(v) >> 20], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  uint32_t total;
-  block_excl_scan<4>(count, wsum, total);
-  if (tid == 0) a.qk_scored[row] = (int32_t)total;
+  for (int off = 32; off > 0; off >>= 1) unscored += (uint32_t)__shfl_xor((int)unscored, off, kWave);
+  if (lane == 0 && unscored)
+    __hip_atomic_fetch_add(&hist[float_to_ordered(-__builtin_inff()) >> 20], unscored, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+  // Keys scored in this chunk: 64 words of 32 keys (wave 0).
+  if (tid < 64) {
+    const int words = (L + 31) / 32;
+    const int wd = c * (kSelectChunk / 32) + tid;
+    uint32_t count = 0;
+    if (wd < words) {
+      uint32_t bits = a.ws.seed_mask[(size_t)row * words + wd];
+      for (int sub = 0; sub < 32; sub += 16) {  // blocks are multiples of 16 keys
+        const int blk = (wd * 32 + sub) / a.block_size;
+        if (blk < a.blocks && a.evaluated[(size_t)row * a.blocks + blk]) bits |= 0xffffu << sub;
+      }
+      const int valid = min(32, L - wd * 32);
+      if (valid < 32) bits &= (1u << valid) - 1u;
+      count = __popc(bits);
+    }
+    for (int off = 32; off > 0; off >>= 1) count += (uint32_t)__shfl_xor((int)count, off, kWave);
+    if (tid == 0 && count)
+      __hip_atomic_fetch_add(a.qk_scored + row, (int32_t)count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  uint32_t* ghist = a.ws.select.hist + (size_t)row * kSelectBins;
+  for (int i = tid; i < kSelectBins; i += 256) {
+    const uint32_t n = hist[i];
+    if (n) __hip_atomic_fetch_add(&ghist[i], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 struct StateArgs {
@@ -533,10 +633,10 @@ int launch_temporal(TemporalArgs a, int32_t wave, int64_t* out_topk, hipStream_t
       if (int st = check_launch("temporal_refresh_kernel")) return st;
     }
   }
-  hipLaunchKernelGGL(temporal_count_kernel, dim3(a.rows), dim3(256), 0, stream, a);
-  if (int st = check_launch("temporal_count_kernel")) return st;
-  if (int st = dsa_topk(a.scores, nullptr, a.rows, a.length, a.length, nullptr, a.k, 0, out_topk, nullptr, stream))
-    return st;
+  const int chunks = (a.length + kSelectChunk - 1) / kSelectChunk;
+  hipLaunchKernelGGL(temporal_hist_kernel, dim3(a.rows * chunks), dim3(256), 0, stream, a);
+  if (int st = check_launch("temporal_hist_kernel")) return st;
+  if (int st = launch_select(a.scores, a.rows, a.length, a.k, a.ws.select, out_topk, nullptr, stream)) return st;
   if (a.policy_mode == 0) return DSA_STATUS_OK;
   StateArgs s = {};
   s.scores = a.scores;

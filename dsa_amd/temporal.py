@@ -152,7 +152,7 @@ def temporal_step(
         _lib.ptr(evaluated), _lib.ptr(topk), _lib.ptr(qk), batch, length, k, block_size,
         SCAN_ORDERS[scan_order], wave, _lib.dtype_code(keys.dtype), _lib.ptr(ws), ws.numel(), stream,
     )
-    return TemporalStep(topk, scores, evaluated.bool(), qk)
+    return TemporalStep(topk, scores, evaluated.view(torch.bool), qk)
 
 
 def block_max(scores: torch.Tensor, block_size: int) -> torch.Tensor:
