@@ -15,6 +15,7 @@ namespace dsa {
 struct KeysB16 {  // bf16 or fp16 rows, 256 B
   static constexpr int kRowBytes = 256;
   static constexpr int kRaw = 4;
+  static constexpr int kBuffers = 2;  // units in flight per wave in the streaming loop
   static constexpr bool kScaled = false;
   // Natural k order: k-step j of lane group g is dims 32j + 8g .. +8, so one
   // load instruction reads 64 contiguous bytes of each of the tile's 16 rows.
@@ -37,6 +38,7 @@ struct KeysB16 {  // bf16 or fp16 rows, 256 B
 struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
   static constexpr int kRowBytes = 128;
   static constexpr int kRaw = 2;
+  static constexpr int kBuffers = 4;  // half-size units: twice as many in flight, same bytes as bf16
   static constexpr bool kScaled = true;
   // Permuted k order: k-step j of lane group g is dims 32g + 8j .. +8; a lane
   // reads 32 contiguous bytes, and two instructions cover each 128-byte row.

@@ -51,26 +51,30 @@ struct DenseArgs {
   uint32_t* hist;  // [sequences][kSelectBins] score histogram (kHist only)
 };
 
-// Keys past the valid range read as zeros (buffer bounds check).
+// Keys past the valid range read as zeros (buffer bounds check).  Scaled
+// keys also fetch the unit's scale (a 64-key unit lies in one 128-key scale
+// block) with the keys, so the compute never waits on it.
 template <class KF>
 __device__ __forceinline__ void dense_load_unit(BufferRsrc keys, int u, int r, int g,
-                                                uint4 (&buf)[4][KF::kRaw]) {
+                                                uint4 (&buf)[4][KF::kRaw], const float* scales, int L,
+                                                float& scale) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) KF::load_buf(keys, u * 64 + 16 * t + r, g, buf[t]);
+  if constexpr (KF::kScaled) scale = scales[min(u * 64, L - 1) >> 7];
 }
 
 template <class Tag, class KF, int M, bool kHist>
 __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], const float (&wr)[M][4],
                                                    const uint4 (&buf)[4][KF::kRaw], int u,
                                                    int valid, int L, int lane, int g,
-                                                   const float* scales, BufferRsrc out,
+                                                   float scale, BufferRsrc out,
                                                    uint32_t* hist) {
   float s[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, M, KF>(qa, wr, buf[t]);
   float keep = unit_reduce(s, g);
   const int key = u * 64 + lane;
-  if constexpr (KF::kScaled) keep *= scales[min(key, L - 1) >> 7];
+  if constexpr (KF::kScaled) keep *= scale;
   // Stores past L are dropped by the buffer bounds check.
   buffer_store_f32(out, (uint32_t)key * 4, key < valid ? keep : -__builtin_inff());
   if constexpr (kHist)
@@ -95,21 +99,28 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
     load_dense_head_tiles<M, KF::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa, wr);
   }
 
-  // Two register buffers.  The next unit's loads are always issued before the
-  // current unit is computed; past the wave's last unit the prefetch re-reads
-  // that last unit (an L2 hit), so no load is conditional and the compiler's
-  // vmcnt waits cover exactly the buffer being consumed.
+  // A ring of KF::kBuffers register buffers.  The loads of the unit
+  // kBuffers - 1 ahead are always issued before the current unit is computed;
+  // past the wave's last unit the prefetch re-reads that last unit (an L2
+  // hit), so no load is conditional and the compiler's vmcnt waits cover
+  // exactly the buffer being consumed.
+  constexpr int NB = KF::kBuffers;
   const int u_last = u_first + u_stride * (count - 1);
-  uint4 buf0[4][KF::kRaw];
-  uint4 buf1[4][KF::kRaw];
-  dense_load_unit<KF>(keys, u_first, r, g, buf0);
-  for (int i = 0; i < count; i += 2) {
+  uint4 buf[NB][4][KF::kRaw];
+  float scale[NB] = {};
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s)
+    dense_load_unit<KF>(keys, min(u_first + u_stride * s, u_last), r, g, buf[s], scales, L, scale[s]);
+  for (int i = 0; i < count; i += NB) {
     const int u = u_first + u_stride * i;
-    dense_load_unit<KF>(keys, min(u + u_stride, u_last), r, g, buf1);
-    dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf0, u, valid, L, lane, g, scales, out, hist);
-    if (i + 1 >= count) break;
-    dense_load_unit<KF>(keys, min(u + 2 * u_stride, u_last), r, g, buf0);
-    dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf1, u + u_stride, valid, L, lane, g, scales, out, hist);
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      if (i + s >= count) break;
+      dense_load_unit<KF>(keys, min(u + u_stride * (s + NB - 1), u_last), r, g, buf[(s + NB - 1) % NB], scales, L,
+                          scale[(s + NB - 1) % NB]);
+      dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf[s], u + u_stride * s, valid, L, lane, g, scale[s], out,
+                                            hist);
+    }
   }
 }
 
@@ -374,12 +385,11 @@ __global__ void promote_blocks_kernel(const uint8_t* direct, const float* block_
 // ---------------------------------------------------------------------------
 // Host-side launch helpers.
 // ---------------------------------------------------------------------------
-int units_per_workgroup(int64_t sequences, int64_t length) {
-  // About one workgroup of four waves per CU: every wave then streams several
-  // units, so its query-block load and pipeline fill are paid once, while at
-  // least four units (one per wave) stay in each workgroup.
+int units_per_workgroup(int64_t sequences, int64_t length, int64_t target_wgs) {
+  // About target_wgs / 256 workgroups of four waves per CU: every wave then
+  // streams several units, so its query-block load and pipeline fill are paid
+  // once, while at least four units (one per wave) stay in each workgroup.
   const int64_t units = (length + 63) / 64;
-  const int64_t target_wgs = 256;
   int64_t per = (units * sequences + target_wgs - 1) / target_wgs;
   per = per < 4 ? 4 : per;
   per = (per + 3) / 4 * 4;
@@ -389,7 +399,7 @@ int units_per_workgroup(int64_t sequences, int64_t length) {
 template <class Tag, class KF, int M, bool kGather, bool kHist = false>
 int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
   const int64_t units = (a.length + 63) / 64;
-  a.units_per_wg = units_per_workgroup(sequences, a.length);
+  a.units_per_wg = units_per_workgroup(sequences, a.length, 256);
   a.wgs_per_seq = (int32_t)((units + a.units_per_wg - 1) / a.units_per_wg);
   a.total_wgs = sequences * a.wgs_per_seq;
   const int64_t grid = (a.total_wgs + kXcds - 1) / kXcds * kXcds;
