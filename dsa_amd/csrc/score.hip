@@ -186,6 +186,99 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
 
 
 // ---------------------------------------------------------------------------
+// Multi-query (prefill) scoring: many query blocks against one shared key set.
+// A workgroup owns kPrefillQueries consecutive queries of one key set (two per
+// wave) and streams the key units they see through LDS: each 64-key unit is
+// loaded from memory once and scored for all eight queries, instead of once
+// per query.  Rows are padded to kPrefillRow bytes so the 16 rows a lane
+// group reads fall on different banks.  With a causal limit the heaviest
+// query blocks are dispatched first.
+// ---------------------------------------------------------------------------
+constexpr int kPrefillQueries = 8;
+constexpr int kPrefillRow = 272;
+
+template <class Tag>
+__global__ __launch_bounds__(256) void prefill_scores_kernel(DenseArgs a, int32_t qblocks, int32_t keysets) {
+  __shared__ __align__(16) uint8_t lds[2][64 * kPrefillRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int qb = qblocks - 1 - (int)(blockIdx.x / keysets);  // heaviest first
+  const int64_t keyset = blockIdx.x % keysets;
+  const int L = a.length;
+  const int qpk = a.queries_per_keyset;
+  auto visible = [&](int t) { return a.causal_offset >= 0 ? min(L, t + a.causal_offset + 1) : L; };
+  const int t_last = min(qpk - 1, qb * kPrefillQueries + kPrefillQueries - 1);
+  const int units = (visible(t_last) + 63) >> 6;
+
+  uint4 qa[2][4][4];
+  float wr[2][4][4];
+  bool active[2];
+  int vis[2];
+  float* orow[2];
+#pragma unroll
+  for (int qi = 0; qi < 2; ++qi) {
+    const int t = qb * kPrefillQueries + 2 * wave + qi;
+    active[qi] = t < qpk;
+    const int64_t seq = keyset * qpk + (active[qi] ? t : 0);
+    load_dense_head_tiles<4, KeysB16::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa[qi],
+                                                 wr[qi]);
+    vis[qi] = active[qi] ? visible(t) : 0;
+    orow[qi] = a.out + seq * a.out_stride;
+  }
+
+  // Cooperative unit load: thread i moves 64 bytes of row i / 4.
+  const BufferRsrc kr = make_buffer(a.keys + keyset * a.key_stride * KeysB16::kRowBytes,
+                                    (uint32_t)L * KeysB16::kRowBytes);
+  const int lrow = threadIdx.x >> 2;
+  const int lpart = threadIdx.x & 3;
+  uint4 stage[4];
+  auto fetch = [&](int u) {
+    const uint32_t off = (uint32_t)(u * 64 + lrow) * KeysB16::kRowBytes + lpart * 64;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) stage[k] = buffer_load_16(kr, off + 16 * k);
+  };
+  auto put = [&](int buf) {
+    uint8_t* dst = lds[buf] + lrow * kPrefillRow + lpart * 64;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(dst + 16 * k) = stage[k];
+  };
+  if (units > 0) {
+    fetch(0);
+    put(0);
+  }
+  __syncthreads();
+  for (int u = 0; u < units; ++u) {
+    if (u + 1 < units) fetch(u + 1);  // in flight while this unit is scored
+    const uint8_t* base = lds[u & 1];
+    float s[2][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint4 raw[KeysB16::kRaw];
+      const uint8_t* row = base + (16 * t + r) * kPrefillRow + g * 16;
+#pragma unroll
+      for (int c = 0; c < KeysB16::kRaw; ++c) raw[c] = *reinterpret_cast<const uint4*>(row + 64 * c);
+#pragma unroll
+      for (int qi = 0; qi < 2; ++qi) s[qi][t] = tile_contrib<Tag, 4, KeysB16>(qa[qi], wr[qi], raw);
+    }
+    const int key = u * 64 + lane;
+#pragma unroll
+    for (int qi = 0; qi < 2; ++qi) {
+      const float score = unit_reduce(s[qi], g);
+      if (active[qi] && key < L) orow[qi][key] = key < vis[qi] ? score : -__builtin_inff();
+    }
+    if (u + 1 < units) put((u + 1) & 1);  // the buffer scored in the previous iteration
+    __syncthreads();
+  }
+  // Keys past this workgroup's units are invisible to all of its queries.
+#pragma unroll
+  for (int qi = 0; qi < 2; ++qi)
+    if (active[qi])
+      for (int key = units * 64 + lane; key < L; key += 64) orow[qi][key] = -__builtin_inff();
+}
+
+// ---------------------------------------------------------------------------
 // fp32 keys and queries (accuracy path): v_mfma_f32_16x16x4_f32, queries
 // staged once per workgroup in LDS (rows padded to 129 floats), one 16-key
 // tile per wave.  k-step j of lane group g uses dim 32 * g + j.
@@ -411,6 +504,17 @@ int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
 
 template <class Tag, class KF>
 int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
+  if constexpr (KF::kRowBytes == KeysB16::kRowBytes) {
+    if (!a.head_ids && a.head_count == kHeads && a.queries_per_keyset >= kPrefillQueries) {
+      const int64_t keysets = sequences / a.queries_per_keyset;
+      const int64_t qblocks = (a.queries_per_keyset + kPrefillQueries - 1) / kPrefillQueries;
+      if (keysets * a.queries_per_keyset == sequences && qblocks * keysets <= 0x7fffffffLL) {
+        hipLaunchKernelGGL((prefill_scores_kernel<Tag>), dim3((unsigned)(qblocks * keysets)), dim3(256), 0, stream, a,
+                           (int32_t)qblocks, (int32_t)keysets);
+        return check_launch("prefill_scores_kernel");
+      }
+    }
+  }
   if (!a.head_ids && a.head_count == kHeads) return launch_dense_m<Tag, KF, 4, false>(a, sequences, stream);
   switch ((a.head_count + 15) / 16) {
     case 1: return launch_dense_m<Tag, KF, 1, true>(a, sequences, stream);

@@ -1,7 +1,8 @@
 // Exact top-k with stable_topk semantics (reference metrics.py:9-22): the k
 // largest values, ties at the cut-off go to the lower index.
 //
-// One 1024-thread workgroup per (virtual) row.  Thread t owns the contiguous
+// One workgroup per (virtual) row: 1024 threads, or 256 when many short rows
+// (at most 4096 entries) make throughput matter more than latency.  Thread t owns the contiguous
 // slice [t * EPT, t * EPT + EPT) of the row in registers, so a single
 // exclusive scan over threads enumerates elements in index order.  The k-th
 // largest (value, index) pair is found by a value-linear bucket select whose
@@ -14,8 +15,7 @@
 namespace dsa {
 namespace {
 
-constexpr int kTopkThreads = 1024;
-constexpr int kTopkWaves = kTopkThreads / kWave;
+constexpr int kTopkThreads = 1024;  // widest workgroup (long rows)
 constexpr int kMaxK = 4096;
 constexpr int kBins = 2048;
 
@@ -33,11 +33,13 @@ struct TopkArgs {
   float* out_val;
 };
 
+template <int THREADS>
 struct TopkShared {
+  static constexpr int kWaves = THREADS / kWave;
   uint32_t hist[kBins];
-  uint32_t wave_sums[kTopkWaves];
-  float wave_lo[kTopkWaves];
-  float wave_hi[kTopkWaves];
+  uint32_t wave_sums[kWaves];
+  float wave_lo[kWaves];
+  float wave_hi[kWaves];
   uint32_t digit;
   uint32_t krem;
   uint64_t cstar;
@@ -46,6 +48,7 @@ struct TopkShared {
 
 // Exclusive prefix sum over the workgroup in thread order; returns the total
 // through `total`.  Contains two barriers.
+template <int WAVES>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_sums,
                                                          uint32_t& total) {
   const int lane = threadIdx.x & 63;
@@ -61,7 +64,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   uint32_t before = 0;
   uint32_t all = 0;
 #pragma unroll
-  for (int i = 0; i < kTopkWaves; ++i) {
+  for (int i = 0; i < WAVES; ++i) {
     const uint32_t s = wave_sums[i];
     before += i < wave ? s : 0u;
     all += s;
@@ -72,11 +75,12 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
 }
 
 // Bitonic sort of keys[0, width) in descending order (width a power of two).
+template <int THREADS>
 __device__ __forceinline__ void bitonic_sort_desc(uint64_t* keys, int width) {
   const int tid = threadIdx.x;
   for (int size = 2; size <= width; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < (width >> 1); i += kTopkThreads) {
+      for (int i = tid; i < (width >> 1); i += THREADS) {
         const int lo = 2 * i - (i & (stride - 1));
         const int hi = lo + stride;
         const uint64_t x = keys[lo];
@@ -113,21 +117,28 @@ __device__ __forceinline__ int value_bucket(uint32_t key, float lo, float scale)
 
 // Finds the bin holding the want-th largest element of the histogram in
 // sh.hist; leaves it in sh.digit and the remaining rank inside it in sh.krem.
-__device__ __forceinline__ void locate_bin(TopkShared& sh, uint32_t want) {
+// Thread t scans bins [t * B, t * B + B), B = kBins / THREADS.
+template <int THREADS>
+__device__ __forceinline__ void locate_bin(TopkShared<THREADS>& sh, uint32_t want) {
+  constexpr int B = kBins / THREADS;
   const int tid = threadIdx.x;
-  const uint32_t c0 = sh.hist[2 * tid];
-  const uint32_t c1 = sh.hist[2 * tid + 1];
-  uint32_t total;
-  const uint32_t before = block_exclusive_scan(c0 + c1, sh.wave_sums, total);
-  const uint32_t above1 = total - before - c0 - c1;  // elements in bins > 2t+1
-  const uint32_t above0 = above1 + c1;               // elements in bins > 2t
-  if (c1 && above1 < want && want <= above1 + c1) {
-    sh.digit = 2 * tid + 1;
-    sh.krem = want - above1;
+  uint32_t c[B];
+  uint32_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    c[i] = sh.hist[B * tid + i];
+    mine += c[i];
   }
-  if (c0 && above0 < want && want <= above0 + c0) {
-    sh.digit = 2 * tid;
-    sh.krem = want - above0;
+  uint32_t total;
+  const uint32_t before = block_exclusive_scan<THREADS / kWave>(mine, sh.wave_sums, total);
+  uint32_t above = total - before - mine;  // elements in bins above this thread's
+#pragma unroll
+  for (int i = B - 1; i >= 0; --i) {
+    if (c[i] && above < want && want <= above + c[i]) {
+      sh.digit = B * tid + i;
+      sh.krem = want - above;
+    }
+    above += c[i];
   }
   __syncthreads();
 }
@@ -142,9 +153,10 @@ __device__ __forceinline__ void locate_bin(TopkShared& sh, uint32_t want) {
 //      11+11+10-bit radix select over the ordered keys for the k-th value,
 //      whose ties are ranked by position with a prefix scan.
 // All per-element work is branch-free (predicated adds and sink-slot writes).
-template <int EPT>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
-  __shared__ TopkShared sh;
+template <int THREADS, int EPT>
+__global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
+  constexpr int kWaves = THREADS / kWave;
+  __shared__ TopkShared<THREADS> sh;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -189,7 +201,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
     uint32_t mine = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) mine += key[e] != 0 ? 1u : 0u;
-    block_exclusive_scan(mine, sh.wave_sums, n_valid);
+    block_exclusive_scan<kWaves>(mine, sh.wave_sums, n_valid);
   }
   if (n_valid > (uint32_t)k) {
     bool resolved = false;
@@ -211,10 +223,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
       sh.wave_lo[wave] = lo;
       sh.wave_hi[wave] = hi;
     }
-    for (int i = tid; i < kBins; i += kTopkThreads) sh.hist[i] = 0;
+    for (int i = tid; i < kBins; i += THREADS) sh.hist[i] = 0;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kTopkWaves; ++i) {
+    for (int i = 0; i < kWaves; ++i) {
       lo = fminf(lo, sh.wave_lo[i]);
       hi = fmaxf(hi, sh.wave_hi[i]);
     }
@@ -236,7 +248,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         for (int e = 0; e < EPT; ++e)
           mine += (key[e] != 0 && value_bucket(key[e], lo, scale) == bucket) ? 1u : 0u;
         uint32_t total;
-        uint32_t slot = block_exclusive_scan(mine, sh.wave_sums, total);
+        uint32_t slot = block_exclusive_scan<kWaves>(mine, sh.wave_sums, total);
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
           const bool in_t = key[e] != 0 && value_bucket(key[e], lo, scale) == bucket;
@@ -245,9 +257,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         }
         int width = 1;
         while (width < (int)crowd) width <<= 1;
-        for (int i = (int)crowd + tid; i < width; i += kTopkThreads) sh.sort_keys[i] = 0;
+        for (int i = (int)crowd + tid; i < width; i += THREADS) sh.sort_keys[i] = 0;
         __syncthreads();
-        bitonic_sort_desc(sh.sort_keys, width);
+        bitonic_sort_desc<THREADS>(sh.sort_keys, width);
         cstar = sh.sort_keys[need - 1];
         resolved = true;
       }
@@ -262,7 +274,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
         const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
         const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
         __syncthreads();
-        for (int i = tid; i < kBins; i += kTopkThreads) sh.hist[i] = 0;
+        for (int i = tid; i < kBins; i += THREADS) sh.hist[i] = 0;
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < EPT; ++e)
@@ -279,7 +291,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) mine += key[e] == threshold ? 1u : 0u;
       uint32_t ties;
-      uint32_t rank = block_exclusive_scan(mine, sh.wave_sums, ties);
+      uint32_t rank = block_exclusive_scan<kWaves>(mine, sh.wave_sums, ties);
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const bool tie = key[e] == threshold;
@@ -297,7 +309,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 #pragma unroll
   for (int e = 0; e < EPT; ++e) n_sel += composite(key[e], e0 + e) >= cstar ? 1u : 0u;
   uint32_t sel_total;
-  uint32_t p = block_exclusive_scan(n_sel, sh.wave_sums, sel_total);
+  uint32_t p = block_exclusive_scan<kWaves>(n_sel, sh.wave_sums, sel_total);
   // Exactly min(valid, k) elements are chosen; the clamp only guards buffers.
   sel_total = min(sel_total, (uint32_t)k);
 #pragma unroll
@@ -312,17 +324,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
   if (a.sorted) {
     int width = 1;
     while (width < (int)sel_total) width <<= 1;
-    for (int i = (int)sel_total + tid; i < width; i += kTopkThreads) sh.sort_keys[i] = 0;
+    for (int i = (int)sel_total + tid; i < width; i += THREADS) sh.sort_keys[i] = 0;
     __syncthreads();
-    bitonic_sort_desc(sh.sort_keys, width);
+    bitonic_sort_desc<THREADS>(sh.sort_keys, width);
   }
-  for (int i = tid; i < (int)sel_total; i += kTopkThreads) {
+  for (int i = tid; i < (int)sel_total; i += THREADS) {
     const uint32_t pos = ~(uint32_t)(sh.sort_keys[i] & 0xffffffffu);
     if (a.out_idx) a.out_idx[out_base + i] = a.in_idx ? a.in_idx[base + pos] : (int64_t)(start + pos);
     if (a.out_val) a.out_val[out_base + i] = a.scores[base + pos];
   }
   // Padding when fewer than k valid entries exist.
-  for (int i = (int)sel_total + tid; i < k; i += kTopkThreads) {
+  for (int i = (int)sel_total + tid; i < k; i += THREADS) {
     if (a.out_idx) a.out_idx[out_base + i] = -1;
     if (a.out_val) a.out_val[out_base + i] = -__builtin_inff();
   }
@@ -331,11 +343,19 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkArgs a) {
 int launch_topk(const TopkArgs& a, int64_t virtual_rows, hipStream_t stream) {
   const int n = a.chunk_len;
   const dim3 grid((unsigned)virtual_rows);
+  if (virtual_rows >= 1024 && n <= 256 * 16) {
+    // Many short rows: 256-thread workgroups, four per CU.
+    const dim3 block(256);
+    if (n <= 256 * 4) hipLaunchKernelGGL((topk_kernel<256, 4>), grid, block, 0, stream, a);
+    else if (n <= 256 * 8) hipLaunchKernelGGL((topk_kernel<256, 8>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((topk_kernel<256, 16>), grid, block, 0, stream, a);
+    return check_launch("topk_kernel");
+  }
   const dim3 block(kTopkThreads);
-  if (n <= kTopkThreads * 4) hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, stream, a);
-  else if (n <= kTopkThreads * 8) hipLaunchKernelGGL(topk_kernel<8>, grid, block, 0, stream, a);
-  else if (n <= kTopkThreads * 16) hipLaunchKernelGGL(topk_kernel<16>, grid, block, 0, stream, a);
-  else hipLaunchKernelGGL(topk_kernel<32>, grid, block, 0, stream, a);
+  if (n <= kTopkThreads * 4) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 4>), grid, block, 0, stream, a);
+  else if (n <= kTopkThreads * 8) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 8>), grid, block, 0, stream, a);
+  else if (n <= kTopkThreads * 16) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 16>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((topk_kernel<kTopkThreads, 32>), grid, block, 0, stream, a);
   return check_launch("topk_kernel");
 }
 

@@ -45,6 +45,26 @@ def test_topk_matches_oracle(device, kind, length, k) -> None:
         assert idx_index[r].cpu().numpy().tolist() == np.sort(want).tolist()
 
 
+@pytest.mark.parametrize("kind", ["normal", "ties", "zeros", "neginf"])
+@pytest.mark.parametrize("length,k", [(300, 17), (2048, 256), (4096, 512)])
+def test_many_short_rows(device, kind, length, k) -> None:
+    # Enough rows of at most 4096 entries for the 256-thread workgroups; every
+    # row checked, with ragged row lengths on half of them.
+    print(f"topk many rows kind={kind} L={length} k={k}", flush=True)
+    rows = 1536
+    host = rows_for(kind, rows, length, seed=7 * length + k)
+    rng = np.random.default_rng(length)
+    lengths = np.where(np.arange(rows) % 2 == 0, length, rng.integers(0, length + 1, size=rows)).astype(np.int32)
+    x = torch.from_numpy(host).to(device)
+    lens = torch.from_numpy(lengths).to(device)
+    idx_sorted = metrics.topk(x, k, sorted=True, row_lengths=lens).cpu().numpy()
+    idx_index = metrics.topk(x, k, sorted=False, row_lengths=lens).cpu().numpy()
+    for r in range(rows):
+        n = int(lengths[r])
+        assert idx_sorted[r].tolist() == T.topk_sorted_padded(host[r], k, n).tolist(), r
+        assert idx_index[r].tolist() == T.topk_index_order(host[r], k, n).tolist(), r
+
+
 def test_row_lengths_pad_short_rows(device) -> None:
     host = rows_for("ties", 4, 600, seed=3)
     lengths = torch.tensor([600, 10, 0, 257], dtype=torch.int32)
