@@ -750,7 +750,7 @@ def run_progressive(args) -> None:
 
     import torch
 
-    from dsa_amd import _lib, progressive_kernel as P
+    from dsa_amd import _lib, metrics as M, progressive_kernel as P
 
     _lib.load()
     device = torch.device("cuda", 0)
@@ -806,7 +806,6 @@ def run_progressive(args) -> None:
             two = P.two_pass_scores_hip(q, w, k, selected, direct, thr, block_size=PROG_BLOCK)
             keep = probe.accepted_blocks.bool().repeat_interleave(PROG_BLOCK)[:ctx]
             err = (probe.scores[keep] - full[keep]).abs()
-            from dsa_amd import metrics as M
             f_ids = M.topk(probe.scores, TOPK, sorted=False)
             t_ids = M.topk(full, TOPK, sorted=False)
             quality.append({"context": ctx, "variant": v, "threshold": threshold, "direct_blocks": item["direct_count"],
@@ -842,8 +841,15 @@ def run_progressive(args) -> None:
                       it["cidx"].data_ptr() if compact else None, it["acc"].data_ptr(), it["bmax"].data_ptr(),
                       it["counter"].data_ptr(), ctx, PROG_BLOCK, int(compact), _lib.DTYPE_BF16, stream())
 
-        def topk(it, scores, n, cand=None):
-            _lib.call("dsa_topk", scores.data_ptr(), None, 1, n, n, None, min(TOPK, n), 0, it["topi"].data_ptr(), None, stream())
+        def topk(it, scores, n):
+            # the library's choice for one row (metrics.topk): the distributed
+            # select from 16K entries, one workgroup below
+            if n >= M.DISTRIBUTED_MIN_LENGTH:
+                _lib.call("dsa_topk_distributed", scores.data_ptr(), 1, n, min(TOPK, n), it["topi"].data_ptr(), None,
+                          it["ws"].data_ptr(), it["ws"].numel(), stream())
+            else:
+                _lib.call("dsa_topk", scores.data_ptr(), None, 1, n, n, None, min(TOPK, n), 0, it["topi"].data_ptr(), None,
+                          stream())
 
         def decode_step(it):
             _lib.call("dsa_score_topk", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), None,

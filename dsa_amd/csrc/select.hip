@@ -368,6 +368,48 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs 
   }
 }
 
+// ---------------------------------------------------------------------------
+// histogram of arbitrary score rows: one workgroup per (row, chunk); every
+// entry is counted (-inf in its own bin), so a row's total is its length.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kSelThreads) void select_hist_kernel(SelectArgs a) {
+  __shared__ __align__(16) uint32_t hist[kSelectBins];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = lane_id();
+  const uint32_t chunks = (uint32_t)a.chunks;
+  const uint32_t logical = logical_block();
+  const uint32_t row = logical / chunks;
+  const uint32_t c = logical % chunks;
+  const uint32_t n = (uint32_t)a.length;
+  for (uint32_t i = tid; i < (uint32_t)kSelectBins; i += kSelThreads) hist[i] = 0;
+  __syncthreads();
+  const uint32_t p0 = c * kSelectChunk + tid * kSelEpt;
+  const BufferRsrc srs = make_buffer(a.scores + (size_t)row * n, n * 4u);
+  const uint4 s0 = buffer_load_16(srs, p0 * 4u);
+  const uint4 s1 = buffer_load_16(srs, (p0 + 4u) * 4u);
+  const uint32_t w8[kSelEpt] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const uint32_t neg_inf_bin = float_to_ordered(-__builtin_inff()) >> 20;
+  uint32_t neg_inf = 0;  // counted per wave: a sparse row is mostly -inf
+#pragma unroll
+  for (int i = 0; i < kSelEpt; ++i) {
+    if (p0 + i >= n) continue;
+    const uint32_t bin = float_to_ordered(__uint_as_float(w8[i])) >> 20;
+    if (bin == neg_inf_bin)
+      ++neg_inf;
+    else
+      __hip_atomic_fetch_add(&hist[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  for (int off = 32; off > 0; off >>= 1) neg_inf += (uint32_t)__shfl_xor((int)neg_inf, off, kWave);
+  if (lane == 0 && neg_inf)
+    __hip_atomic_fetch_add(&hist[neg_inf_bin], neg_inf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+  uint32_t* ghist = a.ws.hist + (size_t)row * kSelectBins;
+  for (uint32_t i = tid; i < (uint32_t)kSelectBins; i += kSelThreads) {
+    const uint32_t v = hist[i];
+    if (v) __hip_atomic_fetch_add(&ghist[i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 }  // namespace
 
 SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length) {
@@ -408,9 +450,43 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
   return check_launch("select_resolve_kernel");
 }
 
+int launch_select_scores(const float* scores, int64_t rows, int64_t length, int64_t k,
+                         const SelectWorkspace& ws, int64_t* out_idx, float* out_val, hipStream_t stream) {
+  SelectArgs a;
+  a.scores = scores;
+  a.rows = (int32_t)rows;
+  a.length = (int32_t)length;
+  a.chunks = (int32_t)((length + kSelectChunk - 1) / kSelectChunk);
+  a.k = (int32_t)k;
+  a.ws = ws;
+  a.out_idx = out_idx;
+  a.out_val = out_val;
+  hipLaunchKernelGGL(select_hist_kernel, dim3((unsigned)(rows * a.chunks)), dim3(kSelThreads), 0, stream, a);
+  if (int st = check_launch("select_hist_kernel")) return st;
+  return launch_select(scores, rows, length, k, ws, out_idx, out_val, stream);
+}
+
 }  // namespace dsa
 
 using namespace dsa;
+
+extern "C" int dsa_topk_distributed(const float* scores, int64_t rows, int64_t length, int64_t k,
+                                    int64_t* out_indices, float* out_values, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  DSA_REQUIRE(scores && out_indices, "null pointer argument");
+  DSA_REQUIRE(rows > 0 && rows <= 65535, "rows %lld out of range", (long long)rows);
+  DSA_REQUIRE(length > 0 && length <= int64_t(kSelectChunk) * kMaxSelectChunks,
+              "length %lld outside [1, %d]", (long long)length, kSelectChunk * kMaxSelectChunks);
+  DSA_REQUIRE(k > 0 && k <= (int64_t(1) << 27), "k=%lld out of range", (long long)k);
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(scores) % 16 == 0 && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+              "scores (16 B) and workspace (256 B) must be aligned");
+  const SelectWorkspace ws = select_workspace_layout(workspace, rows, length);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the distributed top-k needs %lld workspace bytes",
+                (long long)ws.bytes);
+  return launch_select_scores(scores, rows, length, k, ws, out_indices, out_values,
+                              static_cast<hipStream_t>(stream));
+}
 
 extern "C" int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t k,
                                int64_t* out_indices, float* out_values, void* workspace,

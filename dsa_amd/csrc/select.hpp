@@ -23,6 +23,11 @@ struct SelectWorkspace {
 // Carves the workspace out of `base` (base == nullptr only measures it).
 SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length);
 
+// Builds the histogram of scores [rows, length] (every entry, -inf included)
+// in the zeroed ws.hist, then selects their top-k.
+int launch_select_scores(const float* scores, int64_t rows, int64_t length, int64_t k,
+                         const SelectWorkspace& ws, int64_t* out_idx, float* out_val, hipStream_t stream);
+
 // Selects the top-k of scores [rows, length] whose histogram is in ws.
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,

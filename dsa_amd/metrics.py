@@ -17,6 +17,11 @@ from . import _lib
 
 MAX_K = 4096
 MAX_ROW = 32768
+# A few long rows in index order go through the distributed select (every CU
+# works on them) rather than one workgroup per row.
+DISTRIBUTED_MAX_ROWS = 16
+DISTRIBUTED_MIN_LENGTH = 16384  # below, one workgroup per row is as fast (three launches cost more)
+DISTRIBUTED_MAX_LENGTH = 524288
 
 
 def _device() -> torch.device:
@@ -59,7 +64,21 @@ def topk(
     indices = torch.empty((rows, k), device=matrix.device, dtype=torch.int64)
     values = torch.empty((rows, k), device=matrix.device, dtype=torch.float32) if return_values else None
     stream = _lib.stream_of(matrix)
-    if length <= MAX_ROW:
+    if (
+        not sorted
+        and row_lengths is None
+        and rows <= DISTRIBUTED_MAX_ROWS
+        and DISTRIBUTED_MIN_LENGTH <= length <= DISTRIBUTED_MAX_LENGTH
+    ):
+        from .decode import _workspace
+
+        matrix = matrix.contiguous()
+        workspace = _workspace(matrix.device, stream, rows, length)
+        _lib.call(
+            "dsa_topk_distributed", _lib.ptr(matrix), rows, length, k, _lib.ptr(indices), _lib.ptr(values),
+            _lib.ptr(workspace), workspace.numel(), stream,
+        )
+    elif length <= MAX_ROW:
         lengths = None
         if row_lengths is not None:
             lengths = row_lengths.to(device=matrix.device, dtype=torch.int32).contiguous()

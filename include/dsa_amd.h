@@ -215,6 +215,18 @@ int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t 
                     int64_t* out_indices, float* out_values, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* Exact top-k (stable_topk set, ascending index order, -1 padding) of score
+ * rows [rows, length] fp32, spread over the whole GPU: a 4096-bin histogram
+ * of every row, then the decode step's candidate gather and exact resolve.
+ * For a few long rows, where dsa_topk's one workgroup per row is bound by a
+ * single CU.  Replaces torch.topk(scores, k, sorted=False) on such rows
+ * (scripts/benchmark_progressive_dsa.py:123-169).  The workspace is the
+ * decode step's (dsa_score_topk_workspace_bytes(rows, length), zero-filled
+ * before first use and left zeroed); length <= 524288, scores 16-byte aligned. */
+int dsa_topk_distributed(const float* scores, int64_t rows, int64_t length, int64_t k,
+                         int64_t* out_indices, float* out_values, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
 int dsa_score_topk(const void* queries, const float* weights, const void* keys,
                    const float* key_scales, float* scores, int64_t batch, int64_t length,
                    int64_t k, int32_t key_dtype, int64_t* out_indices, float* out_values,

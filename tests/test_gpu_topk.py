@@ -65,6 +65,23 @@ def test_many_short_rows(device, kind, length, k) -> None:
         assert idx_index[r].tolist() == T.topk_index_order(host[r], k, n).tolist(), r
 
 
+@pytest.mark.parametrize("kind", ["normal", "ties", "neginf"])
+@pytest.mark.parametrize("rows,length,k", [(1, 16384, 2048), (3, 32768, 2048), (2, 50000, 4096), (1, 262144, 100)])
+def test_few_long_rows_distributed(device, kind, rows, length, k) -> None:
+    # Index-order top-k of a few long rows takes the distributed select; the
+    # workspace it shares with the decode step is left ready for reuse.
+    print(f"topk distributed kind={kind} rows={rows} L={length} k={k}", flush=True)
+    host = rows_for(kind, rows, length, seed=length + rows)
+    x = torch.from_numpy(host).to(device)
+    for _ in range(2):
+        idx, val = metrics.topk(x, k, sorted=False, return_values=True)
+        idx, val = idx.cpu().numpy(), val.cpu().numpy()
+        for r in range(rows):
+            want = T.topk_index_order(host[r], k)
+            assert idx[r].tolist() == want.tolist(), r
+            np.testing.assert_array_equal(val[r], host[r][want])
+
+
 def test_row_lengths_pad_short_rows(device) -> None:
     host = rows_for("ties", 4, 600, seed=3)
     lengths = torch.tensor([600, 10, 0, 257], dtype=torch.int32)
