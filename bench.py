@@ -699,6 +699,7 @@ def run_c5(args) -> None:
     sc = time_stats(score_ms)
     keys_per_step = C5_BATCH * C5_LENGTH
     score_bytes = keys_per_step * (128 + 4) + C5_BATCH * (blocks * 4 + 64 * 128 * 2 + 64 * 4)
+    progressive = c5_progressive(q, w, sets, idx, flush, device)
     achieved = score_bytes / (sc["median_us"] * 1e-6) / 1e9
     line = {
         "metric": "C5 fp8 long-context decode: G keys scored/s + % HBM roofline, B=4 L=131072 fp8 top-K2048",
@@ -721,11 +722,91 @@ def run_c5(args) -> None:
                      "algorithmic_bytes": score_bytes},
         "step": st,
         "score": sc,
+        "progressive": progressive,
         "timing": f"step: HIP events around the step's launches, 512 MiB {args.flush} flush before each, median over 100; "
                   "score: HIP events around the eager scoring launch, median over 50",
     }
     write_table(args, line, [])
     print(json.dumps(line), flush=True)
+
+
+def c5_progressive(q, w, sets, dense_idx, flush, device) -> dict:
+    """C5 with block-64 progressive pruning: per sequence the fused H8 ->
+    promote -> +56 heads kernel on the fp8 keys (direct blocks drawn as the
+    reference's direct_mask at its 32K fraction, the promotion threshold at its
+    0.10 target, benchmark_progressive_dsa.py:74-91), then the exact top-2048
+    of the four rows (dsa_topk_distributed).  Reports the step time, Recall@K
+    against the dense step's top-K, the QK reduction and the key bytes read
+    (every key row: the H8 screen reads all of a cold block's dimensions)."""
+
+    import torch
+
+    from dsa_amd import _lib, progressive_kernel as P
+
+    block = 64
+    nb = C5_LENGTH // block
+    items = []
+    for v, (keys8, scales) in enumerate(sets):
+        per = []
+        for b in range(C5_BATCH):
+            sel, rem = P.split_head_ids(P.dynamic_head_ids(w[b]).cpu())
+            sel, rem = sel.to(device), rem.to(device)
+            dgen = torch.Generator().manual_seed(SEED + 131072 + 97 * v + b)
+            direct = torch.zeros(nb, dtype=torch.bool)
+            direct[torch.randperm(nb, generator=dgen)[: round(PROG_DIRECT_FRACTIONS[32768] * nb)]] = True
+            direct = direct.to(device)
+            cold = ~direct
+            _, maxima = P.h8_block_max_hip(q[b], w[b], keys8[b], sel, cold, block_size=block, key_scales=scales[b])
+            values = maxima[cold].cpu()
+            promoted = max(1, round(0.10 * values.numel()))
+            thr = float(torch.kthvalue(values, max(1, values.numel() - promoted + 1)).values)
+            per.append({"sel": sel, "rem": rem, "direct": direct.to(torch.uint8),
+                        "thr": torch.tensor([thr], device=device), "cold": cold})
+        items.append(per)
+    out = torch.empty(C5_BATCH, C5_LENGTH, device=device)
+    acc = torch.empty(C5_BATCH, nb, device=device, dtype=torch.int8)
+    bmax = torch.empty(C5_BATCH, nb, device=device)
+    counter = torch.zeros(1, device=device, dtype=torch.int32)
+    top = torch.empty(C5_BATCH, TOPK, device=device, dtype=torch.int64)
+    ws = torch.zeros(int(_lib.query("dsa_score_topk_workspace_bytes", C5_BATCH, C5_LENGTH)), device=device,
+                     dtype=torch.uint8)
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def step(i):
+        keys8, scales = sets[i]
+        for b, it in enumerate(items[i]):
+            _lib.call("dsa_progressive_scores", q[b].data_ptr(), w[b].data_ptr(), keys8[b].data_ptr(),
+                      scales[b].data_ptr(), it["sel"].data_ptr(), it["rem"].data_ptr(), it["direct"].data_ptr(),
+                      it["thr"].data_ptr(), out[b].data_ptr(), None, acc[b].data_ptr(), bmax[b].data_ptr(),
+                      counter.data_ptr(), C5_LENGTH, block, 0, _lib.DTYPE_FP8_E4M3, stream())
+        _lib.call("dsa_topk_distributed", out.data_ptr(), C5_BATCH, C5_LENGTH, TOPK, top.data_ptr(), None,
+                  ws.data_ptr(), ws.numel(), stream())
+
+    ms = graph_times(step, len(sets), flush, 10, 100, device)
+    # Quality of the last key set: recall against the dense step on the same keys.
+    from dsa_amd import decode
+
+    keys8, scales = sets[-1]
+    dense = decode.indexer_topk(q, w, keys8, TOPK, key_scales=scales)
+    step(len(sets) - 1)
+    torch.cuda.synchronize()
+    recall, qk = [], []
+    for b in range(C5_BATCH):
+        recall.append(float(torch.isin(dense[b], top[b]).float().mean()))
+        direct_count = int(items[-1][b]["direct"].sum())
+        promoted_count = int((acc[b].bool() & items[-1][b]["cold"]).sum())
+        qk.append(P.progressive_qk_reduction(C5_LENGTH, direct_count, promoted_count, block_size=block))
+    st = time_stats(ms)
+    return {
+        "method": "fused progressive block 64 (fp8) + distributed top-2048, 4 launches + 3",
+        "step": st,
+        "g_keys_per_s": round(C5_BATCH * C5_LENGTH / (st["median_us"] * 1e-6) / 1e9, 3),
+        "recall_vs_dense": round(sum(recall) / len(recall), 5),
+        "qk_reduction": round(sum(qk) / len(qk), 4),
+        "key_bytes_skipped": 0.0,
+        "direct_fraction": PROG_DIRECT_FRACTIONS[32768],
+        "promotion_target": 0.10,
+    }
 
 
 # --------------------------------------------------------------------------
@@ -821,11 +902,11 @@ def run_progressive(args) -> None:
                       it["full"].data_ptr(), 1, ctx, _lib.DTYPE_BF16, stream())
 
         def h8(it, mask, out):
-            _lib.call("dsa_h8_block_max", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), it["sel"].data_ptr(),
+            _lib.call("dsa_h8_block_max", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), None, it["sel"].data_ptr(),
                       mask.data_ptr(), out.data_ptr(), it["maxima"].data_ptr(), ctx, PROG_BLOCK, _lib.DTYPE_BF16, stream())
 
         def masked(it, mask, out):
-            _lib.call("dsa_masked_full_scores", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), mask.data_ptr(),
+            _lib.call("dsa_masked_full_scores", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), None, mask.data_ptr(),
                       out.data_ptr(), ctx, PROG_BLOCK, _lib.DTYPE_BF16, stream())
 
         def two_pass(it):
@@ -836,7 +917,7 @@ def run_progressive(args) -> None:
 
         def fused(it, compact):
             out = it["compact"] if compact else it["fused"]
-            _lib.call("dsa_progressive_scores", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), it["sel"].data_ptr(),
+            _lib.call("dsa_progressive_scores", it["q"].data_ptr(), it["w"].data_ptr(), it["k"].data_ptr(), None, it["sel"].data_ptr(),
                       it["rem"].data_ptr(), it["direct"].data_ptr(), it["thr"].data_ptr(), out.data_ptr(),
                       it["cidx"].data_ptr() if compact else None, it["acc"].data_ptr(), it["bmax"].data_ptr(),
                       it["counter"].data_ptr(), ctx, PROG_BLOCK, int(compact), _lib.DTYPE_BF16, stream())

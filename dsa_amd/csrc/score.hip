@@ -697,16 +697,17 @@ extern "C" int dsa_score_topk(const void* queries, const float* weights, const v
 }
 
 extern "C" int dsa_h8_block_max(const void* queries, const float* weights, const void* keys,
-                                const int32_t* selected_heads, const uint8_t* cold_blocks,
-                                float* partial, float* block_max, int64_t length,
+                                const float* key_scales, const int32_t* selected_heads,
+                                const uint8_t* cold_blocks, float* partial, float* block_max, int64_t length,
                                 int32_t block_size, int32_t key_dtype, void* stream) {
   if (int st = check_block_common(queries, weights, keys, length, block_size)) return st;
   DSA_REQUIRE(selected_heads && cold_blocks && partial && block_max, "null pointer argument");
-  DSA_REQUIRE(key_dtype != kFP8E4M3, "fp8 keys need scales; use the fp16/bf16 path");
+  DSA_REQUIRE(key_dtype != kFP8E4M3 || key_scales, "fp8 keys need key_scales");
   BlockArgs a = {};
   a.q = static_cast<const uint16_t*>(queries);
   a.w = weights;
   a.keys = static_cast<const uint8_t*>(keys);
+  a.scales = key_scales;
   a.selected = selected_heads;
   a.mask = cold_blocks;
   a.out_scores = partial;
@@ -716,15 +717,16 @@ extern "C" int dsa_h8_block_max(const void* queries, const float* weights, const
 }
 
 extern "C" int dsa_masked_full_scores(const void* queries, const float* weights, const void* keys,
-                                      const uint8_t* keep_blocks, float* out, int64_t length,
-                                      int32_t block_size, int32_t key_dtype, void* stream) {
+                                      const float* key_scales, const uint8_t* keep_blocks, float* out,
+                                      int64_t length, int32_t block_size, int32_t key_dtype, void* stream) {
   if (int st = check_block_common(queries, weights, keys, length, block_size)) return st;
   DSA_REQUIRE(keep_blocks && out, "null pointer argument");
-  DSA_REQUIRE(key_dtype != kFP8E4M3, "fp8 keys need scales; use the fp16/bf16 path");
+  DSA_REQUIRE(key_dtype != kFP8E4M3 || key_scales, "fp8 keys need key_scales");
   BlockArgs a = {};
   a.q = static_cast<const uint16_t*>(queries);
   a.w = weights;
   a.keys = static_cast<const uint8_t*>(keys);
+  a.scales = key_scales;
   a.mask = keep_blocks;
   a.out_scores = out;
   a.length = (int32_t)length;
@@ -732,7 +734,7 @@ extern "C" int dsa_masked_full_scores(const void* queries, const float* weights,
 }
 
 extern "C" int dsa_progressive_scores(const void* queries, const float* weights, const void* keys,
-                                      const int32_t* selected_heads,
+                                      const float* key_scales, const int32_t* selected_heads,
                                       const int32_t* remaining_heads,
                                       const uint8_t* direct_blocks, const float* threshold,
                                       float* out_scores, int32_t* out_indices, int8_t* accepted,
@@ -744,11 +746,12 @@ extern "C" int dsa_progressive_scores(const void* queries, const float* weights,
                   accepted && block_max,
               "null pointer argument");
   DSA_REQUIRE(!compact || (out_indices && counter), "compact output needs indices and counter");
-  DSA_REQUIRE(key_dtype != kFP8E4M3, "fp8 keys need scales; use the fp16/bf16 path");
+  DSA_REQUIRE(key_dtype != kFP8E4M3 || key_scales, "fp8 keys need key_scales");
   BlockArgs a = {};
   a.q = static_cast<const uint16_t*>(queries);
   a.w = weights;
   a.keys = static_cast<const uint8_t*>(keys);
+  a.scales = key_scales;
   a.selected = selected_heads;
   a.remaining = remaining_heads;
   a.mask = direct_blocks;

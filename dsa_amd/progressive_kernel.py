@@ -113,8 +113,11 @@ def _check_gpu_inputs(
     keys: torch.Tensor,
     *,
     allow_fp32: bool = False,
-) -> None:
-    """Input contract of the reference's _check_cuda_inputs (progressive_kernel.py:349-359)."""
+    key_scales: torch.Tensor | None = None,
+) -> torch.Tensor | None:
+    """Input contract of the reference's _check_cuda_inputs (progressive_kernel.py:349-359),
+    plus fp8 e4m3fn keys with one fp32 scale per 128 keys (bf16 queries); returns
+    the scales ready for the kernels (None for fp16/bf16 keys)."""
 
     _lib.load()
     if not queries.is_cuda or not weights.is_cuda or not keys.is_cuda:
@@ -125,9 +128,19 @@ def _check_gpu_inputs(
         raise ValueError("expected keys [L,128]")
     if keys.shape[0] == 0:
         raise ValueError("expected at least one key")
+    if keys.dtype == torch.float8_e4m3fn:
+        if queries.dtype != torch.bfloat16:
+            raise ValueError("fp8 keys are scored against BF16 queries")
+        blocks = (keys.shape[0] + 127) // 128
+        if key_scales is None or key_scales.shape != (blocks,):
+            raise ValueError(f"fp8 keys need key_scales [{blocks}] (one per 128 keys)")
+        return key_scales.to(device=keys.device, dtype=torch.float32).contiguous()
+    if key_scales is not None:
+        raise ValueError("key_scales apply to fp8 keys only")
     allowed = {torch.float16, torch.bfloat16} | ({torch.float32} if allow_fp32 else set())
     if queries.dtype not in allowed or keys.dtype != queries.dtype:
         raise ValueError("queries and keys must share FP16/BF16 dtype")
+    return None
 
 
 def _check_block_size(block_size: int) -> None:
@@ -158,15 +171,17 @@ def full_scores_hip(
     keys: torch.Tensor,
     *,
     block_size: int = 64,
+    key_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Dense 64-head indexer score of every key, fp32 ``[L]``.
 
     Reference: progressive_kernel.py:362-375.  ``block_size`` only selects the
     reference's launch tiling; it is validated and otherwise ignored.  fp32
-    queries and keys are accepted as well (fp32 MFMA path).
+    queries and keys are accepted as well (fp32 MFMA path), and fp8 e4m3fn keys
+    with ``key_scales`` (one fp32 scale per 128 keys) against bf16 queries.
     """
 
-    _check_gpu_inputs(queries, weights, keys, allow_fp32=True)
+    scales = _check_gpu_inputs(queries, weights, keys, allow_fp32=True, key_scales=key_scales)
     _check_block_size(block_size)
     queries = queries.contiguous()
     keys = keys.contiguous()
@@ -174,7 +189,7 @@ def full_scores_hip(
     output = torch.empty(keys.shape[0], device=keys.device, dtype=torch.float32)
     _lib.call(
         "dsa_full_scores",
-        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), None, _lib.ptr(output),
+        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(scales), _lib.ptr(output),
         1, keys.shape[0], _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
     )
     return output
@@ -188,13 +203,15 @@ def h8_block_max_hip(
     cold_blocks: torch.Tensor,
     *,
     block_size: int = 64,
+    key_scales: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """H8 partial scores (-inf outside cold blocks) and per-block maxima.
 
-    Reference: progressive_kernel.py:378-404.
+    Reference: progressive_kernel.py:378-404 (fp8 keys take ``key_scales`` as
+    :func:`full_scores_hip`).
     """
 
-    _check_gpu_inputs(queries, weights, keys)
+    scales = _check_gpu_inputs(queries, weights, keys, key_scales=key_scales)
     _check_block_size(block_size)
     block_count = math.ceil(keys.shape[0] / block_size)
     if cold_blocks.numel() != block_count:
@@ -214,7 +231,7 @@ def h8_block_max_hip(
     maxima = torch.empty(block_count, device=keys.device, dtype=torch.float32)
     _lib.call(
         "dsa_h8_block_max",
-        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(selected), _lib.ptr(cold),
+        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(scales), _lib.ptr(selected), _lib.ptr(cold),
         _lib.ptr(partial), _lib.ptr(maxima), keys.shape[0], block_size,
         _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
     )
@@ -228,13 +245,14 @@ def masked_full_scores_hip(
     keep_blocks: torch.Tensor,
     *,
     block_size: int = 64,
+    key_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Full scores on kept blocks, -inf elsewhere (rejected blocks read no keys).
 
-    Reference: progressive_kernel.py:407-424.
+    Reference: progressive_kernel.py:407-424 (fp8 keys take ``key_scales``).
     """
 
-    _check_gpu_inputs(queries, weights, keys)
+    scales = _check_gpu_inputs(queries, weights, keys, key_scales=key_scales)
     _check_block_size(block_size)
     block_count = math.ceil(keys.shape[0] / block_size)
     if keep_blocks.numel() != block_count:
@@ -246,7 +264,7 @@ def masked_full_scores_hip(
     output = torch.empty(keys.shape[0], device=keys.device, dtype=torch.float32)
     _lib.call(
         "dsa_masked_full_scores",
-        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(keep), _lib.ptr(output),
+        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(scales), _lib.ptr(keep), _lib.ptr(output),
         keys.shape[0], block_size, _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
     )
     return output
@@ -263,6 +281,7 @@ def progressive_scores_hip(
     block_size: int = 64,
     compact: bool = False,
     remaining_heads: torch.Tensor | None = None,
+    key_scales: torch.Tensor | None = None,
 ) -> ProgressiveResult:
     """Fused H8 -> promote -> +56 heads scoring.
 
@@ -270,10 +289,11 @@ def progressive_scores_hip(
     count is the exact number of accepted keys (an atomic add of each accepted
     block's valid-key count), so a ragged last block never exposes unwritten
     slots; blocks appear in completion order, keys inside a block in address
-    order.
+    order.  fp8 keys take ``key_scales``; the promotion threshold is compared
+    with scaled H8 maxima.
     """
 
-    _check_gpu_inputs(queries, weights, keys)
+    scales = _check_gpu_inputs(queries, weights, keys, key_scales=key_scales)
     _check_block_size(block_size)
     if remaining_heads is None:
         selected, remaining = split_head_ids(selected_heads)
@@ -302,7 +322,7 @@ def progressive_scores_hip(
     indices = torch.empty(length, device=keys.device, dtype=torch.int32) if compact else None
     _lib.call(
         "dsa_progressive_scores",
-        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(selected),
+        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(scales), _lib.ptr(selected),
         _lib.ptr(remaining), _lib.ptr(direct), _lib.ptr(threshold_tensor), _lib.ptr(scores),
         _lib.ptr(indices), _lib.ptr(accepted), _lib.ptr(block_max), _lib.ptr(counter),
         length, block_size, int(compact), _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
@@ -325,17 +345,19 @@ def two_pass_scores_hip(
     threshold: float | torch.Tensor,
     *,
     block_size: int = 64,
+    key_scales: torch.Tensor | None = None,
 ) -> ProgressiveResult:
     """H8 pass, promotion mask, then masked full rerank (three launches).
 
-    Reference: progressive_kernel.py:478-497.
+    Reference: progressive_kernel.py:478-497 (fp8 keys take ``key_scales``).
     """
 
-    _check_gpu_inputs(queries, weights, keys)
+    _check_gpu_inputs(queries, weights, keys, key_scales=key_scales)
     _check_block_size(block_size)
     direct = _mask_bytes(direct_full_blocks, keys.device)
     cold = (direct == 0) if direct.dtype != torch.bool else ~direct
-    _, maxima = h8_block_max_hip(queries, weights, keys, selected_heads, cold, block_size=block_size)
+    _, maxima = h8_block_max_hip(queries, weights, keys, selected_heads, cold, block_size=block_size,
+                                 key_scales=key_scales)
     threshold_tensor = torch.as_tensor(threshold, device=keys.device, dtype=torch.float32).reshape(1)
     accepted = torch.empty(maxima.numel(), device=keys.device, dtype=torch.int8)
     _lib.call(
@@ -343,7 +365,7 @@ def two_pass_scores_hip(
         _lib.ptr(direct), _lib.ptr(maxima), _lib.ptr(threshold_tensor), _lib.ptr(accepted),
         maxima.numel(), _lib.stream_of(keys),
     )
-    scores = masked_full_scores_hip(queries, weights, keys, accepted, block_size=block_size)
+    scores = masked_full_scores_hip(queries, weights, keys, accepted, block_size=block_size, key_scales=key_scales)
     return ProgressiveResult(scores, accepted, maxima)
 
 

@@ -104,12 +104,15 @@ int dsa_route_heads(const float* weights, int64_t rows, int64_t heads, int64_t w
  * progressive_kernel.py:218-246 (_h8_block_max_kernel).
  *
  *   selected_heads [8] int32 device array, cold_blocks [ceil(L/bs)] bytes.
+ *   key_scales: fp8 e4m3fn keys only (else NULL), one fp32 scale per 128 keys
+ *   (as dsa_full_scores); every score, partial or full, is scaled.  The same
+ *   holds for dsa_masked_full_scores and dsa_progressive_scores.
  *   partial[s] = sum over the 8 selected heads where the block is cold, else
  *   -inf; block_max[b] = max of partial over the block (-inf if not cold).
  * ------------------------------------------------------------------------ */
 int dsa_h8_block_max(const void* queries, const float* weights, const void* keys,
-                     const int32_t* selected_heads, const uint8_t* cold_blocks, float* partial,
-                     float* block_max, int64_t length, int32_t block_size, int32_t key_dtype,
+                     const float* key_scales, const int32_t* selected_heads, const uint8_t* cold_blocks,
+                     float* partial, float* block_max, int64_t length, int32_t block_size, int32_t key_dtype,
                      void* stream);
 
 /* ------------------------------------------------------------------------
@@ -117,7 +120,7 @@ int dsa_h8_block_max(const void* queries, const float* weights, const void* keys
  * Replaces progressive_kernel.py:407-424 (masked_full_scores_triton).
  * ------------------------------------------------------------------------ */
 int dsa_masked_full_scores(const void* queries, const float* weights, const void* keys,
-                           const uint8_t* keep_blocks, float* out, int64_t length,
+                           const float* key_scales, const uint8_t* keep_blocks, float* out, int64_t length,
                            int32_t block_size, int32_t key_dtype, void* stream);
 
 /* ------------------------------------------------------------------------
@@ -139,7 +142,7 @@ int dsa_masked_full_scores(const void* queries, const float* weights, const void
  *                 in address order).
  * ------------------------------------------------------------------------ */
 int dsa_progressive_scores(const void* queries, const float* weights, const void* keys,
-                           const int32_t* selected_heads, const int32_t* remaining_heads,
+                           const float* key_scales, const int32_t* selected_heads, const int32_t* remaining_heads,
                            const uint8_t* direct_blocks, const float* threshold,
                            float* out_scores, int32_t* out_indices, int8_t* accepted,
                            float* block_max, int32_t* counter, int64_t length,

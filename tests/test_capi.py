@@ -40,7 +40,7 @@ def test_invalid_arguments_are_rejected_without_a_device() -> None:
     assert lib.dsa_full_scores(None, None, None, None, None, 1, 16, 2, None) == 1
     fake = ctypes.c_void_p(256)
     # bad block size is reported before any launch
-    assert lib.dsa_masked_full_scores(fake, fake, fake, fake, fake, 64, 48, 2, None) == 1
+    assert lib.dsa_masked_full_scores(fake, fake, fake, None, fake, fake, 64, 48, 2, None) == 1
     assert b"block_size" in lib.dsa_last_error()
     # unsupported dtype
     assert lib.dsa_score_queries(fake, 8192, fake, 64, None, 0, 64, fake, 16, 1, None, 0, fake, 16, 1, 16, -1, 0, None) == 1

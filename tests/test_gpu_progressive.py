@@ -132,6 +132,50 @@ def test_kernels_match_oracle_semantics(device, block_size, length) -> None:
     assert torch.equal(compact.scores.cpu(), result.scores.cpu()[idx])
 
 
+@pytest.mark.parametrize("block_size", [16, 64, 128])
+def test_fp8_keys_match_oracle_on_dequantised_keys(device, block_size) -> None:
+    # fp8 e4m3fn keys with one fp32 scale per 128 keys: every kernel's scores
+    # (partial or full) equal the oracle's on the dequantised keys, since the
+    # ReLU commutes with a non-negative scale.
+    print(f"progressive fp8 bs={block_size}", flush=True)
+    length = 1000
+    gen = torch.Generator().manual_seed(7 * block_size)
+    q = (torch.randn(64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(64, generator=gen) / 8
+    raw = torch.randn(length, 128, generator=gen)
+    nscale = math.ceil(length / 128)
+    scales = torch.stack([raw[j * 128 : (j + 1) * 128].abs().max() / 448 for j in range(nscale)])
+    k8 = (raw / scales.repeat_interleave(128)[:length, None]).to(torch.float8_e4m3fn)
+    deq = S.dequantize_fp8_blocks(k8[None], scales[None])[0]
+    blocks = math.ceil(length / block_size)
+    direct = torch.rand(blocks, generator=gen) < 0.3
+    selected, remaining = split_head_ids(dynamic_head_ids(w))
+    qn, wn = q.float().numpy(), w.numpy()
+    _, h8_max = S.kernel_h8_block_max(qn, wn, deq, selected.numpy(), (~direct).numpy(), block_size)
+    finite = np.sort(h8_max[np.isfinite(h8_max)])
+    i = finite.size // 2 - 1
+    threshold = float(0.5 * (finite[i] + finite[i + 1]))
+    assert finite[i + 1] - finite[i] > 1e-4 * max(1.0, abs(threshold))
+    ref, ref_acc, _ = S.kernel_progressive(qn, wn, deq, selected.numpy(), remaining.numpy(), direct.numpy(), threshold, block_size)
+    scale = S.abs_weight_scale(qn, deq, wn)
+    dq, dw, dk, ds = q.to(device), w.to(device), k8.to(device), scales.to(device)
+
+    full = full_scores_triton(dq, dw, dk, key_scales=ds).cpu().double().numpy()
+    ref_full = S.relu_index_score(qn, deq, wn)
+    assert np.all(np.abs(full - ref_full) <= 1e-5 * scale + 1e-6)
+    result = progressive_scores_triton(dq, dw, dk, selected, direct, threshold, block_size=block_size, key_scales=ds)
+    assert result.accepted_blocks.cpu().bool().numpy().tolist() == ref_acc.tolist()
+    got = result.scores.cpu().double().numpy()
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * scale[fin] + 1e-6)
+    two = two_pass_scores_triton(dq, dw, dk, selected, direct, threshold, block_size=block_size, key_scales=ds)
+    assert torch.equal(two.accepted_blocks.cpu(), result.accepted_blocks.cpu())
+    torch.testing.assert_close(two.scores.cpu(), result.scores.cpu(), rtol=1e-6, atol=1e-6)
+    with pytest.raises(ValueError, match="key_scales"):
+        progressive_scores_triton(dq, dw, dk, selected, direct, threshold, block_size=block_size)
+
+
 def test_rejects_bad_masks_and_heads(device) -> None:
     queries, weights, keys = cuda_inputs(128, device)
     with pytest.raises(ValueError):
