@@ -114,6 +114,20 @@ __device__ __forceinline__ void buffer_store_u64(BufferRsrc rsrc, uint32_t offse
   __builtin_amdgcn_raw_buffer_store_b64(parts, rsrc, (int)offset, 0, 0);
 }
 
+// Kernel arguments live in the kernarg segment and are fetched by scalar loads
+// that the compiler issues next to their first use, so a prologue with
+// branches waits for several dependent round trips before its first vector
+// load.  Naming the arguments here materialises them in SGPRs at this point:
+// their loads issue together and complete in one round trip.
+template <class T>
+__device__ __forceinline__ void in_sgpr(const T& v) {
+  asm volatile("" ::"s"(v));
+}
+template <class... T>
+__device__ __forceinline__ void args_in_sgprs(const T&... v) {
+  (in_sgpr(v), ...);
+}
+
 // ReLU as a signed-integer max on the float's bits: negative values (sign bit
 // set) become +0.0, non-negative values pass unchanged.  One VALU op, where
 // fmaxf(x, 0) costs two (NaN quieting).

@@ -129,6 +129,12 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
   // kHist: also count every valid score into the sequence's histogram of the
   // top 12 bits of its order-preserving key (input of the distributed top-k).
   __shared__ uint32_t hist[kHist ? kSelectBins : 1];
+  args_in_sgprs(a.q, a.q_stride, a.w, a.w_stride, a.keys, a.key_stride, a.queries_per_keyset, a.out,
+                a.out_stride, a.length, a.causal_offset, a.units_per_wg, a.wgs_per_seq, a.total_wgs,
+                gridDim.x);
+  if constexpr (kHist) args_in_sgprs(a.hist);
+  if constexpr (KF::kScaled) args_in_sgprs(a.scales, a.scale_stride);
+  if constexpr (kGather) args_in_sgprs(a.head_ids, a.ids_stride, a.head_count);
   const int lane = threadIdx.x & 63;
   // Wave-uniform control flow: every loop bound below lives in SGPRs.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -136,11 +142,12 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
   const int g = lane >> 4;
   // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so
   // that consecutive logical workgroups (one sequence's chunks) share an XCD
-  // and its L2 fetches that sequence's query block once.
-  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
-  if (logical >= a.total_wgs) return;
-  const int64_t seq = logical / a.wgs_per_seq;
-  const int chunk = (int)(logical % a.wgs_per_seq);
+  // and its L2 fetches that sequence's query block once.  (The launch keeps
+  // the grid below 2^31 workgroups.)
+  const uint32_t logical = (blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
+  if (logical >= (uint64_t)a.total_wgs) return;
+  const int64_t seq = logical / (uint32_t)a.wgs_per_seq;
+  const int chunk = (int)(logical % (uint32_t)a.wgs_per_seq);
   const int L = a.length;
   const int64_t keyset = seq / a.queries_per_keyset;
   int valid = L;
@@ -166,17 +173,23 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
   for (int uu = u_first + u_stride * count; uu < u_end; uu += u_stride)
     buffer_store_f32(out, (uint32_t)(uu * 64 + lane) * 4, -__builtin_inff());
   if constexpr (kHist) {
-    for (int i = threadIdx.x; i < kSelectBins; i += 256) hist[i] = 0;
+#pragma unroll
+    for (int j = 0; j < kSelectBins / 256; ++j) hist[threadIdx.x + 256 * j] = 0;
     __syncthreads();
     if (count > 0)
       dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
                                                out, scales, hist);
     __syncthreads();
+    // All sixteen LDS reads first, then the atomics for the bins in use: one
+    // LDS round trip instead of one per bin.
     uint32_t* ghist = a.hist + seq * kSelectBins;
-    for (int i = threadIdx.x; i < kSelectBins; i += 256) {
-      const uint32_t n = hist[i];
-      if (n) __hip_atomic_fetch_add(&ghist[i], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    uint32_t n[kSelectBins / 256];
+#pragma unroll
+    for (int j = 0; j < kSelectBins / 256; ++j) n[j] = hist[threadIdx.x + 256 * j];
+#pragma unroll
+    for (int j = 0; j < kSelectBins / 256; ++j)
+      if (n[j])
+        __hip_atomic_fetch_add(&ghist[threadIdx.x + 256 * j], n[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   if (count == 0) return;
