@@ -141,7 +141,8 @@ def main() -> None:
     def score(keys):
         _lib.call(
             "dsa_score_hist", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(),
-            BATCH, LENGTH, _lib.DTYPE_BF16, workspace.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream,
+            BATCH, LENGTH, TOPK, _lib.DTYPE_BF16, workspace.data_ptr(), ws_bytes,
+            torch.cuda.current_stream().cuda_stream,
         )
 
     def select():
@@ -671,7 +672,7 @@ def run_c5(args) -> None:
     def score(i):
         keys8, scales = sets[i]
         _lib.call("dsa_score_hist", q.data_ptr(), w.data_ptr(), keys8.data_ptr(), scales.data_ptr(), scores.data_ptr(),
-                  C5_BATCH, C5_LENGTH, _lib.DTYPE_FP8_E4M3, workspace.data_ptr(), ws_bytes,
+                  C5_BATCH, C5_LENGTH, TOPK, _lib.DTYPE_FP8_E4M3, workspace.data_ptr(), ws_bytes,
                   torch.cuda.current_stream().cuda_stream)
 
     def select(i):

@@ -9,6 +9,7 @@
 #include "indexer.hpp"
 #include "select.hpp"
 #include "status.hpp"
+#include "waveops.hpp"
 
 namespace dsa {
 namespace {
@@ -49,6 +50,10 @@ struct DenseArgs {
   int32_t wgs_per_seq;
   int64_t total_wgs;  // the launch pads the grid to a multiple of kXcds
   uint32_t* hist;  // [sequences][kSelectBins] score histogram (kHist only)
+  // Candidate lists (kLists only): list (s, chunk) at lists[s * length + chunk * chunk_keys].
+  uint64_t* lists;
+  uint32_t* list_meta;  // [sequences][kMaxListChunks][2]: length, lowest bin listed
+  int32_t list_quota;
 };
 
 // Keys past the valid range read as zeros (buffer bounds check).  Scaled
@@ -63,12 +68,12 @@ __device__ __forceinline__ void dense_load_unit(BufferRsrc keys, int u, int r, i
   if constexpr (KF::kScaled) scale = scales[min(u * 64, L - 1) >> 7];
 }
 
-template <class Tag, class KF, int M, bool kHist>
+template <class Tag, class KF, int M, bool kHist, bool kLists>
 __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], const float (&wr)[M][4],
                                                    const uint4 (&buf)[4][KF::kRaw], int u,
                                                    int valid, int L, int lane, int g,
                                                    float scale, BufferRsrc out,
-                                                   uint32_t* hist) {
+                                                   uint32_t* hist, float* chunk_scores, int chunk_base) {
   float s[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, M, KF>(qa, wr, buf[t]);
@@ -77,6 +82,7 @@ __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], cons
   if constexpr (KF::kScaled) keep *= scale;
   // Stores past L are dropped by the buffer bounds check.
   buffer_store_f32(out, (uint32_t)key * 4, key < valid ? keep : -__builtin_inff());
+  if constexpr (kLists) chunk_scores[key - chunk_base] = keep;
   if constexpr (kHist)
     __hip_atomic_fetch_add(&hist[float_to_ordered(keep) >> 20], key < valid ? 1u : 0u,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -84,11 +90,11 @@ __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], cons
 
 // The streaming part of dense_scores_kernel: query block into registers, then
 // the two-buffer unit loop.
-template <class Tag, class KF, int M, bool kGather, bool kHist>
+template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists>
 __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int u_first, int u_stride,
                                              int64_t seq, int valid, int L, int lane, int r, int g,
                                              BufferRsrc keys, BufferRsrc out, const float* scales,
-                                             uint32_t* hist) {
+                                             uint32_t* hist, float* chunk_scores, int chunk_base) {
   uint4 qa[M][4];
   float wr[M][4];
   if constexpr (kGather) {
@@ -118,21 +124,51 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
       if (i + s >= count) break;
       dense_load_unit<KF>(keys, min(u + u_stride * (s + NB - 1), u_last), r, g, buf[(s + NB - 1) % NB], scales, L,
                           scale[(s + NB - 1) % NB]);
-      dense_compute_unit<Tag, KF, M, kHist>(qa, wr, buf[s], u + u_stride * s, valid, L, lane, g, scale[s], out,
-                                            hist);
+      dense_compute_unit<Tag, KF, M, kHist, kLists>(qa, wr, buf[s], u + u_stride * s, valid, L, lane, g,
+                                                    scale[s], out, hist, chunk_scores, chunk_base);
     }
   }
 }
 
-template <class Tag, class KF, int M, bool kGather, bool kHist>
+// A scoring workgroup's candidate list: thread t takes keys [t * per, t * per
+// + per) of the chunk (per <= P), all read from LDS at once, and writes those
+// in bins >= lbin in index order at offsets from one block scan.
+template <int P>
+__device__ __forceinline__ uint32_t emit_list(const float* chunk_scores, int per, int n_chunk, int chunk_base,
+                                              uint32_t lbin, uint64_t* list, uint32_t* wsum) {
+  const int i0 = (int)threadIdx.x * per;
+  uint32_t key[P];
+  uint32_t takes = 0;  // bit e: key e is listed
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    key[e] = float_to_ordered(chunk_scores[e < per ? i0 + e : i0]);
+    if (e < per && i0 + e < n_chunk && (key[e] >> 20) >= lbin) takes |= 1u << e;
+  }
+  uint32_t listed;
+  uint32_t slot = block_excl_scan<4>((uint32_t)__builtin_popcount(takes), wsum, listed);
+  if (takes) {
+#pragma unroll
+    for (int e = 0; e < P; ++e)
+      if (takes & (1u << e)) list[slot++] = select_composite(key[e], (uint32_t)(chunk_base + i0 + e));
+  }
+  return listed;
+}
+
+template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists>
 __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
-  // kHist: also count every valid score into the sequence's histogram of the
-  // top 12 bits of its order-preserving key (input of the distributed top-k).
+  // kHist: also count every valid score into a histogram of the top 12 bits
+  // of its order-preserving key; without kLists it is added to the sequence's
+  // histogram (input of the distributed top-k).  kLists: the workgroup keeps
+  // its chunk's scores in LDS (dynamic shared memory, chunk_keys floats) and
+  // writes its candidate list instead (input of the list top-k).
+  static_assert(kHist || !kLists, "candidate lists come with the histogram");
   __shared__ uint32_t hist[kHist ? kSelectBins : 1];
+  extern __shared__ float chunk_scores[];
   args_in_sgprs(a.q, a.q_stride, a.w, a.w_stride, a.keys, a.key_stride, a.queries_per_keyset, a.out,
                 a.out_stride, a.length, a.causal_offset, a.units_per_wg, a.wgs_per_seq, a.total_wgs,
                 gridDim.x);
-  if constexpr (kHist) args_in_sgprs(a.hist);
+  if constexpr (kHist && !kLists) args_in_sgprs(a.hist);
+  if constexpr (kLists) args_in_sgprs(a.lists, a.list_meta, a.list_quota);
   if constexpr (KF::kScaled) args_in_sgprs(a.scales, a.scale_stride);
   if constexpr (kGather) args_in_sgprs(a.head_ids, a.ids_stride, a.head_count);
   const int lane = threadIdx.x & 63;
@@ -176,10 +212,49 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
 #pragma unroll
     for (int j = 0; j < kSelectBins / 256; ++j) hist[threadIdx.x + 256 * j] = 0;
     __syncthreads();
+    const int chunk_keys = a.units_per_wg * 64;
+    const int chunk_base = chunk * chunk_keys;
     if (count > 0)
-      dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
-                                               out, scales, hist);
+      dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g,
+                                                       keys, out, scales, hist, chunk_scores, chunk_base);
     __syncthreads();
+    if constexpr (kLists) {
+      // The chunk's list: every valid key whose bin is at least the bin of
+      // the chunk's list_quota-th largest score (all valid keys when the
+      // chunk has no more), in index order.
+      __shared__ uint32_t s_list_bin;
+      __shared__ __align__(16) uint32_t s_list_wsum[4];
+      const int n_chunk = min(chunk_keys, valid - chunk_base);
+      if (wave == 0) {
+        const Locate t = wave_locate<kSelectBins / kWave>(hist, (uint32_t)a.list_quota, true);
+        if (lane == 0) s_list_bin = t.digit == kNoBin ? 0u : t.digit;
+      }
+      __syncthreads();
+      const uint32_t lbin = s_list_bin;
+      uint64_t* list = a.lists + seq * (int64_t)L + chunk_base;
+      uint32_t listed;
+      switch (chunk_keys / 256) {  // keys per thread, 1..32
+        case 1: listed = emit_list<1>(chunk_scores, 1, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
+        case 2: listed = emit_list<2>(chunk_scores, 2, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
+        case 3:
+        case 4: listed = emit_list<4>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
+          break;
+        case 5: case 6: case 7:
+        case 8: listed = emit_list<8>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
+          break;
+        case 9: case 10: case 11: case 12: case 13: case 14: case 15:
+        case 16: listed = emit_list<16>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
+          break;
+        default: listed = emit_list<32>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
+          break;
+      }
+      if (threadIdx.x == 0) {
+        uint32_t* meta = a.list_meta + 2 * (seq * kMaxListChunks + chunk);
+        meta[0] = listed;
+        meta[1] = lbin;
+      }
+      return;
+    }
     // All sixteen LDS reads first, then the atomics for the bins in use: one
     // LDS round trip instead of one per bin.
     uint32_t* ghist = a.hist + seq * kSelectBins;
@@ -193,8 +268,8 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
     return;
   }
   if (count == 0) return;
-  dense_stream<Tag, KF, M, kGather, kHist>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
-                                           out, scales, hist);
+  dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
+                                                   out, scales, hist, chunk_scores, 0);
 }
 
 
@@ -491,27 +566,17 @@ __global__ void promote_blocks_kernel(const uint8_t* direct, const float* block_
 // ---------------------------------------------------------------------------
 // Host-side launch helpers.
 // ---------------------------------------------------------------------------
-int units_per_workgroup(int64_t sequences, int64_t length, int64_t target_wgs) {
-  // About target_wgs / 256 workgroups of four waves per CU: every wave then
-  // streams several units, so its query-block load and pipeline fill are paid
-  // once, while at least four units (one per wave) stay in each workgroup.
-  const int64_t units = (length + 63) / 64;
-  int64_t per = (units * sequences + target_wgs - 1) / target_wgs;
-  per = per < 4 ? 4 : per;
-  per = (per + 3) / 4 * 4;
-  return (int)per;
-}
-
-template <class Tag, class KF, int M, bool kGather, bool kHist = false>
+template <class Tag, class KF, int M, bool kGather, bool kHist = false, bool kLists = false>
 int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
   const int64_t units = (a.length + 63) / 64;
-  a.units_per_wg = units_per_workgroup(sequences, a.length, 256);
+  a.units_per_wg = dense_units_per_wg(sequences, a.length);
   a.wgs_per_seq = (int32_t)((units + a.units_per_wg - 1) / a.units_per_wg);
   a.total_wgs = sequences * a.wgs_per_seq;
   const int64_t grid = (a.total_wgs + kXcds - 1) / kXcds * kXcds;
   if (grid > 0x7fffffffLL) return fail(DSA_STATUS_INVALID_ARGUMENT, "problem too large");
-  hipLaunchKernelGGL((dense_scores_kernel<Tag, KF, M, kGather, kHist>), dim3((unsigned)grid),
-                     dim3(256), 0, stream, a);
+  const size_t lds = kLists ? (size_t)a.units_per_wg * 64 * sizeof(float) : 0;
+  hipLaunchKernelGGL((dense_scores_kernel<Tag, KF, M, kGather, kHist, kLists>), dim3((unsigned)grid),
+                     dim3(256), lds, stream, a);
   return check_launch("dense_scores_kernel");
 }
 
@@ -655,12 +720,13 @@ extern "C" int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length)
 
 extern "C" int dsa_score_hist(const void* queries, const float* weights, const void* keys,
                               const float* key_scales, float* scores, int64_t batch,
-                              int64_t length, int32_t key_dtype, void* workspace,
+                              int64_t length, int64_t k, int32_t key_dtype, void* workspace,
                               int64_t workspace_bytes, void* stream) {
   DSA_REQUIRE(queries && weights && keys && scores, "null pointer argument");
   DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(length > 0 && length <= int64_t(kSelectChunk) * kMaxSelectChunks,
               "length %lld outside [1, %d]", (long long)length, kSelectChunk * kMaxSelectChunks);
+  DSA_REQUIRE(k > 0 && k <= (int64_t(1) << 27), "k=%lld out of range", (long long)k);
   DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16 || key_dtype == kFP8E4M3,
               "dsa_score_hist takes fp16/bf16/fp8 keys (got %d)", key_dtype);
   DSA_REQUIRE(key_dtype != kFP8E4M3 || key_scales, "fp8 keys need key_scales");
@@ -690,6 +756,19 @@ extern "C" int dsa_score_hist(const void* queries, const float* weights, const v
   a.causal_offset = -1;
   a.hist = ws.hist;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const ListPlan plan = list_plan(batch, length, k);
+  if (plan.on) {
+    // Each scoring workgroup writes its chunk's candidate list; the row
+    // histogram stays untouched (and zero).
+    a.lists = ws.cand;
+    a.list_meta = ws.list_meta;
+    a.list_quota = plan.quota;
+    switch (key_dtype) {
+      case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true, true>(a, batch, s);
+      case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true, true>(a, batch, s);
+      default: return launch_dense_m<Bf16Tag, KeysFP8, 4, false, true, true>(a, batch, s);
+    }
+  }
   switch (key_dtype) {
     case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true>(a, batch, s);
     case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true>(a, batch, s);
@@ -702,7 +781,7 @@ extern "C" int dsa_score_topk(const void* queries, const float* weights, const v
                               int64_t length, int64_t k, int32_t key_dtype, int64_t* out_indices,
                               float* out_values, void* workspace, int64_t workspace_bytes,
                               void* stream) {
-  if (int st = dsa_score_hist(queries, weights, keys, key_scales, scores, batch, length, key_dtype,
+  if (int st = dsa_score_hist(queries, weights, keys, key_scales, scores, batch, length, k, key_dtype,
                               workspace, workspace_bytes, stream))
     return st;
   return dsa_select_topk(scores, batch, length, k, out_indices, out_values, workspace,

@@ -42,8 +42,63 @@ struct SelectArgs {
   float* out_val;    // [rows, k] or null
 };
 
-__device__ __forceinline__ uint64_t composite(uint32_t key, int pos) {
-  return (uint64_t(key) << 32) | (uint64_t)(~(uint32_t)pos);
+__device__ __forceinline__ uint64_t composite(uint32_t key, int pos) { return select_composite(key, (uint32_t)pos); }
+
+// Radix select of the want-th largest composite among the n entries at(i)
+// whose top 12 bits equal `bin`: 11-bit digits of bits 51..8, then bits
+// 7..0.  All waves count a digit, wave 0 locates the digit holding the cut
+// while the other waves clear the other counter buffer, and a digit with a
+// single entry ends the search (that entry was recorded while counting).
+// digits[0] must be zero on entry; both buffers are left dirty.
+struct RadixShared {
+  uint64_t last[kDigitBins];  // an entry of each digit (the only one when its count is 1)
+  uint32_t digit, rem, count;
+};
+
+template <class At>
+__device__ __forceinline__ uint64_t radix_cut(uint32_t bin, uint32_t want, uint32_t n, At at,
+                                              uint32_t (*digits)[kDigitBins], RadixShared& rs) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = lane_id();
+  const uint32_t wave = tid / kWave;
+  uint64_t prefix = uint64_t(bin) << 52;
+  uint64_t mask = uint64_t(0xfff) << 52;
+  uint32_t rem = want;
+#pragma unroll 1
+  for (int pass = 0; pass < 5; ++pass) {
+    const int shift = pass < 4 ? 41 - 11 * pass : 0;
+    const uint32_t dmask = pass < 4 ? 0x7ffu : 0xffu;
+    uint32_t* dig = digits[pass & 1];
+    for (uint32_t i = tid; i < n; i += kSelThreads) {
+      const uint64_t x = at(i);
+      if ((x & mask) == prefix) {
+        const uint32_t d = (uint32_t)(x >> shift) & dmask;
+        __hip_atomic_fetch_add(&dig[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        rs.last[d] = x;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const Locate t = wave_locate<kDigitBins / kWave>(dig, rem, false);
+      if (lane == 0) {
+        rs.digit = t.digit;
+        rs.rem = t.rem;
+        rs.count = t.count;
+      }
+    } else {
+      uint32_t* next = digits[(pass + 1) & 1];
+      for (uint32_t i = tid - kWave; i < (uint32_t)kDigitBins; i += kSelThreads - kWave) next[i] = 0;
+    }
+    __syncthreads();
+    if (rs.digit == kNoBin) break;  // unreachable for consistent counts
+    prefix |= uint64_t(rs.digit) << shift;
+    mask |= uint64_t(dmask) << shift;
+    rem = rs.rem;
+    if (rs.count == 1) return rs.last[rs.digit];  // the one entry carrying the prefix
+    // rs is rewritten only after the next pass's first barrier, which every
+    // thread reaches after reading it here.
+  }
+  return prefix;  // all 64 bits fixed
 }
 
 // Same XCD-aware renumbering as the scoring kernel: with a grid that is a
@@ -134,19 +189,17 @@ __global__ __launch_bounds__(kSelThreads) void select_gather_kernel(SelectArgs a
 // One round trip fetches this chunk's scores, the row's meta, the per-chunk
 // counts (wave 0 scans them) and the first slots of every chunk's candidate
 // slice; the candidates are staged in LDS.  The exact cut is a radix select
-// over (key, ~position) composites: all waves count 11-bit digits, wave 0
-// locates the digit holding the cut, and a digit with a single candidate ends
-// it (that candidate was recorded while counting).  The candidates of the
+// over (key, ~position) composites (radix_cut).  The candidates of the
 // earlier chunks at or above the cut and this chunk's chosen scores share one
 // block scan.  Five barriers in the common case.
 // ---------------------------------------------------------------------------
 struct ResolveShared {
   uint64_t cands[kCandCapacity];
-  uint64_t last[kDigitBins];            // a candidate of each digit (the only one when its count is 1)
+  RadixShared radix;
   uint32_t digits[2][kDigitBins];
   uint32_t base[kMaxSelectChunks + 1];  // candidate prefix over the row's chunks
   uint32_t wsum[2][kSelWaves];
-  uint32_t digit, rem, count, offset, crowd, overflow;
+  uint32_t offset, crowd, overflow;
 };
 
 __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs a) {
@@ -264,52 +317,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs 
       }
       __syncthreads();
     }
-    // Radix select of the want-th largest composite: the top 12 bits are the
-    // bin; 11-bit digits of bits 51..8, then bits 7..0.
-    uint64_t prefix = uint64_t(bin) << 52;
-    uint64_t mask = uint64_t(0xfff) << 52;
-    uint32_t rem = want;
-    bool done = false;
-#pragma unroll 1
-    for (int pass = 0; pass < 5; ++pass) {
-      const int shift = pass < 4 ? 41 - 11 * pass : 0;
-      const uint32_t dmask = pass < 4 ? 0x7ffu : 0xffu;
-      uint32_t* dig = sh.digits[pass & 1];
-      for (uint32_t i = tid; i < crowd; i += kSelThreads) {
-        const uint64_t x = cand_at(i);
-        if ((x & mask) == prefix) {
-          const uint32_t d = (uint32_t)(x >> shift) & dmask;
-          __hip_atomic_fetch_add(&dig[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          sh.last[d] = x;
-        }
-      }
-      __syncthreads();
-      if (wave == 0) {
-        const Locate t = wave_locate<kDigitBins / kWave>(dig, rem, false);
-        if (lane == 0) {
-          sh.digit = t.digit;
-          sh.rem = t.rem;
-          sh.count = t.count;
-        }
-      } else {
-        // Meanwhile clear the other buffer for the next pass.
-        uint32_t* next = sh.digits[(pass + 1) & 1];
-        for (uint32_t i = tid - kWave; i < (uint32_t)kDigitBins; i += kSelThreads - kWave) next[i] = 0;
-      }
-      __syncthreads();
-      if (sh.digit == kNoBin) break;  // unreachable for consistent counts
-      prefix |= uint64_t(sh.digit) << shift;
-      mask |= uint64_t(dmask) << shift;
-      rem = sh.rem;
-      if (sh.count == 1) {
-        cstar = sh.last[sh.digit];  // the one candidate carrying the prefix
-        done = true;
-        break;
-      }
-      // sh.digit / sh.rem / sh.last are rewritten only after the next pass's
-      // first barrier, which every thread reaches after reading them here.
-    }
-    if (!done) cstar = prefix;  // all 64 bits fixed
+    cstar = radix_cut(bin, want, crowd, cand_at, sh.digits, sh.radix);
   }
 
   // This chunk's chosen scores in index order, after the chosen scores of the
@@ -369,6 +377,276 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs 
 }
 
 // ---------------------------------------------------------------------------
+// list select: one workgroup per (row, candidate list) of the decode step,
+// after a scoring kernel that wrote candidate lists (no histogram pass).
+//
+// List j holds, in index order, every key of the row's chunk j (keys
+// [j * chunk_keys, ...)) whose 12-bit bin is at least b_j.  Every workgroup of
+// a row reads all of the row's lists (staged in LDS when they fit), counts
+// their bins and locates the bin B of the k-th largest listed key.  The lists
+// hold every key at or above the cut when each b_j <= B: the cut among the
+// listed keys is then the row's cut, because the row's k-th largest is at
+// least the listed k-th largest.  A list with b_j > B may miss keys; its
+// chunk's raw scores replace it and the workgroup counts again.  The second
+// round always holds: B can only rise, and raw chunks miss nothing.  The
+// entries of bin B are compacted and radix_cut finds the cut among them; the
+// workgroup then writes its own list's chosen keys after the chosen keys of
+// the lists before it.
+//
+// Each list is read by threads_per_list consecutive threads (entry s by
+// thread s mod threads_per_list), whose first kListSpec entries are fetched
+// with the lists' lengths, in one round trip.
+// ---------------------------------------------------------------------------
+constexpr int kListSpec = 24;
+
+struct ListArgs {
+  const float* scores;      // [rows, length]
+  const uint64_t* lists;    // [rows, length]: list j at j * chunk_keys
+  const uint32_t* meta;     // [rows][kMaxListChunks][2]: length, lowest bin listed
+  int32_t length;
+  int32_t chunks;           // lists per row
+  int32_t chunk_keys;
+  int32_t k;
+  uint32_t total_wgs;       // rows * chunks (the grid is padded to a multiple of 8)
+  int64_t* out_idx;         // [rows, k]
+  float* out_val;           // [rows, k] or null
+};
+
+struct ListShared {
+  uint64_t stage[kListStageCapacity];  // the row's entries, list j at base[j]
+  uint64_t cands[kCandCapacity];       // the entries of the cut's bin
+  RadixShared radix;
+  uint32_t hist[kSelectBins];  // bins of the entries; then the radix digit counters
+  uint32_t base[kMaxListChunks + 1];  // entry prefix over the row's sources
+  uint32_t raw[kMaxListChunks];       // 1: the source is the chunk's raw scores
+  uint32_t wsum[2][kSelWaves];
+  uint32_t bin, want, miss, crowd;
+};
+
+__global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
+  __shared__ ListShared sh;
+  args_in_sgprs(a.scores, a.lists, a.meta, a.length, a.chunks, a.chunk_keys, a.k, a.total_wgs, a.out_idx,
+                a.out_val);
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = lane_id();
+  const uint32_t wave = tid / kWave;
+  const uint32_t logical = logical_block();
+  if (logical >= a.total_wgs) return;
+  const uint32_t chunks = (uint32_t)a.chunks;
+  const uint32_t row = logical / chunks;
+  const uint32_t c = logical % chunks;
+  const uint32_t n = (uint32_t)a.length;
+  const uint32_t ck = (uint32_t)a.chunk_keys;
+  const uint32_t kk = (uint32_t)a.k;
+  const float* srow = a.scores + (size_t)row * n;
+  const uint64_t* lrow = a.lists + (size_t)row * n;
+
+  // This thread's list j and its place r among the list's threads.
+  const uint32_t tpl = chunks >= (uint32_t)kSelThreads ? 1u : (uint32_t)kSelThreads / chunks;
+  const uint32_t j = tid / tpl;
+  const uint32_t r = tid % tpl;
+  const bool has_list = j < chunks;
+  const uint32_t chunk_len = has_list ? min(ck, n - j * ck) : 0u;
+  uint32_t list_len = 0;
+  uint32_t list_bin = 0;
+  uint64_t pre[kListSpec] = {};
+  if (has_list) {
+    const uint32_t* m = a.meta + 2 * ((size_t)row * kMaxListChunks + j);
+    list_len = min(m[0], chunk_len);  // (keeps every read inside the row whatever the workspace holds)
+    list_bin = m[1];
+#pragma unroll
+    for (int q = 0; q < kListSpec; ++q) {
+      const uint32_t s = r + tpl * q;
+      pre[q] = s < chunk_len ? lrow[j * ck + s] : 0u;
+    }
+  }
+  bool raw = false;
+  auto load_entry = [&](uint32_t s) -> uint64_t {  // entry s of this thread's source
+    const uint32_t pos = j * ck + s;
+    return raw ? select_composite(float_to_ordered(srow[pos]), pos) : lrow[pos];
+  };
+
+  uint32_t entries = 0;
+  uint32_t src_len = 0;
+  uint32_t src_base = 0;
+  bool staged = false;
+#pragma unroll 1
+  for (int round = 0; round < 2; ++round) {
+#pragma unroll
+    for (int q = 0; q < kSelectBins / kSelThreads; ++q) sh.hist[tid + kSelThreads * q] = 0;
+    src_len = has_list ? (raw ? chunk_len : list_len) : 0u;
+    const uint32_t before = block_excl_scan<kSelWaves>(r == 0 ? src_len : 0u, sh.wsum[round], entries);
+    if (has_list && r == 0) {
+      sh.base[j] = before;
+      sh.raw[j] = raw ? 1u : 0u;
+    }
+    if (tid == 0) {
+      sh.base[chunks] = entries;
+      sh.miss = 0;
+      sh.crowd = 0;
+    }
+    __syncthreads();
+    src_base = has_list ? sh.base[j] : 0u;
+    staged = entries <= (uint32_t)kListStageCapacity;
+    // Count every entry's bin; stage the entries when they fit.
+    auto take = [&](uint32_t s, uint64_t x) {
+      __hip_atomic_fetch_add(&sh.hist[(uint32_t)(x >> 52)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (staged) sh.stage[src_base + s] = x;
+    };
+    if (!raw) {
+#pragma unroll
+      for (int q = 0; q < kListSpec; ++q)
+        if (r + tpl * q < src_len) take(r + tpl * q, pre[q]);
+    }
+    for (uint32_t s = r + (raw ? 0u : tpl * kListSpec); s < src_len; s += tpl) take(s, load_entry(s));
+    __syncthreads();
+    if (wave == 0) {
+      const Locate t = wave_locate<kSelectBins / kWave>(sh.hist, kk, true);
+      if (lane == 0) {
+        sh.bin = t.digit;
+        sh.want = t.rem;
+      }
+    }
+    __syncthreads();
+    // A list misses keys of the cut's bin or above when it stops above that
+    // bin (or, when every entry is chosen, when it is not its whole chunk).
+    const uint32_t bin = sh.bin;
+    const bool miss = has_list && !raw && (bin == kNoBin ? list_bin != 0u : list_bin > bin);
+    if (miss) sh.miss = 1;
+    __syncthreads();
+    if (!sh.miss) break;
+    raw = raw || miss;
+    __syncthreads();  // every thread has read sh.miss before the next round clears it
+  }
+
+  const uint32_t bin = sh.bin;
+  auto raw_of = [&](uint32_t list) { return sh.raw[list] != 0u; };
+  auto entry_of = [&](uint32_t s) -> uint64_t {  // entry s of this thread's source
+    return staged ? sh.stage[src_base + s] : load_entry(s);
+  };
+  // Entries of the sources before this chunk's: those above the cut's bin
+  // are chosen; those inside it are compacted with the rest of the bin.
+  // (With at most k entries, every entry of the earlier sources is chosen.)
+  uint32_t before = (bin == kNoBin && tid == 0) ? sh.base[c] : 0u;
+  uint64_t cstar = uint64_t(1) << 32;  // every listed key when they number at most k
+  if (bin != kNoBin) {
+    // Count, scan, then place the entries of the cut's bin: from the
+    // registers that fetched them where they still hold them, else from the
+    // stage (or memory).
+    const bool in_regs = !raw;
+    const uint32_t spec_end = in_regs ? min(src_len, tpl * kListSpec) : 0u;
+    uint32_t n_cand = 0;
+#pragma unroll
+    for (int q = 0; q < kListSpec; ++q) {
+      const uint32_t s = r + tpl * q;
+      const uint32_t b = (uint32_t)(pre[q] >> 52);
+      n_cand += (s < spec_end && b == bin) ? 1u : 0u;
+      before += (s < spec_end && b > bin && j < c) ? 1u : 0u;
+    }
+    const uint32_t tail0 = in_regs ? r + tpl * kListSpec : r;
+    for (uint32_t s = tail0; s < src_len; s += tpl) {
+      const uint32_t b = (uint32_t)(entry_of(s) >> 52);
+      n_cand += b == bin ? 1u : 0u;
+      before += (b > bin && j < c) ? 1u : 0u;
+    }
+    uint32_t crowd_total;
+    uint32_t slot = block_excl_scan<kSelWaves>(n_cand, sh.wsum[0], crowd_total);
+    if (n_cand) {
+#pragma unroll
+      for (int q = 0; q < kListSpec; ++q) {
+        const uint32_t s = r + tpl * q;
+        if (s < spec_end && (uint32_t)(pre[q] >> 52) == bin) {
+          if (slot < (uint32_t)kCandCapacity) sh.cands[slot] = pre[q];
+          ++slot;
+        }
+      }
+      for (uint32_t s = tail0; s < src_len; s += tpl) {
+        const uint64_t x = entry_of(s);
+        if ((uint32_t)(x >> 52) == bin) {
+          if (slot < (uint32_t)kCandCapacity) sh.cands[slot] = x;
+          ++slot;
+        }
+      }
+    }
+    if (tid == 0) sh.crowd = crowd_total;
+    // The bin counters are dead: they become the radix digit counters.
+    uint32_t (*digits)[kDigitBins] = reinterpret_cast<uint32_t (*)[kDigitBins]>(sh.hist);
+    for (uint32_t i = tid; i < (uint32_t)kDigitBins; i += kSelThreads) digits[0][i] = 0;
+    __syncthreads();
+    const uint32_t crowd = sh.crowd;
+    if (crowd <= (uint32_t)kCandCapacity) {
+      cstar = radix_cut(bin, sh.want, crowd, [&](uint32_t i) { return sh.cands[i]; }, digits, sh.radix);
+      // The chosen entries of the cut's bin in the lists before this chunk's.
+      for (uint32_t i = tid; i < crowd; i += kSelThreads) {
+        const uint64_t x = sh.cands[i];
+        before += (x >= cstar && (~(uint32_t)x) / ck < c) ? 1u : 0u;
+      }
+    } else {
+      // Too many to compact (heavy ties): cut over every entry in place, then
+      // recount the chosen entries of the earlier lists.
+      auto entry_at = [&](uint32_t i) -> uint64_t {
+        if (staged) return sh.stage[i];
+        uint32_t lo = 0;
+        uint32_t hi = chunks - 1;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi + 1) >> 1;
+          if (sh.base[mid] <= i) lo = mid; else hi = mid - 1;
+        }
+        const uint32_t pos = lo * ck + (i - sh.base[lo]);
+        return raw_of(lo) ? select_composite(float_to_ordered(srow[pos]), pos) : lrow[pos];
+      };
+      cstar = radix_cut(bin, sh.want, entries, entry_at, digits, sh.radix);
+      before = 0;
+      for (uint32_t i = tid; i < sh.base[c]; i += kSelThreads) before += entry_at(i) >= cstar ? 1u : 0u;
+    }
+  }
+
+  // This chunk's own source, a contiguous run per thread, in index order.
+  const uint32_t own0 = sh.base[c];
+  const uint32_t own_n = sh.base[c + 1] - own0;
+  const uint32_t per = (own_n + kSelThreads - 1) / kSelThreads;
+  const uint32_t first = min(own_n, tid * per);
+  const uint32_t last = min(own_n, first + per);
+  auto own_at = [&](uint32_t s) -> uint64_t {
+    if (staged) return sh.stage[own0 + s];
+    const uint32_t pos = c * ck + s;
+    return raw_of(c) ? select_composite(float_to_ordered(srow[pos]), pos) : lrow[pos];
+  };
+  uint32_t mine = 0;
+  for (uint32_t i = first; i < last; ++i) mine += own_at(i) >= cstar ? 1u : 0u;
+  uint32_t slot;
+  if (kk < 65536u) {
+    uint32_t packed_total;
+    const uint32_t packed = block_excl_scan<kSelWaves>((before << 16) | mine, sh.wsum[0], packed_total);
+    slot = (packed_total >> 16) + (packed & 0xffffu);
+  } else {
+    uint32_t before_all;
+    block_excl_scan<kSelWaves>(before, sh.wsum[0], before_all);
+    uint32_t own_total;
+    slot = before_all + block_excl_scan<kSelWaves>(mine, sh.wsum[1], own_total);
+  }
+  int64_t* oidx = a.out_idx + (size_t)row * kk;
+  float* oval = a.out_val ? a.out_val + (size_t)row * kk : nullptr;
+  for (uint32_t i = first; i < last && mine; ++i) {
+    const uint64_t x = own_at(i);
+    if (x >= cstar) {
+      if (slot < kk) {  // always true for consistent counts; keeps writes in the row
+        oidx[slot] = (int64_t)(~(uint32_t)x);
+        if (oval) oval[slot] = ordered_to_float((uint32_t)(x >> 32));
+      }
+      ++slot;
+      --mine;
+    }
+  }
+  if (c == 0) {
+    for (uint32_t i = min(n, kk) + tid; i < kk; i += kSelThreads) {
+      oidx[i] = -1;
+      if (oval) oval[i] = -__builtin_inff();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // histogram of arbitrary score rows: one workgroup per (row, chunk); every
 // entry is counted (-inf in its own bin), so a row's total is its length.
 // ---------------------------------------------------------------------------
@@ -419,7 +697,8 @@ SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length
   const int64_t count_off = hist_off + round(rows * kSelectBins * 4);
   const int64_t meta_off = count_off + round(rows * chunks * 4);
   const int64_t above_off = meta_off + round(rows * 16);
-  const int64_t cand_off = above_off + round(rows * chunks * 4);
+  const int64_t list_off = above_off + round(rows * chunks * 4);
+  const int64_t cand_off = list_off + round(rows * kMaxListChunks * 8);
   SelectWorkspace ws;
   ws.bytes = cand_off + rows * length * 8;
   const uintptr_t p = reinterpret_cast<uintptr_t>(base);
@@ -428,6 +707,7 @@ SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length
   ws.meta = base ? reinterpret_cast<uint32_t*>(p + meta_off) : nullptr;
   ws.above = base ? reinterpret_cast<uint32_t*>(p + above_off) : nullptr;
   ws.cand = base ? reinterpret_cast<uint64_t*>(p + cand_off) : nullptr;
+  ws.list_meta = base ? reinterpret_cast<uint32_t*>(p + list_off) : nullptr;
   return ws;
 }
 
@@ -448,6 +728,27 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
   if (int st = check_launch("select_gather_kernel")) return st;
   hipLaunchKernelGGL(select_resolve_kernel, grid, dim3(kSelThreads), 0, stream, a);
   return check_launch("select_resolve_kernel");
+}
+
+int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64_t k,
+                        const ListPlan& plan, const SelectWorkspace& ws, int64_t* out_idx,
+                        float* out_val, hipStream_t stream) {
+  ListArgs a;
+  a.scores = scores;
+  a.lists = ws.cand;
+  a.meta = ws.list_meta;
+  a.length = (int32_t)length;
+  a.chunks = plan.chunks;
+  a.chunk_keys = plan.chunk_keys;
+  a.k = (int32_t)k;
+  a.total_wgs = (uint32_t)(rows * plan.chunks);
+  a.out_idx = out_idx;
+  a.out_val = out_val;
+  // Padded to a multiple of 8 so that logical_block maps workgroup (row, j)
+  // to the XCD whose L2 holds the list that scoring workgroup wrote.
+  const int64_t grid = (rows * plan.chunks + 7) / 8 * 8;
+  hipLaunchKernelGGL(select_lists_kernel, dim3((unsigned)grid), dim3(kSelThreads), 0, stream, a);
+  return check_launch("select_lists_kernel");
 }
 
 int launch_select_scores(const float* scores, int64_t rows, int64_t length, int64_t k,
@@ -501,6 +802,10 @@ extern "C" int dsa_select_topk(const float* scores, int64_t batch, int64_t lengt
   if (!workspace || workspace_bytes < ws.bytes)
     return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the decode step needs %lld workspace bytes",
                 (long long)ws.bytes);
+  const ListPlan plan = list_plan(batch, length, k);
+  if (plan.on)
+    return launch_select_lists(scores, batch, length, k, plan, ws, out_indices, out_values,
+                               static_cast<hipStream_t>(stream));
   return launch_select(scores, batch, length, k, ws, out_indices, out_values,
                        static_cast<hipStream_t>(stream));
 }

@@ -206,14 +206,17 @@ int dsa_topk_long(const float* scores, int64_t rows, int64_t length, int64_t k, 
 int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length);
 
 /* The two halves of dsa_score_topk, for callers that time or overlap them:
- * dsa_score_hist writes the scores and the per-row score histogram into the
- * workspace; dsa_select_topk turns scores + histogram into the top-k and
- * leaves the workspace ready for the next dsa_score_hist.  Every
- * dsa_score_hist on a workspace must be followed by a dsa_select_topk on it
- * (same batch and length) before the next dsa_score_hist. */
+ * dsa_score_hist writes the scores and the selection's intermediate state
+ * (per-chunk candidate lists, or the per-row score histogram when a
+ * workgroup's chunk exceeds 8192 keys) into the workspace; dsa_select_topk
+ * turns scores + that state into the top-k and leaves the workspace ready for
+ * the next dsa_score_hist.  Every dsa_score_hist on a workspace must be
+ * followed by a dsa_select_topk on it (same batch, length and k) before the
+ * next dsa_score_hist. */
 int dsa_score_hist(const void* queries, const float* weights, const void* keys,
                    const float* key_scales, float* scores, int64_t batch, int64_t length,
-                   int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+                   int64_t k, int32_t key_dtype, void* workspace, int64_t workspace_bytes,
+                   void* stream);
 int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t k,
                     int64_t* out_indices, float* out_values, void* workspace,
                     int64_t workspace_bytes, void* stream);

@@ -56,6 +56,9 @@ def inputs(batch, length, seed, hot=0.0, ties=False):
         (16, 32768, 2048, 0.0, "all"),
         (16, 32768, 2048, 0.0, "region"),
         (64, 32768, 2048, 0.01, False),
+        # One long row: 256 scoring chunks, beyond the candidate lists' plan
+        # (the histogram select runs instead).
+        (1, 524288, 2048, 0.01, False),
     ],
 )
 def test_indexer_topk_matches_stable_topk(device, batch, length, k, hot, ties) -> None:
@@ -157,3 +160,30 @@ def test_graph_replays_match_eager(device, batch) -> None:
         assert torch.equal(idx, eager_idx), f"replay {r}"
         decode.indexer_topk(q, w, keys, 300)  # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("batch,length,k", [(16, 32768, 2048), (3, 4096, 256), (1, 524288, 2048)])
+def test_two_halves_match_fused_step(device, batch, length, k) -> None:
+    # dsa_score_hist + dsa_select_topk (the halves a caller may time apart)
+    # equal dsa_score_topk on the same workspace, for a shape on the
+    # candidate-list plan and one on the histogram plan.
+    from dsa_amd import _lib
+
+    q, w, keys = inputs(batch, length, seed=5 + length, hot=0.01)
+    q, w, keys = q.to(device), w.to(device).float(), keys.to(device)
+    ws = torch.zeros(int(_lib.query("dsa_score_topk_workspace_bytes", batch, length)), device=device, dtype=torch.uint8)
+    stream = torch.cuda.current_stream().cuda_stream
+    scores = torch.empty(batch, length, device=device)
+    fused = torch.empty(batch, k, device=device, dtype=torch.int64)
+    halves = torch.full((batch, k), -7, device=device, dtype=torch.int64)
+    _lib.call("dsa_score_topk", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(), batch, length, k,
+              _lib.DTYPE_BF16, fused.data_ptr(), None, ws.data_ptr(), ws.numel(), stream)
+    _lib.call("dsa_score_hist", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(), batch, length, k,
+              _lib.DTYPE_BF16, ws.data_ptr(), ws.numel(), stream)
+    _lib.call("dsa_select_topk", scores.data_ptr(), batch, length, k, halves.data_ptr(), None, ws.data_ptr(), ws.numel(),
+              stream)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, halves)
+    host = scores.cpu().numpy()
+    for b in (0, batch - 1):
+        assert halves[b].cpu().tolist() == T.topk_index_order(host[b], k).tolist()
