@@ -43,6 +43,8 @@ _SIGNATURES: dict[str, list] = {
     "dsa_score_topk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_score_hist": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "dsa_select_topk": [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
+    "dsa_score_hist_timed": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p],
+    "dsa_select_topk_timed": [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p],
     "dsa_topk_distributed": [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
     "dsa_h8_block_max": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _p],
     "dsa_masked_full_scores": [_p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _p],

@@ -567,7 +567,8 @@ __global__ void promote_blocks_kernel(const uint8_t* direct, const float* block_
 // Host-side launch helpers.
 // ---------------------------------------------------------------------------
 template <class Tag, class KF, int M, bool kGather, bool kHist = false, bool kLists = false>
-int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
+int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream, hipEvent_t start = nullptr,
+                   hipEvent_t stop = nullptr) {
   const int64_t units = (a.length + 63) / 64;
   a.units_per_wg = dense_units_per_wg(sequences, a.length);
   a.wgs_per_seq = (int32_t)((units + a.units_per_wg - 1) / a.units_per_wg);
@@ -575,8 +576,8 @@ int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream) {
   const int64_t grid = (a.total_wgs + kXcds - 1) / kXcds * kXcds;
   if (grid > 0x7fffffffLL) return fail(DSA_STATUS_INVALID_ARGUMENT, "problem too large");
   const size_t lds = kLists ? (size_t)a.units_per_wg * 64 * sizeof(float) : 0;
-  hipLaunchKernelGGL((dense_scores_kernel<Tag, KF, M, kGather, kHist, kLists>), dim3((unsigned)grid),
-                     dim3(256), lds, stream, a);
+  launch_timed(dense_scores_kernel<Tag, KF, M, kGather, kHist, kLists>, dim3((unsigned)grid), dim3(256),
+               (uint32_t)lds, stream, start, stop, a);
   return check_launch("dense_scores_kernel");
 }
 
@@ -718,10 +719,9 @@ extern "C" int64_t dsa_score_topk_workspace_bytes(int64_t batch, int64_t length)
   return select_workspace_layout(nullptr, batch, length).bytes;
 }
 
-extern "C" int dsa_score_hist(const void* queries, const float* weights, const void* keys,
-                              const float* key_scales, float* scores, int64_t batch,
-                              int64_t length, int64_t k, int32_t key_dtype, void* workspace,
-                              int64_t workspace_bytes, void* stream) {
+static int score_hist(const void* queries, const float* weights, const void* keys, const float* key_scales,
+                      float* scores, int64_t batch, int64_t length, int64_t k, int32_t key_dtype, void* workspace,
+                      int64_t workspace_bytes, void* stream, hipEvent_t start, hipEvent_t stop) {
   DSA_REQUIRE(queries && weights && keys && scores, "null pointer argument");
   DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(length > 0 && length <= int64_t(kSelectChunk) * kMaxSelectChunks,
@@ -764,16 +764,34 @@ extern "C" int dsa_score_hist(const void* queries, const float* weights, const v
     a.list_meta = ws.list_meta;
     a.list_quota = plan.quota;
     switch (key_dtype) {
-      case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true, true>(a, batch, s);
-      case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true, true>(a, batch, s);
-      default: return launch_dense_m<Bf16Tag, KeysFP8, 4, false, true, true>(a, batch, s);
+      case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true, true>(a, batch, s, start, stop);
+      case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true, true>(a, batch, s, start, stop);
+      default: return launch_dense_m<Bf16Tag, KeysFP8, 4, false, true, true>(a, batch, s, start, stop);
     }
   }
   switch (key_dtype) {
-    case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true>(a, batch, s);
-    case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true>(a, batch, s);
-    default: return launch_dense_m<Bf16Tag, KeysFP8, 4, false, true>(a, batch, s);
+    case kBF16: return launch_dense_m<Bf16Tag, KeysB16, 4, false, true>(a, batch, s, start, stop);
+    case kF16: return launch_dense_m<F16Tag, KeysB16, 4, false, true>(a, batch, s, start, stop);
+    default: return launch_dense_m<Bf16Tag, KeysFP8, 4, false, true>(a, batch, s, start, stop);
   }
+}
+
+extern "C" int dsa_score_hist(const void* queries, const float* weights, const void* keys,
+                              const float* key_scales, float* scores, int64_t batch,
+                              int64_t length, int64_t k, int32_t key_dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  return score_hist(queries, weights, keys, key_scales, scores, batch, length, k, key_dtype, workspace,
+                    workspace_bytes, stream, nullptr, nullptr);
+}
+
+extern "C" int dsa_score_hist_timed(const void* queries, const float* weights, const void* keys,
+                                    const float* key_scales, float* scores, int64_t batch,
+                                    int64_t length, int64_t k, int32_t key_dtype, void* workspace,
+                                    int64_t workspace_bytes, void* stream, void* start_event,
+                                    void* stop_event) {
+  return score_hist(queries, weights, keys, key_scales, scores, batch, length, k, key_dtype, workspace,
+                    workspace_bytes, stream, static_cast<hipEvent_t>(start_event),
+                    static_cast<hipEvent_t>(stop_event));
 }
 
 extern "C" int dsa_score_topk(const void* queries, const float* weights, const void* keys,

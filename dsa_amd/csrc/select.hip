@@ -713,7 +713,7 @@ SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length
 
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,
-                  hipStream_t stream) {
+                  hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   SelectArgs a;
   a.scores = scores;
   a.rows = (int32_t)rows;
@@ -724,15 +724,15 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
   a.out_idx = out_idx;
   a.out_val = out_val;
   const dim3 grid((unsigned)(rows * a.chunks));
-  hipLaunchKernelGGL(select_gather_kernel, grid, dim3(kSelThreads), 0, stream, a);
+  launch_timed(select_gather_kernel, grid, dim3(kSelThreads), 0, stream, start, nullptr, a);
   if (int st = check_launch("select_gather_kernel")) return st;
-  hipLaunchKernelGGL(select_resolve_kernel, grid, dim3(kSelThreads), 0, stream, a);
+  launch_timed(select_resolve_kernel, grid, dim3(kSelThreads), 0, stream, nullptr, stop, a);
   return check_launch("select_resolve_kernel");
 }
 
 int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64_t k,
                         const ListPlan& plan, const SelectWorkspace& ws, int64_t* out_idx,
-                        float* out_val, hipStream_t stream) {
+                        float* out_val, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   ListArgs a;
   a.scores = scores;
   a.lists = ws.cand;
@@ -747,7 +747,7 @@ int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64
   // Padded to a multiple of 8 so that logical_block maps workgroup (row, j)
   // to the XCD whose L2 holds the list that scoring workgroup wrote.
   const int64_t grid = (rows * plan.chunks + 7) / 8 * 8;
-  hipLaunchKernelGGL(select_lists_kernel, dim3((unsigned)grid), dim3(kSelThreads), 0, stream, a);
+  launch_timed(select_lists_kernel, dim3((unsigned)grid), dim3(kSelThreads), 0, stream, start, stop, a);
   return check_launch("select_lists_kernel");
 }
 
@@ -789,9 +789,9 @@ extern "C" int dsa_topk_distributed(const float* scores, int64_t rows, int64_t l
                               static_cast<hipStream_t>(stream));
 }
 
-extern "C" int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t k,
-                               int64_t* out_indices, float* out_values, void* workspace,
-                               int64_t workspace_bytes, void* stream) {
+static int select_topk(const float* scores, int64_t batch, int64_t length, int64_t k, int64_t* out_indices,
+                       float* out_values, void* workspace, int64_t workspace_bytes, void* stream,
+                       hipEvent_t start, hipEvent_t stop) {
   DSA_REQUIRE(scores && out_indices, "null pointer argument");
   DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(length > 0 && length <= int64_t(kSelectChunk) * kMaxSelectChunks,
@@ -805,7 +805,22 @@ extern "C" int dsa_select_topk(const float* scores, int64_t batch, int64_t lengt
   const ListPlan plan = list_plan(batch, length, k);
   if (plan.on)
     return launch_select_lists(scores, batch, length, k, plan, ws, out_indices, out_values,
-                               static_cast<hipStream_t>(stream));
+                               static_cast<hipStream_t>(stream), start, stop);
   return launch_select(scores, batch, length, k, ws, out_indices, out_values,
-                       static_cast<hipStream_t>(stream));
+                       static_cast<hipStream_t>(stream), start, stop);
+}
+
+extern "C" int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t k,
+                               int64_t* out_indices, float* out_values, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  return select_topk(scores, batch, length, k, out_indices, out_values, workspace, workspace_bytes, stream,
+                     nullptr, nullptr);
+}
+
+extern "C" int dsa_select_topk_timed(const float* scores, int64_t batch, int64_t length, int64_t k,
+                                     int64_t* out_indices, float* out_values, void* workspace,
+                                     int64_t workspace_bytes, void* stream, void* start_event,
+                                     void* stop_event) {
+  return select_topk(scores, batch, length, k, out_indices, out_values, workspace, workspace_bytes, stream,
+                     static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
 }

@@ -2,6 +2,7 @@
 // (select.hip), shared with the scoring kernel that fills its histogram.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -65,6 +66,17 @@ inline ListPlan list_plan(int64_t rows, int64_t length, int64_t k) {
   return p;
 }
 
+// A launch that, given events, records them at the kernel's own start and
+// end (the interval a profiler's kernel trace reports), else a plain launch.
+template <class K, class... Args>
+inline void launch_timed(K kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t stream, hipEvent_t start,
+                         hipEvent_t stop, Args... args) {
+  if (start || stop)
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, start, stop, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+}
+
 // (order-preserving key << 32) | ~position: distinct per row, and larger for
 // the larger score, or for the lower position among equal scores.
 __device__ __forceinline__ uint64_t select_composite(uint32_t key, uint32_t pos) {
@@ -80,14 +92,17 @@ int launch_select_scores(const float* scores, int64_t rows, int64_t length, int6
                          const SelectWorkspace& ws, int64_t* out_idx, float* out_val, hipStream_t stream);
 
 // Selects the top-k of scores [rows, length] whose histogram is in ws.
+// start/stop, when not null, are recorded by the first and last kernel at
+// their own start and end (hipExtLaunchKernel).
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,
-                  hipStream_t stream);
+                  hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
 // Selects the top-k of scores [rows, length] from the candidate lists that
 // the scoring kernel wrote to ws under `plan`.
 int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64_t k,
                         const ListPlan& plan, const SelectWorkspace& ws, int64_t* out_idx,
-                        float* out_val, hipStream_t stream);
+                        float* out_val, hipStream_t stream, hipEvent_t start = nullptr,
+                        hipEvent_t stop = nullptr);
 
 }  // namespace dsa

@@ -221,6 +221,21 @@ int dsa_select_topk(const float* scores, int64_t batch, int64_t length, int64_t 
                     int64_t* out_indices, float* out_values, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* Measurement variants of the two halves (no counterpart in the reference,
+ * whose benchmark brackets launches with events): the half's first kernel
+ * records start_event at its own start and its last kernel records
+ * stop_event at its own end (hipExtLaunchKernel), so the interval is the
+ * kernels' execution alone, as a profiler's kernel trace reports it.  The
+ * events (hipEvent_t) are created by the caller; either may be NULL. */
+int dsa_score_hist_timed(const void* queries, const float* weights, const void* keys,
+                         const float* key_scales, float* scores, int64_t batch, int64_t length,
+                         int64_t k, int32_t key_dtype, void* workspace, int64_t workspace_bytes,
+                         void* stream, void* start_event, void* stop_event);
+int dsa_select_topk_timed(const float* scores, int64_t batch, int64_t length, int64_t k,
+                          int64_t* out_indices, float* out_values, void* workspace,
+                          int64_t workspace_bytes, void* stream, void* start_event,
+                          void* stop_event);
+
 /* Exact top-k (stable_topk set, ascending index order, -1 padding) of score
  * rows [rows, length] fp32, spread over the whole GPU: a 4096-bin histogram
  * of every row, then the decode step's candidate gather and exact resolve.
