@@ -61,11 +61,9 @@ struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
   }
 };
 
-// w_h * ReLU(acc) summed over the M-tiles' head slots held by this lane.
+// The M head tiles' dot products with one 16-key tile: acc[m] = Q_m . K^T.
 template <class Tag, int M, class KF>
-__device__ __forceinline__ float tile_contrib(const uint4 (&qa)[M][4], const float (&wr)[M][4],
-                                              const uint4 (&raw)[KF::kRaw]) {
-  floatx4 acc[M];
+__device__ __forceinline__ void tile_mfma(const uint4 (&qa)[M][4], const uint4 (&raw)[KF::kRaw], floatx4 (&acc)[M]) {
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -74,12 +72,25 @@ __device__ __forceinline__ float tile_contrib(const uint4 (&qa)[M][4], const flo
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = mfma_16x16x32(Tag{}, qa[m][j], kf, acc[m]);
   }
+}
+
+// w_h * ReLU(acc) summed over the M-tiles' head slots held by this lane.
+template <int M>
+__device__ __forceinline__ float tile_reduce(const float (&wr)[M][4], const floatx4 (&acc)[M]) {
   float v = 0.f;
 #pragma unroll
   for (int m = 0; m < M; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i) v = fmaf(wr[m][i], relu(acc[m][i]), v);
   return v;
+}
+
+template <class Tag, int M, class KF>
+__device__ __forceinline__ float tile_contrib(const uint4 (&qa)[M][4], const float (&wr)[M][4],
+                                              const uint4 (&raw)[KF::kRaw]) {
+  floatx4 acc[M];
+  tile_mfma<Tag, M, KF>(qa, raw, acc);
+  return tile_reduce<M>(wr, acc);
 }
 
 // Element offset of k-step j's 8 dims for lane group g, in the key format's

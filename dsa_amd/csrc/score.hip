@@ -275,8 +275,8 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
 
 // ---------------------------------------------------------------------------
 // Multi-query (prefill) scoring: many query blocks against one shared key set.
-// A workgroup owns kPrefillQueries consecutive queries of one key set (two per
-// wave) and streams the key units they see through LDS: each 64-key unit is
+// A workgroup owns kPrefillQueries consecutive queries of one key set
+// (kPrefillQPW per wave) and streams the key units they see through LDS: each 64-key unit is
 // loaded from memory once and scored for all eight queries, instead of once
 // per query.  Rows are padded to kPrefillRow bytes so the 16 rows a lane
 // group reads fall on different banks.  With a causal limit the heaviest
@@ -284,9 +284,19 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kPrefillQueries = 8;
 constexpr int kPrefillRow = 272;
+constexpr int kPrefillQPW = 1;  // queries per wave
 
-template <class Tag>
-__global__ __launch_bounds__(256) void prefill_scores_kernel(DenseArgs a, int32_t qblocks, int32_t keysets) {
+// QPW queries per wave, kPrefillQueries / QPW waves per workgroup.  With one
+// query per wave the wave needs about half the registers of two, so two waves
+// share each SIMD and one's ReLU / weight / reduction VALU work runs under the
+// other's MFMAs.
+template <class Tag, int QPW>
+__global__ __launch_bounds__(64 * kPrefillQueries / QPW) void prefill_scores_kernel(DenseArgs a, int32_t qblocks,
+                                                                                    int32_t keysets) {
+  constexpr int kThreads = 64 * kPrefillQueries / QPW;
+  constexpr int kRowSplit = kThreads / 64;         // threads per staged key row
+  constexpr int kRowBytesPer = 256 / kRowSplit;    // bytes each of them moves
+  constexpr int kVecs = kRowBytesPer / 16;
   __shared__ __align__(16) uint8_t lds[2][64 * kPrefillRow];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -300,14 +310,14 @@ __global__ __launch_bounds__(256) void prefill_scores_kernel(DenseArgs a, int32_
   const int t_last = min(qpk - 1, qb * kPrefillQueries + kPrefillQueries - 1);
   const int units = (visible(t_last) + 63) >> 6;
 
-  uint4 qa[2][4][4];
-  float wr[2][4][4];
-  bool active[2];
-  int vis[2];
-  float* orow[2];
+  uint4 qa[QPW][4][4];
+  float wr[QPW][4][4];
+  bool active[QPW];
+  int vis[QPW];
+  float* orow[QPW];
 #pragma unroll
-  for (int qi = 0; qi < 2; ++qi) {
-    const int t = qb * kPrefillQueries + 2 * wave + qi;
+  for (int qi = 0; qi < QPW; ++qi) {
+    const int t = qb * kPrefillQueries + QPW * wave + qi;
     active[qi] = t < qpk;
     const int64_t seq = keyset * qpk + (active[qi] ? t : 0);
     load_dense_head_tiles<4, KeysB16::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa[qi],
@@ -316,21 +326,21 @@ __global__ __launch_bounds__(256) void prefill_scores_kernel(DenseArgs a, int32_
     orow[qi] = a.out + seq * a.out_stride;
   }
 
-  // Cooperative unit load: thread i moves 64 bytes of row i / 4.
+  // Cooperative unit load: thread i moves kRowBytesPer bytes of row i / kRowSplit.
   const BufferRsrc kr = make_buffer(a.keys + keyset * a.key_stride * KeysB16::kRowBytes,
                                     (uint32_t)L * KeysB16::kRowBytes);
-  const int lrow = threadIdx.x >> 2;
-  const int lpart = threadIdx.x & 3;
-  uint4 stage[4];
+  const int lrow = threadIdx.x / kRowSplit;
+  const int lpart = threadIdx.x % kRowSplit;
+  uint4 stage[kVecs];
   auto fetch = [&](int u) {
-    const uint32_t off = (uint32_t)(u * 64 + lrow) * KeysB16::kRowBytes + lpart * 64;
+    const uint32_t off = (uint32_t)(u * 64 + lrow) * KeysB16::kRowBytes + lpart * kRowBytesPer;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) stage[k] = buffer_load_16(kr, off + 16 * k);
+    for (int k = 0; k < kVecs; ++k) stage[k] = buffer_load_16(kr, off + 16 * k);
   };
   auto put = [&](int buf) {
-    uint8_t* dst = lds[buf] + lrow * kPrefillRow + lpart * 64;
+    uint8_t* dst = lds[buf] + lrow * kPrefillRow + lpart * kRowBytesPer;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(dst + 16 * k) = stage[k];
+    for (int k = 0; k < kVecs; ++k) *reinterpret_cast<uint4*>(dst + 16 * k) = stage[k];
   };
   if (units > 0) {
     fetch(0);
@@ -340,19 +350,29 @@ __global__ __launch_bounds__(256) void prefill_scores_kernel(DenseArgs a, int32_
   for (int u = 0; u < units; ++u) {
     if (u + 1 < units) fetch(u + 1);  // in flight while this unit is scored
     const uint8_t* base = lds[u & 1];
-    float s[2][4];
+    float s[QPW][4];
+    // Software-pipelined over the unit's four tiles: the MFMAs of tile t are
+    // issued before the ReLU / weight VALU work of tile t - 1, which depends
+    // only on the previous accumulators, so the two can co-execute.
+    floatx4 acc[2][QPW][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint4 raw[KeysB16::kRaw];
-      const uint8_t* row = base + (16 * t + r) * kPrefillRow + g * 16;
+    for (int t = 0; t <= 4; ++t) {
+      if (t < 4) {
+        uint4 raw[KeysB16::kRaw];
+        const uint8_t* row = base + (16 * t + r) * kPrefillRow + g * 16;
 #pragma unroll
-      for (int c = 0; c < KeysB16::kRaw; ++c) raw[c] = *reinterpret_cast<const uint4*>(row + 64 * c);
+        for (int c = 0; c < KeysB16::kRaw; ++c) raw[c] = *reinterpret_cast<const uint4*>(row + 64 * c);
 #pragma unroll
-      for (int qi = 0; qi < 2; ++qi) s[qi][t] = tile_contrib<Tag, 4, KeysB16>(qa[qi], wr[qi], raw);
+        for (int qi = 0; qi < QPW; ++qi) tile_mfma<Tag, 4, KeysB16>(qa[qi], raw, acc[t & 1][qi]);
+      }
+      if (t > 0) {
+#pragma unroll
+        for (int qi = 0; qi < QPW; ++qi) s[qi][t - 1] = tile_reduce<4>(wr[qi], acc[(t - 1) & 1][qi]);
+      }
     }
     const int key = u * 64 + lane;
 #pragma unroll
-    for (int qi = 0; qi < 2; ++qi) {
+    for (int qi = 0; qi < QPW; ++qi) {
       const float score = unit_reduce(s[qi], g);
       if (active[qi] && key < L) orow[qi][key] = key < vis[qi] ? score : -__builtin_inff();
     }
@@ -361,7 +381,7 @@ __global__ __launch_bounds__(256) void prefill_scores_kernel(DenseArgs a, int32_
   }
   // Keys past this workgroup's units are invisible to all of its queries.
 #pragma unroll
-  for (int qi = 0; qi < 2; ++qi)
+  for (int qi = 0; qi < QPW; ++qi)
     if (active[qi])
       for (int key = units * 64 + lane; key < L; key += 64) orow[qi][key] = -__builtin_inff();
 }
@@ -588,7 +608,8 @@ int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
       const int64_t keysets = sequences / a.queries_per_keyset;
       const int64_t qblocks = (a.queries_per_keyset + kPrefillQueries - 1) / kPrefillQueries;
       if (keysets * a.queries_per_keyset == sequences && qblocks * keysets <= 0x7fffffffLL) {
-        hipLaunchKernelGGL((prefill_scores_kernel<Tag>), dim3((unsigned)(qblocks * keysets)), dim3(256), 0, stream, a,
+        hipLaunchKernelGGL((prefill_scores_kernel<Tag, kPrefillQPW>), dim3((unsigned)(qblocks * keysets)),
+                           dim3(64 * kPrefillQueries / kPrefillQPW), 0, stream, a,
                            (int32_t)qblocks, (int32_t)keysets);
         return check_launch("prefill_scores_kernel");
       }
