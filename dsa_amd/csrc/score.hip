@@ -133,7 +133,7 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
 // A scoring workgroup's candidate list: thread t takes keys [t * per, t * per
 // + per) of the chunk (per <= P), all read from LDS at once, and writes those
 // in bins >= lbin in index order at offsets from one block scan.
-template <int P>
+template <int P, int kWaves>
 __device__ __forceinline__ uint32_t emit_list(const float* chunk_scores, int per, int n_chunk, int chunk_base,
                                               uint32_t lbin, uint64_t* list, uint32_t* wsum) {
   const int i0 = (int)threadIdx.x * per;
@@ -145,7 +145,7 @@ __device__ __forceinline__ uint32_t emit_list(const float* chunk_scores, int per
     if (e < per && i0 + e < n_chunk && (key[e] >> 20) >= lbin) takes |= 1u << e;
   }
   uint32_t listed;
-  uint32_t slot = block_excl_scan<4>((uint32_t)__builtin_popcount(takes), wsum, listed);
+  uint32_t slot = block_excl_scan<kWaves>((uint32_t)__builtin_popcount(takes), wsum, listed);
   if (takes) {
 #pragma unroll
     for (int e = 0; e < P; ++e)
@@ -154,8 +154,9 @@ __device__ __forceinline__ uint32_t emit_list(const float* chunk_scores, int per
   return listed;
 }
 
-template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists>
-__global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
+template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists, int kWaves>
+__global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores_kernel(DenseArgs a) {
+  constexpr int kThreads = 64 * kWaves;
   // kHist: also count every valid score into a histogram of the top 12 bits
   // of its order-preserving key; without kLists it is added to the sequence's
   // histogram (input of the distributed top-k).  kLists: the workgroup keeps
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
   // lie wholly beyond the causal limit and only get -inf.  (Interleaving the
   // units over all of a sequence's waves measured ~10 % slower; handing them
   // out from a per-sequence atomic counter serialises on that counter.)
-  const int u_stride = 4;
+  const int u_stride = kWaves;
   const int u_end = min((L + 63) >> 6, (chunk + 1) * a.units_per_wg);
   const int u_first = chunk * a.units_per_wg + wave;
   const int u_compute_end = min(u_end, (valid + 63) >> 6);
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
     buffer_store_f32(out, (uint32_t)(uu * 64 + lane) * 4, -__builtin_inff());
   if constexpr (kHist) {
 #pragma unroll
-    for (int j = 0; j < kSelectBins / 256; ++j) hist[threadIdx.x + 256 * j] = 0;
+    for (int j = 0; j < kSelectBins / kThreads; ++j) hist[threadIdx.x + kThreads * j] = 0;
     __syncthreads();
     const int chunk_keys = a.units_per_wg * 64;
     const int chunk_base = chunk * chunk_keys;
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
       // the chunk's list_quota-th largest score (all valid keys when the
       // chunk has no more), in index order.
       __shared__ uint32_t s_list_bin;
-      __shared__ __align__(16) uint32_t s_list_wsum[4];
+      __shared__ __align__(16) uint32_t s_list_wsum[kWaves];
       const int n_chunk = min(chunk_keys, valid - chunk_base);
       if (wave == 0) {
         const Locate t = wave_locate<kSelectBins / kWave>(hist, (uint32_t)a.list_quota, true);
@@ -233,19 +234,18 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
       const uint32_t lbin = s_list_bin;
       uint64_t* list = a.lists + seq * (int64_t)L + chunk_base;
       uint32_t listed;
-      switch (chunk_keys / 256) {  // keys per thread, 1..32
-        case 1: listed = emit_list<1>(chunk_scores, 1, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
-        case 2: listed = emit_list<2>(chunk_scores, 2, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
+      const int per = chunk_keys / kThreads;  // keys per thread, 1..32
+      switch (per) {
+        case 1: listed = emit_list<1, kWaves>(chunk_scores, 1, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
+        case 2: listed = emit_list<2, kWaves>(chunk_scores, 2, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
         case 3:
-        case 4: listed = emit_list<4>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
-          break;
+        case 4: listed = emit_list<4, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
         case 5: case 6: case 7:
-        case 8: listed = emit_list<8>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
-          break;
+        case 8: listed = emit_list<8, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
         case 9: case 10: case 11: case 12: case 13: case 14: case 15:
-        case 16: listed = emit_list<16>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
+        case 16: listed = emit_list<16, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum);
           break;
-        default: listed = emit_list<32>(chunk_scores, chunk_keys / 256, n_chunk, chunk_base, lbin, list, s_list_wsum);
+        default: listed = emit_list<32, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum);
           break;
       }
       if (threadIdx.x == 0) {
@@ -258,13 +258,13 @@ __global__ __launch_bounds__(256, 2) void dense_scores_kernel(DenseArgs a) {
     // All sixteen LDS reads first, then the atomics for the bins in use: one
     // LDS round trip instead of one per bin.
     uint32_t* ghist = a.hist + seq * kSelectBins;
-    uint32_t n[kSelectBins / 256];
+    uint32_t n[kSelectBins / kThreads];
 #pragma unroll
-    for (int j = 0; j < kSelectBins / 256; ++j) n[j] = hist[threadIdx.x + 256 * j];
+    for (int j = 0; j < kSelectBins / kThreads; ++j) n[j] = hist[threadIdx.x + kThreads * j];
 #pragma unroll
-    for (int j = 0; j < kSelectBins / 256; ++j)
+    for (int j = 0; j < kSelectBins / kThreads; ++j)
       if (n[j])
-        __hip_atomic_fetch_add(&ghist[threadIdx.x + 256 * j], n[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&ghist[threadIdx.x + kThreads * j], n[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   if (count == 0) return;
@@ -589,14 +589,18 @@ __global__ void promote_blocks_kernel(const uint8_t* direct, const float* block_
 template <class Tag, class KF, int M, bool kGather, bool kHist = false, bool kLists = false>
 int launch_dense_m(DenseArgs a, int64_t sequences, hipStream_t stream, hipEvent_t start = nullptr,
                    hipEvent_t stop = nullptr) {
+  // Waves per workgroup of the decode step (histogram / candidate lists).
+  // Eight (two per SIMD, twice the loads in flight per CU) measured slower
+  // than four at C2.
+  constexpr int kWaves = kHist ? kDecodeWaves : 4;
   const int64_t units = (a.length + 63) / 64;
-  a.units_per_wg = dense_units_per_wg(sequences, a.length);
+  a.units_per_wg = dense_units_per_wg(sequences, a.length, 256, kWaves);
   a.wgs_per_seq = (int32_t)((units + a.units_per_wg - 1) / a.units_per_wg);
   a.total_wgs = sequences * a.wgs_per_seq;
   const int64_t grid = (a.total_wgs + kXcds - 1) / kXcds * kXcds;
   if (grid > 0x7fffffffLL) return fail(DSA_STATUS_INVALID_ARGUMENT, "problem too large");
   const size_t lds = kLists ? (size_t)a.units_per_wg * 64 * sizeof(float) : 0;
-  launch_timed(dense_scores_kernel<Tag, KF, M, kGather, kHist, kLists>, dim3((unsigned)grid), dim3(256),
+  launch_timed(dense_scores_kernel<Tag, KF, M, kGather, kHist, kLists, kWaves>, dim3((unsigned)grid), dim3(64 * kWaves),
                (uint32_t)lds, stream, start, stop, a);
   return check_launch("dense_scores_kernel");
 }

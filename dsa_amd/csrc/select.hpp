@@ -27,16 +27,18 @@ struct SelectWorkspace {
 };
 
 // Units of 64 keys per workgroup of the dense scoring kernel: about
-// target_wgs workgroups of four waves (one per CU at 256), so that every wave
-// streams several units and pays its query-block load and pipeline fill
-// once, with at least four units (one per wave) in each workgroup.
-inline int32_t dense_units_per_wg(int64_t sequences, int64_t length, int64_t target_wgs = 256) {
+// target_wgs workgroups (one per CU at 256), so that every wave streams
+// several units and pays its query-block load and pipeline fill once, with
+// a multiple of `waves` units (at least one per wave) in each workgroup.
+inline int32_t dense_units_per_wg(int64_t sequences, int64_t length, int64_t target_wgs = 256, int32_t waves = 4) {
   const int64_t units = (length + 63) / 64;
   int64_t per = (units * sequences + target_wgs - 1) / target_wgs;
-  per = per < 4 ? 4 : per;
-  per = (per + 3) / 4 * 4;
+  per = per < waves ? waves : per;
+  per = (per + waves - 1) / waves * waves;
   return (int32_t)per;
 }
+
+constexpr int kDecodeWaves = 4;  // waves per workgroup of the decode step's scoring kernel (8 measured slower)
 
 // Candidate lists of the decode step.  Each scoring workgroup owns
 // chunk_keys consecutive keys of one row and, when the plan is on, lists the
@@ -56,7 +58,7 @@ struct ListPlan {
 
 inline ListPlan list_plan(int64_t rows, int64_t length, int64_t k) {
   ListPlan p;
-  p.units_per_wg = dense_units_per_wg(rows, length);
+  p.units_per_wg = dense_units_per_wg(rows, length, 256, kDecodeWaves);
   p.chunk_keys = p.units_per_wg * 64;
   p.chunks = (int32_t)((length + p.chunk_keys - 1) / p.chunk_keys);
   const int64_t quota = (5 * k + 4 * (int64_t)p.chunks - 1) / (4 * (int64_t)p.chunks) + 16;
