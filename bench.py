@@ -45,10 +45,11 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--config", choices=("c2", "c3", "c4", "c5", "progressive"), default="c2",
+    parser.add_argument("--config", choices=("c2", "c3", "c4", "c5", "progressive", "sidecar"), default="c2",
                         help="c2: the headline decode step (default); c3: temporal replay over 256 decode steps; "
                         "c4: causal prefill indexer + top-512; c5: fp8 long-context decode; "
-                        "progressive: the reference's method comparison (full / H8 / two-pass / fused)")
+                        "progressive: the reference's method comparison (full / H8 / two-pass / fused); "
+                        "sidecar: the indexer's query/key encoders at the decode and prefill shapes")
     parser.add_argument("--out", default=None, help="c4/c5/progressive: also write the full table (JSON) here")
     parser.add_argument("--flush", choices=("read", "write"), default="read",
                         help="c4/c5/progressive: cache flush before each timed replay: read 512 MiB (default) or "
@@ -120,8 +121,8 @@ def main() -> None:
     if args.config == "c3":
         run_c3(args)
         return
-    if args.config in ("c4", "c5", "progressive"):
-        {"c4": run_c4, "c5": run_c5, "progressive": run_progressive}[args.config](args)
+    if args.config in ("c4", "c5", "progressive", "sidecar"):
+        {"c4": run_c4, "c5": run_c5, "progressive": run_progressive, "sidecar": run_sidecar}[args.config](args)
         return
     import torch
 
@@ -1000,6 +1001,155 @@ def run_progressive(args) -> None:
     write_table(args, line, rows)
     print(json.dumps(line), flush=True)
 
+
+
+
+
+# --------------------------------------------------------------------------
+# Sidecar encoders: the producers of the indexer's q, w and K
+# --------------------------------------------------------------------------
+SIDECAR_HIDDEN = 2048
+
+
+def torch_formula_encode(module, hidden, positions, cache, rows):
+    """Baseline: the reference's encoder formula (sidecar.py:10-88) as torch
+    eager ops on the same GPU and weights -- projection, LayerNorm, the
+    non-interleaved RoPE by slices, products and a concatenation -- then the
+    key-cache append by index_copy_."""
+
+    import torch
+    from torch.nn import functional as F
+
+    def rope(x, pos):
+        half = module.rope_dim // 2
+        inv = module.rope_theta ** (-torch.arange(half, device=x.device, dtype=torch.float32) / half)
+        ang = pos.to(torch.float32).unsqueeze(-1) * inv
+        cos, sin = torch.cos(ang).to(x.dtype), torch.sin(ang).to(x.dtype)
+        while cos.ndim < x.ndim:
+            cos, sin = cos.unsqueeze(-2), sin.unsqueeze(-2)
+        a, b = x[..., :half], x[..., half:]
+        return torch.cat((a * cos - b * sin, b * cos + a * sin), dim=-1)
+
+    def partial(x, pos):
+        return torch.cat((rope(x[..., : module.rope_dim], pos), x[..., module.rope_dim:]), dim=-1)
+
+    keys = partial(F.layer_norm(F.linear(hidden, module.wk.weight), (module.head_dim,), module.k_norm.weight,
+                                module.k_norm.bias, module.k_norm.eps), positions)
+    cache.index_copy_(0, rows, keys.reshape(-1, module.head_dim))
+    q = F.linear(hidden, module.wq.weight).view(*hidden.shape[:-1], module.heads, module.head_dim)
+    q = partial(q, positions)
+    w = F.linear(hidden.float(), module.weights_proj.weight.float()) * (module.heads * module.head_dim) ** -0.5
+    return q, w
+
+
+def run_sidecar(args) -> None:
+    """The indexer sidecar's encoders (reference sidecar.py:31-88, bf16 module,
+    hidden 2048, 64 heads x 128 dims, rope_dim 64) per decode step (16
+    sequences, one new token each, keys appended to a 16 x 32768-row cache)
+    and per prefill chunk (4096 tokens).  Reports the library path (platform
+    GEMMs + the fused HIP epilogues) and the reference formula as torch eager
+    ops on the same GPU, HIP events around each call after a cache flush,
+    median over 100."""
+
+    import torch
+    from torch.nn import functional as F
+
+    from dsa_amd import _lib, sidecar
+
+    _lib.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    torch.manual_seed(SEED)
+    module = sidecar.LightningIndexerSidecar(hidden_size=SIDECAR_HIDDEN).to(device=device, dtype=torch.bfloat16)
+    module.eval()
+    flush = make_flush(args, device)
+    results = {}
+    for name, tokens in (("decode", BATCH), ("prefill", 4096)):
+        hidden = torch.randn(tokens, SIDECAR_HIDDEN, device=device, dtype=torch.bfloat16)
+        positions = torch.randint(0, LENGTH, (tokens,), device=device)
+        cache = torch.zeros(BATCH * LENGTH, 128, device=device, dtype=torch.bfloat16)
+        rows = torch.randperm(BATCH * LENGTH, device=device)[:tokens]
+
+        def library():
+            module.encode_keys(hidden, positions, out=cache, out_rows=rows)
+            return module.encode_queries(hidden, positions)
+
+        def formula():
+            return torch_formula_encode(module, hidden, positions, cache, rows)
+
+        def epilogues_only():
+            # the HIP pass alone, on precomputed projections
+            _lib.call("dsa_encode_keys_epilogue", _lib.ptr(pk), _lib.DTYPE_BF16, 128, _lib.ptr(lw), _lib.ptr(lb),
+                      1e-6, _lib.ptr(positions), 64, 10_000.0, _lib.ptr(cache), _lib.DTYPE_BF16, 128, _lib.ptr(rows),
+                      cache.shape[0], tokens, 128, torch.cuda.current_stream().cuda_stream)
+            _lib.call("dsa_encode_queries_epilogue", _lib.ptr(pq), _lib.ptr(pw), _lib.ptr(positions), 64, 10_000.0,
+                      float((64 * 128) ** -0.5), _lib.ptr(oq), _lib.ptr(ow), tokens, 64, 128, _lib.DTYPE_BF16,
+                      torch.cuda.current_stream().cuda_stream)
+
+        with torch.no_grad():
+            pk = F.linear(hidden, module.wk.weight).contiguous()
+            pq = F.linear(hidden, module.wq.weight).contiguous()
+            pw = F.linear(hidden.float(), module.weights_proj.weight.float()).contiguous()
+            lw = module.k_norm.weight.float().contiguous()
+            lb = module.k_norm.bias.float().contiguous()
+            oq = torch.empty_like(pq)
+            ow = torch.empty_like(pw)
+            q_lib, w_lib = library()
+            q_ref, w_ref = formula()
+            q_diff = float((q_lib.float() - q_ref.float()).abs().max())
+            w_diff = float((w_lib - w_ref).abs().max())
+            timings = {}
+            for label, fn in (("library", library), ("torch_formula", formula), ("epilogues", epilogues_only)):
+                ms = []
+                for it in range(110):
+                    flush()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fn()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    if it >= 10:
+                        ms.append(e0.elapsed_time(e1))
+                timings[label] = time_stats(ms)
+        weight_bytes = (module.wq.weight.numel() + module.wk.weight.numel()) * 2 + module.weights_proj.weight.numel() * 4
+        epi_bytes = tokens * (128 * 2 * 2 + 64 * 128 * 2 * 2 + 64 * 4 * 2 + 8 + 8)
+        results[name] = {
+            "tokens": tokens,
+            **{f"{k}_us": v["median_us"] for k, v in timings.items()},
+            "speedup_vs_torch_formula": round(timings["torch_formula"]["median_us"] / timings["library"]["median_us"], 3),
+            "weight_bytes": weight_bytes,
+            "weight_stream_floor_us": round(weight_bytes / HBM_PEAK_GBS / 1e3, 3),
+            "epilogue_bytes": epi_bytes,
+            "epilogue_gbs": round(epi_bytes / (timings["epilogues"]["median_us"] * 1e-6) / 1e9, 1),
+            "max_abs_diff_vs_formula": {"queries": q_diff, "weights": w_diff},
+            "timings": timings,
+        }
+    dec = results["decode"]
+    line = {
+        "metric": "sidecar encoders: us per decode step (16 tokens: keys appended to the cache, queries + head weights)",
+        "value": dec["library_us"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": 100,
+        "warmup": 10,
+        "ms_per_step": round(dec["library_us"] / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "LightningIndexerSidecar(hidden 2048, 64 x 128, rope_dim 64), bf16, random init; "
+                   "decode: 16 tokens, prefill: 4096 tokens"},
+        "roofline": {"bound": "hbm", "achieved": round(dec["weight_bytes"] / (dec["library_us"] * 1e-6) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec["weight_bytes"] / (dec["library_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "decode step: weight streaming of wq/wk/weights_proj + epilogues",
+                     "algorithmic_bytes": dec["weight_bytes"]},
+        "shapes": results,
+        "timing": f"HIP events around each call, 512 MiB {args.flush} flush before each, median over 100",
+    }
+    write_table(args, line, [])
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

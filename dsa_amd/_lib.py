@@ -55,6 +55,11 @@ _SIGNATURES: dict[str, list] = {
     "dsa_topk": [_p, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p, _p],
     "dsa_topk_long": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_block_max": [_p, _i64, _i64, _i64, _i32, _p, _p],
+    "dsa_rope": [_p, _p, _p, _i64, _i32, _i32, _i32, ctypes.c_float, _i32, _p],
+    "dsa_encode_keys_epilogue": [_p, _i32, _i64, _p, _p, ctypes.c_float, _p, _i32, ctypes.c_float, _p, _i32, _i64,
+                                 _p, _i64, _i64, _i32, _p],
+    "dsa_encode_queries_epilogue": [_p, _p, _p, _i32, ctypes.c_float, ctypes.c_float, _p, _p, _i64, _i32, _i32,
+                                    _i32, _p],
     "dsa_block_key_norms": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p],
     "dsa_temporal_score_radius": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "dsa_temporal_step": [

@@ -1,25 +1,40 @@
-"""Batched / multi-query indexer scoring (``score_encoded``).
+"""Sidecar indexer: encoders and batched / multi-query scoring.
 
-Reference: ``LightningIndexerSidecar.score_encoded`` (sidecar.py:89-107):
-``[B,Q,H,D] x [B,K,D] -> [B,Q,K]`` fp32, ``ReLU(q.k) * w`` summed over heads.
-The sidecar's projections, RoPE and training live upstream of this path and
-are not part of this package.
+Reference: ``temporal_dsa/sidecar.py``.
+  * ``apply_noninterleaved_rope`` (sidecar.py:10-28) and the encoders of
+    ``LightningIndexerSidecar`` (sidecar.py:31-88): the projections wq / wk /
+    weights_proj are plain GEMMs (the platform BLAS through torch); the
+    LayerNorm, RoPE, head-weight scaling and the key-cache append after them
+    run in one HIP pass per row (``dsa_encode_keys_epilogue``,
+    ``dsa_encode_queries_epilogue``, ``dsa_rope``), with torch's per-op
+    rounding in the row dtype.  The module runs in its parameter dtype
+    (fp32 or bf16); autocast's mixed flow is not reproduced.
+  * ``score_encoded`` (sidecar.py:89-107): ``[B,Q,H,D] x [B,K,D] -> [B,Q,K]``
+    fp32, ``ReLU(q.k) * w`` summed over heads.
 
-Differences from the reference, all documented at the call:
+Differences of ``score_encoded`` from the reference, all documented at the call:
   * dots stay fp32 (the reference's bf16 einsum rounds each dot to bf16 before
     the ReLU; both agree within the 1e-2 relative bf16 tolerance);
   * ``causal=True`` masks key j of query t unless ``j <= t + causal_offset``
     (masked scores are -inf); the reference has no mask;
   * fp8 e4m3fn keys with one fp32 scale per 128 keys are accepted through
     ``key_scales`` ``[B, ceil(K/128)]``.
+The KL loss and the teacher target (sidecar.py:123-137) belong to training
+and are not part of this package.
 """
 
 from __future__ import annotations
 
+import math
+
 import torch
+from torch import nn
+from torch.nn import functional as F
 
 from . import _lib
 from .progressive_kernel import HEAD_DIM, HEADS
+
+_ROW_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 
 
 def score_encoded(
@@ -80,3 +95,178 @@ def score_encoded(
         _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
     )
     return out
+
+
+def _row_dtype(t: torch.Tensor) -> int:
+    try:
+        return _ROW_DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError("sidecar rows must be float32 or bfloat16") from None
+
+
+def _token_positions(positions, shape, device) -> torch.Tensor:
+    pos = torch.as_tensor(positions, device=device)
+    if pos.shape != shape:
+        pos = pos.expand(shape)
+    return pos.to(torch.int64).contiguous().reshape(-1)
+
+
+def apply_noninterleaved_rope(x: torch.Tensor, positions: torch.Tensor, *, theta: float = 10_000.0) -> torch.Tensor:
+    """Non-interleaved RoPE (reference sidecar.py:10-28) of x ``[..., d]``;
+    positions has shape ``x.shape[:-1]`` or ``x.shape[:-2]`` (one position
+    per token, shared by its heads)."""
+
+    if x.shape[-1] % 2:
+        raise ValueError("RoPE dimension must be even")
+    if not x.is_cuda:
+        raise ValueError("HIP kernels require GPU tensors")
+    dtype = _row_dtype(x)
+    d = x.shape[-1]
+    pos = torch.as_tensor(positions, device=x.device)
+    if tuple(pos.shape) == tuple(x.shape[:-1]):
+        heads = 1
+        tokens_shape = x.shape[:-1]
+    elif x.ndim >= 2 and tuple(pos.shape) == tuple(x.shape[:-2]):
+        heads = x.shape[-2]
+        tokens_shape = x.shape[:-2]
+    else:
+        raise ValueError("positions must match x.shape[:-1] or x.shape[:-2]")
+    if d > 256:
+        raise ValueError("RoPE rows of more than 256 dims are not supported")
+    rows = x.contiguous()
+    out = torch.empty_like(rows)
+    tokens = math.prod(tokens_shape)
+    _lib.call("dsa_rope", _lib.ptr(rows), _lib.ptr(out), _lib.ptr(_token_positions(pos, tokens_shape, x.device)),
+              tokens, heads, d, d, float(theta), dtype, _lib.stream_of(rows))
+    return out
+
+
+class LightningIndexerSidecar(nn.Module):
+    """The indexer sidecar (reference sidecar.py:31-121): same constructor,
+    parameters and initialisation; the encoders' epilogues run in HIP."""
+
+    def __init__(
+        self,
+        hidden_size: int = 2048,
+        heads: int = 64,
+        head_dim: int = 128,
+        rope_dim: int = 64,
+        rope_theta: float = 10_000.0,
+    ) -> None:
+        super().__init__()
+        if not 0 <= rope_dim <= head_dim or rope_dim % 2:
+            raise ValueError("rope_dim must be even and no larger than head_dim")
+        self.hidden_size = hidden_size
+        self.heads = heads
+        self.head_dim = head_dim
+        self.rope_dim = rope_dim
+        self.rope_theta = rope_theta
+        self.wq = nn.Linear(hidden_size, heads * head_dim, bias=False)
+        self.wk = nn.Linear(hidden_size, head_dim, bias=False)
+        self.k_norm = nn.LayerNorm(head_dim, eps=1e-6)
+        self.weights_proj = nn.Linear(hidden_size, heads, bias=False, dtype=torch.float32)
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        nn.init.normal_(self.wq.weight, mean=0.0, std=self.hidden_size**-0.5)
+        nn.init.normal_(self.wk.weight, mean=0.0, std=self.hidden_size**-0.5)
+        nn.init.normal_(self.weights_proj.weight, mean=0.0, std=self.hidden_size**-0.5)
+
+    def encode_keys(
+        self,
+        hidden: torch.Tensor,
+        positions: torch.Tensor,
+        *,
+        out: torch.Tensor | None = None,
+        out_rows: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """RoPE(LayerNorm(wk(hidden))) (sidecar.py:74-76) ``[..., head_dim]``.
+
+        With ``out`` (a key cache ``[rows, head_dim]``, fp32 or bf16) and
+        ``out_rows`` (int64, one cache row per token), the keys are written
+        into the cache rows instead and ``out`` is returned: the decode step's
+        append without a separate copy.  A token whose row lies outside the
+        cache is not written.  Inference only: no autograd graph is kept.
+        """
+
+        if not hidden.is_cuda:
+            raise ValueError("HIP kernels require GPU tensors")
+        proj = F.linear(hidden, self.wk.weight)
+        tokens_shape = proj.shape[:-1]
+        tokens = math.prod(tokens_shape)
+        flat = proj.reshape(tokens, self.head_dim).contiguous()
+        pos = _token_positions(positions, tokens_shape, hidden.device)
+        ln_w = self.k_norm.weight.detach().to(torch.float32).contiguous()
+        ln_b = self.k_norm.bias.detach().to(torch.float32).contiguous()
+        if out is None:
+            result = torch.empty_like(flat)
+            rows = None
+            target = result
+        else:
+            if out.ndim != 2 or out.shape[1] != self.head_dim or not out.is_contiguous():
+                raise ValueError("out must be a contiguous [rows, head_dim] key cache")
+            if out_rows is None or out_rows.numel() != tokens:
+                raise ValueError("out_rows must give one cache row per token")
+            # (rows outside the cache are skipped by the kernel: no host sync here)
+            rows = out_rows.to(device=hidden.device, dtype=torch.int64).contiguous()
+            target = out
+        _lib.call(
+            "dsa_encode_keys_epilogue", _lib.ptr(flat), _row_dtype(flat), self.head_dim, _lib.ptr(ln_w),
+            _lib.ptr(ln_b), float(self.k_norm.eps), _lib.ptr(pos), self.rope_dim, float(self.rope_theta),
+            _lib.ptr(target), _row_dtype(target), self.head_dim, _lib.ptr(rows), target.shape[0], tokens,
+            self.head_dim, _lib.stream_of(flat),
+        )
+        if out is not None:
+            return out
+        return result.reshape(*tokens_shape, self.head_dim)
+
+    def encode_queries(self, hidden: torch.Tensor, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(queries ``[..., heads, head_dim]``, weights ``[..., heads]`` fp32)
+        (sidecar.py:78-88)."""
+
+        if not hidden.is_cuda:
+            raise ValueError("HIP kernels require GPU tensors")
+        proj = F.linear(hidden, self.wq.weight)
+        proj_w = F.linear(hidden.float(), self.weights_proj.weight.float())
+        tokens_shape = proj.shape[:-1]
+        tokens = math.prod(tokens_shape)
+        flat = proj.reshape(tokens, self.heads * self.head_dim).contiguous()
+        flat_w = proj_w.reshape(tokens, self.heads).contiguous()
+        pos = _token_positions(positions, tokens_shape, hidden.device)
+        queries = torch.empty_like(flat)
+        weights = torch.empty_like(flat_w)
+        _lib.call(
+            "dsa_encode_queries_epilogue", _lib.ptr(flat), _lib.ptr(flat_w), _lib.ptr(pos), self.rope_dim,
+            float(self.rope_theta), float((self.heads * self.head_dim) ** -0.5), _lib.ptr(queries),
+            _lib.ptr(weights), tokens, self.heads, self.head_dim, _row_dtype(flat), _lib.stream_of(flat),
+        )
+        return (queries.reshape(*tokens_shape, self.heads, self.head_dim), weights.reshape(*tokens_shape, self.heads))
+
+    def score_encoded(
+        self,
+        queries: torch.Tensor,
+        weights: torch.Tensor,
+        keys: torch.Tensor,
+        *,
+        key_chunk_size: int | None = None,
+    ) -> torch.Tensor:
+        """``[B,Q,H,D] x [B,K,D] -> [B,Q,K]`` (sidecar.py:89-107) on the HIP
+        scoring kernel: 64 heads x 128 dims, bf16/fp16 queries (fp32 keys are
+        cast to the query dtype, as autocast does in the reference's flow)."""
+
+        if keys.is_floating_point() and keys.dtype == torch.float32 and queries.dtype != torch.float32:
+            keys = keys.to(queries.dtype)
+        return score_encoded(queries, weights, keys, key_chunk_size=key_chunk_size)
+
+    def forward(
+        self,
+        query_hidden: torch.Tensor,
+        key_hidden: torch.Tensor,
+        query_positions: torch.Tensor,
+        key_positions: torch.Tensor,
+        *,
+        key_chunk_size: int | None = None,
+    ) -> torch.Tensor:
+        queries, weights = self.encode_queries(query_hidden, query_positions)
+        keys = self.encode_keys(key_hidden, key_positions)
+        return self.score_encoded(queries, weights, keys, key_chunk_size=key_chunk_size)

@@ -385,6 +385,42 @@ int dsa_temporal_score_radius(const float* q_now, const float* q_prev, const flo
                               const float* w_prev, const float* block_key_norm, int64_t blocks,
                               int64_t heads, int64_t dim, float* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Sidecar encoder epilogues (sidecar.py:10-88).  The projections wq / wk /
+ * weights_proj are plain GEMMs done by the caller's BLAS; these entry points
+ * run everything after them in one pass per row.  dtype codes: DSA_DTYPE_F32
+ * or DSA_DTYPE_BF16; arithmetic follows torch's per-op rounding in that dtype.
+ * ------------------------------------------------------------------------ */
+
+/* apply_noninterleaved_rope (sidecar.py:10-28) on the first rope_dim dims of
+ * every head: x, out [tokens][heads][dim] (dim even, <= 256), positions [tokens]
+ * (one position per token, shared by its heads), inv_freq_i = theta^(-i/half),
+ * pairs (i, i + half) rotated by position * inv_freq_i. */
+int dsa_rope(const void* x, void* out, const int64_t* positions, int64_t tokens, int32_t heads,
+             int32_t dim, int32_t rope_dim, float theta, int32_t dtype, void* stream);
+
+/* encode_keys after wk (sidecar.py:74-76 and 67-72): LayerNorm over dim
+ * (fp32 weight/bias, biased variance, eps), then RoPE on the first rope_dim
+ * dims, written to out row out_rows[t] (or t when out_rows is NULL) so that a
+ * decode step appends straight into its key cache; a token whose row is
+ * outside [0, out_row_limit) is not written.  proj [tokens] rows of
+ * proj_row_stride elements (proj_dtype), out rows of out_row_stride elements
+ * (out_dtype). */
+int dsa_encode_keys_epilogue(const void* proj, int32_t proj_dtype, int64_t proj_row_stride,
+                             const float* ln_weight, const float* ln_bias, float ln_eps,
+                             const int64_t* positions, int32_t rope_dim, float theta, void* out,
+                             int32_t out_dtype, int64_t out_row_stride, const int64_t* out_rows,
+                             int64_t out_row_limit, int64_t tokens, int32_t dim, void* stream);
+
+/* encode_queries after wq / weights_proj (sidecar.py:78-88): RoPE on every
+ * head of proj [tokens][heads][dim] (dtype) into out, and
+ * out_weights = proj_weights * weight_scale (fp32 [tokens][heads]; the
+ * reference's scale is (heads * dim)^-0.5). */
+int dsa_encode_queries_epilogue(const void* proj, const float* proj_weights, const int64_t* positions,
+                                int32_t rope_dim, float theta, float weight_scale, void* out,
+                                float* out_weights, int64_t tokens, int32_t heads, int32_t dim,
+                                int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
