@@ -7,8 +7,11 @@ the names of the reference package ``temporal_dsa``:
 
   progressive_kernel  dense / H8 / masked / progressive scoring
   metrics             stable_topk, topk, topk_recall
-  sidecar             score_encoded (batched and multi-query scoring)
-  verifier_scoring    score_head_sparse, dynamic_head_indices
+  verifier_scoring    score_head_sparse, score_dim_sparse, normalized_hadamard,
+                      fake_symmetric_quantize, dynamic_head_indices
+  verifier            live two-path verifier step, dim sketches, step metrics
+  approx              device own-trajectory policy state and step
+  sidecar             LightningIndexerSidecar encoders and score_encoded
   certified           block_key_norms, temporal_score_radius
   temporal            device temporal pruning (seed, hot-first, running top-K)
 """

@@ -71,6 +71,16 @@ _SIGNATURES: dict[str, list] = {
         _i32, _i32, _i32, _p, _i64, _p,
     ],
     "dsa_approx_init_state": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p],
+    "dsa_verifier_step": [
+        _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64,  # temporal step and policy state
+        _p, _p, _i64, _p, _p, _i64,  # spec, head ids, sketches
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,  # outputs
+        _i64, _i64, _i64, _i32, _i32, _i32, _p, _i64, _p,
+    ],
+    "dsa_dim_sketch": [_p, _i64, _i32, _i32, _p, _i32, _i32, _i32, ctypes.c_float, _p, _i32, _p],
+    "dsa_abs_max": [_p, _i64, _i32, _p, _p],
+    "dsa_fake_quantize": [_p, _i64, _i32, _i32, ctypes.c_float, _p, _p, _p],
+    "dsa_sketch_scores": [_p, _p, _i64, _i32, _p, _i32, ctypes.c_float, _i32, _i64, _p, _p],
 }
 _RESTYPES: dict[str, object] = {
     "dsa_topk_long_workspace_bytes": (_i64, [_i64, _i64, _i64]),
@@ -96,6 +106,20 @@ class ApproxPolicyC(ctypes.Structure):
         ("recent_window", _i32),
         ("full_refresh", _i32),
         ("reserved", _i32),
+    ]
+
+
+class VerifierSpecC(ctypes.Structure):
+    """``dsa_verifier_spec`` of include/dsa_amd.h."""
+
+    _fields_ = [
+        ("path", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("promotion", ctypes.c_int32),
+        ("sketch_codes", ctypes.c_int32),
+        ("rescue_fraction", ctypes.c_double),
+        ("promotion_threshold", ctypes.c_float),
+        ("sketch_scale", ctypes.c_float),
     ]
 
 

@@ -1,0 +1,229 @@
+// Internal interface of the temporal step shared by temporal.hip and
+// verifier.hip: argument and workspace layouts, the scan-order sort, the
+// unit scorer, and the two halves of a step (the seeded block scan; then the
+// histogram, the top-k select and the policy-state update).
+#pragma once
+
+#include "common.hpp"
+#include "dsa_amd.h"
+#include "indexer.hpp"
+#include "select.hpp"
+#include "waveops.hpp"
+
+#include <cmath>
+
+namespace dsa {
+
+constexpr int kMaxTemporalBlocks = 2048;  // blocks per row (sorted in one workgroup)
+constexpr int kMaxMerge = 8192;            // k + one wave's keys, merged in LDS
+constexpr uint32_t kFarKey = 0x00ffffffu;  // a key index whose rows lie past every buffer
+constexpr int kDigitBinsT = 2048;          // 11-bit radix digits of the threshold refresh
+
+struct TemporalWorkspace {
+  uint32_t* tau;        // [rows] ordered key of the threshold in force
+  uint32_t* run;        // [rows][k] ordered keys of the k largest evaluated scores
+  uint32_t* order;      // [rows][blocks] block ids in scan order
+  double* upper;        // [rows][blocks] U_b, in double like the float64 reference
+  uint32_t* seed_mask;  // [rows][ceil(L / 32)] keys evaluated as seeds
+  SelectWorkspace select;  // final top-k over the evaluated keys
+  int64_t bytes;
+};
+
+inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t length, int64_t k, int32_t block_size) {
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  auto round = [](int64_t bytes) { return (bytes + 255) / 256 * 256; };
+  const int64_t tau_off = 0;
+  const int64_t run_off = tau_off + round(rows * 4);
+  const int64_t order_off = run_off + round(rows * k * 4);
+  const int64_t upper_off = order_off + round(rows * blocks * 4);
+  const int64_t mask_off = upper_off + round(rows * blocks * 8);
+  const int64_t select_off = mask_off + round(rows * ((length + 31) / 32) * 4);
+  TemporalWorkspace ws;
+  const uintptr_t p = reinterpret_cast<uintptr_t>(base);
+  ws.select = select_workspace_layout(base ? reinterpret_cast<void*>(p + select_off) : nullptr, rows, length);
+  ws.bytes = select_off + round(ws.select.bytes);
+  ws.tau = base ? reinterpret_cast<uint32_t*>(p + tau_off) : nullptr;
+  ws.run = base ? reinterpret_cast<uint32_t*>(p + run_off) : nullptr;
+  ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
+  ws.upper = base ? reinterpret_cast<double*>(p + upper_off) : nullptr;
+  ws.seed_mask = base ? reinterpret_cast<uint32_t*>(p + mask_off) : nullptr;
+  return ws;
+}
+
+// Own-trajectory policy state (approx.py:42-50), [rows][stride] per field.
+struct ApproxDev {
+  float* last_max;
+  float* ema;
+  float* vol;
+  int16_t* age;
+  int16_t* cold;
+  int64_t stride;
+  const double* gamma_rows;  // per-row gamma, or null for p.gamma
+  dsa_approx_policy p;
+};
+
+struct TemporalArgs {
+  const uint16_t* q;      // [rows][64][128]
+  const float* w;         // [rows][64]
+  const uint8_t* keys;    // [rows][key_stride] key rows (the first length are scored)
+  int64_t key_stride;     // key rows between sequences
+  const float* scales;    // fp8: [rows][ceil(key_stride / 128)]
+  const float* prev_max;  // [rows][prev_blocks]
+  const int64_t* seeds;   // [rows][k]
+  const float* gamma;     // [rows]
+  float* scores;          // [rows][length]
+  uint8_t* evaluated;     // [rows][blocks]
+  int32_t* qk_scored;     // [rows]
+  int32_t rows, length, k, block_size, blocks, prev_length, prev_blocks;
+  int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper
+  int32_t wave_start, wave_len;
+  int32_t policy_mode;    // 0: bound prev_max + gamma (replay filter); 1: own-trajectory policy
+  ApproxDev ap;
+  TemporalWorkspace ws;
+};
+
+// Order-preserving double -> uint64 map (NaN as -inf, -0.0 as +0.0, so the
+// sort sees the values a float64 sort key would).
+__device__ __forceinline__ uint64_t double_to_ordered(double d) {
+  if (__builtin_isnan(d)) d = -HUGE_VAL;
+  if (d == 0.0) d = 0.0;
+  const uint64_t u = (uint64_t)__double_as_longlong(d);
+  return (u >> 63) ? ~u : (u | (1ull << 63));
+}
+
+// Risk of a block under the policy (approx.py:178-189).  The float32 product
+// volatility_lambda * volatility and the left-to-right float64 sums follow
+// numpy's evaluation of the reference expression.
+__device__ __forceinline__ double policy_risk(const dsa_approx_policy& p, double gamma, float last_max, float ema,
+                                              float vol, int age) {
+#pragma clang fp contract(off)
+  const double aged = p.age_slope * (double)age;
+  if (p.risk_model == DSA_RISK_EMA) {
+    const float spread = (float)p.volatility_lambda * vol;
+    return (((double)ema + (double)spread) + gamma) + aged;
+  }
+  return ((double)last_max + gamma) + aged;
+}
+
+// Sort entries: ascending (lo >> 31, hi, lo & 0x7fffffff).  Branch-free: the
+// sort is VALU-bound on one CU, so each compare is a handful of v_cmp with
+// the masks combined on the scalar unit.
+__device__ __forceinline__ bool sorts_before(uint64_t hi_a, uint32_t lo_a, uint64_t hi_b, uint32_t lo_b) {
+  const uint32_t ga = lo_a >> 31;
+  const uint32_t gb = lo_b >> 31;
+  const uint32_t aa = lo_a & 0x7fffffffu;
+  const uint32_t ab = lo_b & 0x7fffffffu;
+  return (ga < gb) | ((ga == gb) & ((hi_a < hi_b) | ((hi_a == hi_b) & (aa < ab))));
+}
+
+constexpr int kSortN = kMaxTemporalBlocks;  // most entries one 1024-thread workgroup sorts
+
+// Bitonic sort of n entries (a power of two, 2 <= n <= kSortN) held two per
+// thread (entries 2t and 2t+1 of thread t; threads with 2t >= n only join
+// the barriers).  Compare-exchange partners at distance 1 are in the same
+// thread, at distance 2..64 in the same wave (lane shuffles, no barrier), and
+// further apart they meet through LDS (xh, xl: kSortN entries).  Partners of
+// an active entry are active: e ^ stride < n for every e < n.
+__device__ inline void block_sort(uint64_t (&h)[2], uint32_t (&l)[2], uint64_t* xh, uint32_t* xl, int n) {
+  const int t = threadIdx.x;
+  const bool active = 2 * t < n;
+  for (int size = 2; size <= n; size <<= 1) {
+    const bool up = ((2 * t) & size) == 0;
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride == 1) {
+        const bool second_first = sorts_before(h[1], l[1], h[0], l[0]);
+        const bool same = (h[0] == h[1]) & (l[0] == l[1]);
+        const bool swap = up ? second_first : !(second_first | same);
+        const uint64_t h0 = swap ? h[1] : h[0];
+        const uint64_t h1 = swap ? h[0] : h[1];
+        const uint32_t l0 = swap ? l[1] : l[0];
+        const uint32_t l1 = swap ? l[0] : l[1];
+        h[0] = h0;
+        h[1] = h1;
+        l[0] = l0;
+        l[1] = l1;
+        continue;
+      }
+      const int mask = stride >> 1;  // partner thread t ^ mask
+      const bool lower = (t & mask) == 0;
+      uint64_t oh[2];
+      uint32_t ol[2];
+      if (stride <= 64) {
+        if (!active) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          oh[j] = __shfl_xor(h[j], mask, kWave);
+          ol[j] = __shfl_xor(l[j], mask, kWave);
+        }
+      } else {
+        if (active) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            xh[2 * t + j] = h[j];
+            xl[2 * t + j] = l[j];
+          }
+        }
+        __syncthreads();
+        if (active) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            oh[j] = xh[(2 * t + j) ^ stride];
+            ol[j] = xl[(2 * t + j) ^ stride];
+          }
+        }
+        __syncthreads();
+        if (!active) continue;
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // other-first decides for the lower entry of an ascending pair and the
+        // upper entry of a descending one; the rest take the other entry iff
+        // it is strictly later (equal entries are padding).
+        const bool other_first = sorts_before(oh[j], ol[j], h[j], l[j]);
+        const bool same = (oh[j] == h[j]) & (ol[j] == l[j]);
+        const bool take = (up == lower) ? other_first : !(other_first | same);
+        h[j] = take ? oh[j] : h[j];
+        l[j] = take ? ol[j] : l[j];
+      }
+    }
+  }
+}
+
+// Scores 64 keys of one row with the dense kernel's unit code: lane (r, g)
+// loads, for each tile t, its slice of key tile_key[t] (kFarKey: nothing is
+// loaded and the result is not a key's score).  Lane l returns the score of
+// the key that lane (l & 15, .) of tile l >> 4 loaded.
+template <class Tag, class KF>
+__device__ __forceinline__ float score_unit(const TemporalArgs& a, int row, const int (&tile_key)[4],
+                                            int r, int g) {
+  uint4 qa[4][4];
+  float wr[4][4];
+  load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads,
+                                          r, g, qa, wr);
+  const BufferRsrc keys = make_buffer(a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
+                                      (uint32_t)a.length * KF::kRowBytes);
+  uint4 buf[4][KF::kRaw];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) KF::load_buf(keys, tile_key[t], g, buf[t]);
+  float s[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[t]);
+  return unit_reduce(s, g);
+}
+
+// First half of a step: clean slate, bounds and scan order, the seeds, and the
+// block scan (with threshold refreshes when wave > 0).  Leaves the scores of
+// the evaluated keys (-inf elsewhere) and the refreshed-block flags.
+int temporal_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream);
+
+// Second half: the select histogram and the keys-scored count, the stable
+// top-k of the scores row into out_topk, and (policy mode) the state update
+// of every block refreshed by the scan or flagged in `rescued` (may be null).
+int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, hipStream_t stream);
+
+// Shared argument checks of the step entry points.
+int check_step(const void* queries, const void* keys, int64_t key_stride, const float* key_scales,
+               int64_t prev_length, int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
+               int32_t key_dtype, const void* workspace);
+
+}  // namespace dsa

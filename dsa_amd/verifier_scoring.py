@@ -1,13 +1,17 @@
-"""Head-sparse verifier scoring and per-query head routing.
+"""Verifier scores on the GPU: head-sparse and dim-sparse paths, routing.
 
-Mirrors the hot-path part of ``temporal_dsa.verifier_scoring`` (reference
-``src/temporal_dsa/verifier_scoring.py:49-92`` ``score_head_sparse`` and
-``:142-159`` ``dynamic_head_indices``).  The dim-sparse / Hadamard verifier
-variants are outside this package.
+Mirrors ``temporal_dsa.verifier_scoring`` (reference
+``src/temporal_dsa/verifier_scoring.py``): ``normalized_hadamard`` (:9-26),
+``fake_symmetric_quantize`` (:29-41), ``score_head_sparse`` (:49-92),
+``score_dim_sparse`` (:95-139), ``dynamic_head_indices`` (:142-159) and
+``layer_energy_dimensions`` (:162-170).  Dot products accumulate in float32
+(the reference's einsum rounds each head's dot to the input dtype; the
+kernels keep float32, as the reference's own Triton kernels do).
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -101,3 +105,96 @@ def score_head_sparse(
         _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
     )
     return out
+
+
+def normalized_hadamard(tensor: torch.Tensor) -> torch.Tensor:
+    """Orthonormal Walsh-Hadamard transform on the last axis (a power of two
+    <= 128), each butterfly stage rounded to the tensor's dtype like the
+    reference's tensor arithmetic (verifier_scoring.py:9-26)."""
+
+    from .verifier import dim_sketch
+
+    size = tensor.shape[-1]
+    if size <= 0 or size & (size - 1):
+        raise ValueError("Hadamard dimension must be a positive power of two")
+    return dim_sketch(tensor, torch.arange(size), rotation="hadamard")
+
+
+def fake_symmetric_quantize(tensor: torch.Tensor, bits: int, scale: float | None = None):
+    """(fake-quantized tensor, scale) with a fixed symmetric tensor scale
+    (verifier_scoring.py:29-41): scale = max|x| / (2^(bits-1) - 1) unless
+    given, at least 1e-12."""
+
+    from .verifier import _tensor_scale, fake_quantize
+
+    if bits not in {2, 4, 8}:
+        raise ValueError("bits must be one of 2, 4, 8")
+    if not tensor.is_cuda:
+        raise ValueError("HIP kernels require GPU tensors")
+    if tensor.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError("fake quantization takes fp32, fp16 or bf16 tensors")
+    scale = _tensor_scale(tensor.contiguous(), bits) if scale is None else max(float(scale), 1e-12)
+    return fake_quantize(tensor, bits, scale), scale
+
+
+def score_dim_sparse(
+    queries: torch.Tensor,
+    weights: torch.Tensor,
+    keys: torch.Tensor,
+    dimension_indices,
+    *,
+    rotation: str = "none",
+    bits: int | None = None,
+    query_scale: float | None = None,
+    key_scale: float | None = None,
+    query_chunk_size: int = 1,
+    key_chunk_size: int = 8192,
+) -> torch.Tensor:
+    """All-head partial-dimension verifier scores, fp32 ``[Q, K]``
+    (verifier_scoring.py:95-139).  BF16 queries ``[Q, H, D]`` (H <= 64, D a
+    power of two <= 128) and keys ``[K, D]``; the dimension count must be a
+    multiple of 8.  The chunk sizes are accepted for API compatibility."""
+
+    from .verifier import dim_sketch
+
+    del query_chunk_size, key_chunk_size
+    if queries.ndim != 3 or weights.shape != queries.shape[:2] or keys.ndim != 2:
+        raise ValueError("expected queries [Q,H,D], weights [Q,H], keys [K,D]")
+    if rotation not in ("none", "hadamard"):
+        raise ValueError("rotation must be 'none' or 'hadamard'")
+    if not (queries.is_cuda and weights.is_cuda and keys.is_cuda):
+        raise ValueError("HIP kernels require GPU tensors")
+    if queries.dtype != torch.bfloat16:
+        raise ValueError("the sketch kernels take BF16 queries")
+    num_queries, heads, dim = queries.shape
+    if keys.shape[1] != dim:
+        raise ValueError("queries and keys disagree on the head dimension")
+    if heads > 64:
+        raise ValueError("at most 64 heads are supported")
+    dims = torch.as_tensor(dimension_indices, device=queries.device).reshape(-1)
+    width = dims.numel()
+    if width % 8 or width > 128:
+        raise ValueError("the dimension count must be a multiple of 8, at most 128")
+    keys = keys.to(queries.dtype)
+    q_sketch = dim_sketch(queries, dims, rotation=rotation, bits=bits, scale=query_scale)
+    k_sketch = dim_sketch(keys, dims, rotation=rotation, bits=bits, scale=key_scale)
+    out = torch.empty((num_queries, keys.shape[0]), device=queries.device, dtype=torch.float32)
+    if num_queries == 0 or keys.shape[0] == 0:
+        return out
+    w = weights.to(torch.float32).contiguous()
+    _lib.call(
+        "dsa_sketch_scores", _lib.ptr(q_sketch.contiguous()), _lib.ptr(w), num_queries, heads,
+        _lib.ptr(k_sketch.contiguous()), 0, 0.0, width, keys.shape[0], _lib.ptr(out), _lib.stream_of(queries),
+    )
+    return out
+
+
+def layer_energy_dimensions(queries: torch.Tensor, keys: torch.Tensor, width: int) -> np.ndarray:
+    """A fixed dimension subset from validation q/k energy
+    (verifier_scoring.py:162-170): the ``width`` dims of largest
+    mean(q^2) * mean(k^2), ascending.  A one-off calibration on the host."""
+
+    q = queries.detach().float().cpu().numpy()
+    k = keys.detach().float().cpu().numpy()
+    energy = (q * q).reshape(-1, q.shape[-1]).mean(axis=0, dtype=np.float32) * (k * k).mean(axis=0, dtype=np.float32)
+    return np.sort(np.argsort(-energy, kind="stable")[:width]).astype(np.int64)

@@ -365,6 +365,89 @@ int dsa_approx_init_state(const float* scores, int64_t score_stride, const int64
                           void* stream);
 
 /* ------------------------------------------------------------------------
+ * Two-path verifier step (verifier.py:173-392 verifier_step with
+ * apply_rescue_to_state :103-170; the reference replays it offline over
+ * recorded dense and verifier score rows, here it is a live decode step).
+ *
+ * The own-trajectory temporal scan of dsa_approx_step, then a verifier score
+ * of every key the scan left unscored ("cold"):
+ *   DSA_VERIFIER_HEAD: sum over spec->width selected heads (head_ids [width],
+ *     or [batch][head_id_stride] per sequence, e.g. dynamic_head_indices)
+ *     of w_h relu(q_h . k) over the full key rows;
+ *   DSA_VERIFIER_DIM: all 64 heads over spec->width sketch dims: query_sketch
+ *     [batch][64][width] bf16 against key_sketch [batch][sketch_stride][width]
+ *     (int8 codes scaled by spec->sketch_scale and rounded to bf16, or bf16
+ *     values), as written by dsa_dim_sketch.
+ * Cold blocks are ranked by their largest cold verifier score (larger first,
+ * lower block id on ties; ranking [batch][blocks] lists them, -1 after, and
+ * is nullable); the first min(cold, ceil(rescue_fraction * cold)) are rescued
+ * (spec->promotion 0), or every cold block whose score is >= the float32
+ * promotion_threshold (1).  Rescued blocks' cold keys are scored in full;
+ * out_topk is the stable top-k of every scored key (ascending index).  The
+ * state is then advanced as by dsa_approx_step with rescued blocks updated
+ * like refreshed ones and the cold streak restarted from the final top-k.
+ * Outputs: scores (dense score of every scored key, -inf elsewhere),
+ * verifier_scores (nullable; cold keys, -inf elsewhere), block_scores and
+ * cold_count (cold keys per block), evaluated_blocks (temporal refreshes),
+ * rescued_blocks, qk_scored (temporal exact keys), counts [batch][4] = cold
+ * keys, cold blocks, rescued blocks, rescued cold keys.
+ * Limits as dsa_approx_step; the dim path takes bf16 queries.
+ * ------------------------------------------------------------------------ */
+#define DSA_VERIFIER_HEAD 0
+#define DSA_VERIFIER_DIM 1
+
+typedef struct dsa_verifier_spec {
+  int32_t path;         /* DSA_VERIFIER_* */
+  int32_t width;        /* head path: 1..64 heads; dim path: multiple of 8 in [8, 128] */
+  int32_t promotion;    /* 0: global budget (rescue_fraction), 1: fixed threshold */
+  int32_t sketch_codes; /* dim path: 1 = int8 codes, 0 = bf16 values */
+  double rescue_fraction;
+  float promotion_threshold;
+  float sketch_scale;
+} dsa_verifier_spec;
+
+int dsa_verifier_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
+                      const float* key_scales, const dsa_approx_policy* policy, const double* gamma_rows,
+                      int64_t prev_length, const int64_t* prev_topk, float* last_max, float* ema,
+                      float* volatility, int16_t* age, int16_t* cold_streak, int64_t state_stride,
+                      const dsa_verifier_spec* spec, const int32_t* head_ids, int64_t head_id_stride,
+                      const void* query_sketch, const void* key_sketch, int64_t sketch_stride, float* scores,
+                      float* verifier_scores, float* block_scores, uint8_t* cold_count, uint8_t* evaluated_blocks,
+                      uint8_t* rescued_blocks, int32_t* ranking, int64_t* out_topk, int32_t* qk_scored,
+                      int32_t* counts, int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
+                      int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Dimension sketch of rows x [rows][dim] (verifier_scoring.py:9-41, 95-139):
+ * the normalized Walsh-Hadamard transform over dim (a power of two <= 128;
+ * when rotate != 0), each butterfly sum and the final multiply by dim^-0.5
+ * rounded to dtype (F32 / F16 / BF16), then the dims listed in dims [width]
+ * (NULL: the first width), then, when bits is 2, 4 or 8, symmetric
+ * quantization with limit 2^(bits-1) - 1: code = clamp(rint(v / scale)).
+ * out [rows][width]: int8 codes (out_codes != 0) or values in dtype
+ * (code * scale rounded to dtype when quantized). */
+int dsa_dim_sketch(const void* x, int64_t rows, int32_t dim, int32_t dtype, const int32_t* dims, int32_t width,
+                   int32_t rotate, int32_t bits, float scale, void* out, int32_t out_codes, void* stream);
+
+/* max |x| over n values (fake_symmetric_quantize's tensor scale,
+ * verifier_scoring.py:37-38), written to *out as fp32. */
+int dsa_abs_max(const void* x, int64_t n, int32_t dtype, float* out, void* stream);
+
+/* Elementwise symmetric fake quantization (verifier_scoring.py:29-41):
+ * codes (nullable) = clamp(rint(x / scale), +-(2^(bits-1) - 1)); values
+ * (nullable) = code * scale rounded to dtype. */
+int dsa_fake_quantize(const void* x, int64_t n, int32_t dtype, int32_t bits, float scale, void* values,
+                      int8_t* codes, void* stream);
+
+/* All-head sketch scores (score_dim_sparse, verifier_scoring.py:95-139, after
+ * the sketches): out[q][key] = sum_h w[q][h] relu(qs[q][h] . ks[key]) for
+ * query sketches [queries][heads][width] bf16 (heads <= 64) and key sketches
+ * [keys][width] (int8 codes scaled by sketch_scale and rounded to bf16, or
+ * bf16 values); fp32 dot products. */
+int dsa_sketch_scores(const void* query_sketch, const float* weights, int64_t queries, int32_t heads,
+                      const void* key_sketch, int32_t sketch_codes, float sketch_scale, int32_t width, int64_t keys,
+                      float* out, void* stream);
+
+/* ------------------------------------------------------------------------
  * Per-block maxima of score rows (replay.py:149-150 _block_max,
  * approx.py:53-55): out[r, b] = max(scores[r, b*bs : min(len, (b+1)*bs)]).
  * block_size is any positive value.
