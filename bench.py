@@ -45,11 +45,12 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--config", choices=("c2", "c3", "c4", "c5", "progressive", "sidecar"), default="c2",
+    parser.add_argument("--config", choices=("c2", "c3", "c4", "c5", "progressive", "sidecar", "verifier"), default="c2",
                         help="c2: the headline decode step (default); c3: temporal replay over 256 decode steps; "
                         "c4: causal prefill indexer + top-512; c5: fp8 long-context decode; "
                         "progressive: the reference's method comparison (full / H8 / two-pass / fused); "
-                        "sidecar: the indexer's query/key encoders at the decode and prefill shapes")
+                        "sidecar: the indexer's query/key encoders at the decode and prefill shapes; "
+                        "verifier: the live two-path verifier step against the dense step (C3 shape)")
     parser.add_argument("--out", default=None, help="c4/c5/progressive: also write the full table (JSON) here")
     parser.add_argument("--flush", choices=("read", "write"), default="read",
                         help="c4/c5/progressive: cache flush before each timed replay: read 512 MiB (default) or "
@@ -121,8 +122,9 @@ def main() -> None:
     if args.config == "c3":
         run_c3(args)
         return
-    if args.config in ("c4", "c5", "progressive", "sidecar"):
-        {"c4": run_c4, "c5": run_c5, "progressive": run_progressive, "sidecar": run_sidecar}[args.config](args)
+    if args.config in ("c4", "c5", "progressive", "sidecar", "verifier"):
+        {"c4": run_c4, "c5": run_c5, "progressive": run_progressive, "sidecar": run_sidecar,
+         "verifier": run_verifier}[args.config](args)
         return
     import torch
 
@@ -1149,6 +1151,159 @@ def run_sidecar(args) -> None:
         "timing": f"HIP events around each call, 512 MiB {args.flush} flush before each, median over 100",
     }
     write_table(args, line, [])
+    print(json.dumps(line), flush=True)
+
+
+
+# --------------------------------------------------------------------------
+# Two-path verifier (live decode step) at the C3 shape
+# --------------------------------------------------------------------------
+VERIFIER_STEPS = 32
+VERIFIER_GAMMA_SIGMA = (-0.25, -0.5, -1.0)  # margins of the temporal policy, in units of the score std
+VERIFIER_HEADLINE_GAMMA = -0.5
+VERIFIER_CONFIGS = (
+    # name, path, width, rescue fraction, dims strategy, bits
+    ("head_dynamic_abs_w8_b64_r0.1", "head", 8, 0.1, None, None),
+    ("head_dynamic_abs_w16_b64_r0.1", "head", 16, 0.1, None, None),
+    ("dim_had_even_w16_b64_r0.1", "dim", 16, 0.1, "even", None),
+    ("dim_had_random_w32_int4_b64_r0.1", "dim", 32, 0.1, "random", 4),
+)
+
+
+def run_verifier(args) -> None:
+    """The live verifier step (reference verifier.py:173-392 as a decode
+    step) on the C3 shape: B=4 sequences from 16384 keys, one key appended per
+    step, K=2048, block 64, the reference's selected two-path configs
+    (configs/two_path_full_selected.json: head width 8 / 16 with dynamic
+    |w| routing, dim width 16 even / 32 random with a Hadamard rotation) over a
+    dynamic previous-max own-trajectory policy at three margins, beside the
+    temporal step alone and the dense step
+    (scores + exact top-k).  HIP events around each step (eager, every launch
+    included), median over the steps; recall and byte accounting from the
+    reference's metrics dict against the dense step of the same inputs."""
+
+    import numpy as np
+    import torch
+
+    from dsa_amd import _lib, approx, decode, verifier, verifier_scoring
+
+    _lib.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    keys, w, queries = c3_inputs(device)
+    steps = min(VERIFIER_STEPS, len(queries) - 1)
+    k, block = C3_TOPK, 64
+    start = C3_LENGTH
+    flush = make_flush(args, device)
+
+    def timed(fn):
+        flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return out, e0.elapsed_time(e1)
+
+    # the dense step of every decode step: truth for the metrics, and the baseline timing
+    dense_rows, dense_ms = [], []
+    for t in range(steps + 1):
+        cur = start + t
+        kv = keys[:, :cur].contiguous()
+        (idx, sc), ms = timed(lambda: decode.indexer_topk(queries[t], w, kv, k, return_scores=True))
+        dense_rows.append(sc)
+        if t:
+            dense_ms.append(ms)
+    sigma = float(dense_rows[0].std())
+    blocks = -(-(start + steps) // block)
+    wave = c3_wave(blocks, block, args.c3_refreshes)
+    rows = []
+    summary = {}
+    for gamma_sigma in VERIFIER_GAMMA_SIGMA:
+        policy = approx.ApproxPolicy(name="dynamic_previous_max", gamma=gamma_sigma * sigma, cold_streak=0,
+                                     dynamic_threshold=True, order="previous_max")
+        runs = [("temporal_only", None, 0, 0.0, None, None), *VERIFIER_CONFIGS]
+        for name, path, width, fraction, strategy, bits in runs:
+            state = approx.initialize_state(dense_rows[0], k=k, block_size=block, capacity=start + steps)
+            cfg = None
+            kwargs = {}
+            if path is not None:
+                cfg = verifier.VerifierConfig(
+                    name=name, path=path, width=width, score_ratio=width / 64 if path == "head" else width / 128,
+                    block_size=block, rescue_fraction=fraction,
+                    sketch_bytes_per_token=0.0 if path == "head" else width * (bits or 16) / 8)
+            if path == "dim":
+                dims = (np.linspace(0, 127, width).astype(np.int64) if strategy == "even"
+                        else np.sort(np.random.default_rng(SEED).choice(128, width, replace=False)))
+                scale = None
+                if bits is not None:
+                    scale = verifier._tensor_scale(verifier.dim_sketch(keys, dims), bits)
+                kwargs["key_sketch"] = verifier.sketch_keys(keys, dims, bits=bits, scale=scale)
+                kwargs["sketch_scale"] = scale
+            ms_all, metric_rows, recalls = [], [], []
+            for t in range(1, steps + 1):
+                cur = start + t
+                if path is None:
+                    out, ms = timed(lambda: approx.approx_step(state, queries[t], w, keys[:, :cur], policy=policy,
+                                                               step=t, wave=wave))
+                    ms_all.append(ms)
+                    truth = decode.indexer_topk(queries[t], w, keys[:, :cur].contiguous(), k)
+                    for b in range(C3_BATCH):
+                        recalls.append(np.intersect1d(out.topk[b].cpu().numpy(), truth[b].cpu().numpy()).size / k)
+                    continue
+                if path == "head":
+                    kwargs["head_ids"] = verifier_scoring.dynamic_head_indices(w, width, "high_weight")
+                else:
+                    kwargs["query_sketch"] = verifier.sketch_queries(queries[t], dims, bits=bits, scale=scale)
+                out, ms = timed(lambda: verifier.verifier_step(state, queries[t], w, keys[:, :cur], policy=policy,
+                                                               config=cfg, step=t, wave=wave, **kwargs))
+                ms_all.append(ms)
+                for b in range(C3_BATCH):
+                    metric_rows.append(verifier.verifier_metrics(out, dense_rows[t], config=cfg, policy=policy,
+                                                                 step=t, row=b))
+            key = f"{name}@gamma{gamma_sigma}"
+            if path is None:
+                summary[key] = {"us_per_step": time_stats(ms_all)["median_us"],
+                                "recall_mean": round(float(np.mean(recalls)), 5)}
+                continue
+            col = lambda f: np.asarray([r[f] for r in metric_rows], dtype=np.float64)  # noqa: E731
+            summary[key] = {
+                "us_per_step": time_stats(ms_all)["median_us"],
+                "recall_mean": round(float(col("recall").mean()), 5),
+                "exact_match": round(float(col("exact_match").mean()), 4),
+                "net_qk_reduction_median": round(float(np.median(col("net_qk_reduction"))), 4),
+                "ideal_key_byte_reduction_median": round(float(np.median(col("ideal_key_byte_reduction"))), 4),
+                "physical_b64_key_byte_reduction_median": round(
+                    float(np.median(col("physical_b64_key_byte_reduction"))), 4),
+                "cold_tokens_scanned_median": float(np.median(col("cold_tokens_scanned"))),
+                "rescue_blocks_median": float(np.median(col("rescue_blocks"))),
+                "newly_active_block_recall": round(float(col("newly_active_block_recall").mean()), 4),
+            }
+            rows.extend({"verifier": name, "gamma_sigma": gamma_sigma, **r} for r in metric_rows)
+    dense_us = time_stats(dense_ms)["median_us"]
+    head = summary[f"{VERIFIER_CONFIGS[0][0]}@gamma{VERIFIER_HEADLINE_GAMMA}"]
+    line = {
+        "metric": "two-path verifier decode step: us per step (B=4, L=16K+, K=2048, block 64) and Recall@K vs dense",
+        "value": head["us_per_step"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 0,
+        "ms_per_step": round(head["us_per_step"] / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"C3 shape: B={C3_BATCH}, L={start}+t, K={k}, block {block}, dynamic previous-max "
+                   f"own-trajectory policy, gamma {VERIFIER_GAMMA_SIGMA} sigma (headline {VERIFIER_HEADLINE_GAMMA}), "
+                   f"threshold refresh every {wave} blocks, {steps} decode steps",
+                   "verifiers": [c[0] for c in VERIFIER_CONFIGS]},
+        "dense_step_us": dense_us,
+        "verifiers": summary,
+        "timing": f"HIP events around each eager step, 512 MiB {args.flush} flush before each, median over the steps",
+    }
+    write_table(args, line, rows)
     print(json.dumps(line), flush=True)
 
 

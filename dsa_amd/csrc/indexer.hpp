@@ -115,7 +115,8 @@ __device__ __forceinline__ void load_dense_head_tiles(const uint16_t* q, const f
 }
 
 // Loads the A fragments of M head tiles.  Row slot s of the stacked tiles is
-// head ids[s] (or head s when ids == nullptr) for s < count, else a zero row.
+// head ids[s] (or head s when ids == nullptr) for s < count, else a zero row;
+// an id outside [0, 64) also gives a zero row (and weight 0).
 template <int M, bool kNaturalK>
 __device__ __forceinline__ void load_head_tiles(const uint16_t* q, const float* w,
                                                 const int32_t* ids, int count, int r, int g,
@@ -123,7 +124,8 @@ __device__ __forceinline__ void load_head_tiles(const uint16_t* q, const float* 
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     const int slot = 16 * m + r;
-    const int head = slot < count ? (ids ? ids[slot] : slot) : -1;
+    int head = slot < count ? (ids ? ids[slot] : slot) : -1;
+    head = head < kHeads ? head : -1;  // an id outside [0, 64) is a zero row
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       qa[m][j] = head >= 0 ? *reinterpret_cast<const uint4*>(q + head * kHeadDim + kstep_dims<kNaturalK>(g, j))
@@ -131,7 +133,8 @@ __device__ __forceinline__ void load_head_tiles(const uint16_t* q, const float* 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ws = 16 * m + 4 * g + i;
-      const int wh = ws < count ? (ids ? ids[ws] : ws) : -1;
+      int wh = ws < count ? (ids ? ids[ws] : ws) : -1;
+      wh = wh < kHeads ? wh : -1;
       wr[m][i] = wh >= 0 ? w[wh] : 0.f;
     }
   }

@@ -257,9 +257,6 @@ def test_verifier_step_rejects_bad_inputs(device) -> None:
     pol = approx.ApproxPolicy("s")
     with pytest.raises(ValueError, match="head_ids"):
         verifier.verifier_step(state, q, w, keys, policy=pol, config=cfg, step=1)
-    with pytest.raises(ValueError, match="out of range"):
-        verifier.verifier_step(state, q, w, keys, policy=pol, config=cfg, step=1,
-                               head_ids=torch.full((8,), 64, device=device))
     with pytest.raises(ValueError, match="block_size"):
         verifier.verifier_step(state, q, w, keys, policy=pol, step=1, head_ids=torch.arange(8, device=device),
                                config=verifier.VerifierConfig(name="h", path="head", width=8, score_ratio=0.1,
