@@ -281,6 +281,174 @@ __global__ __launch_bounds__(1024) void temporal_refresh_kernel(TemporalArgs a) 
   if (tid == 0) a.ws.tau[row] = prefix;
 }
 
+// The dynamic scan of one row in one workgroup: for each wave of W scan
+// positions, every block of the wave is pruned or kept against the threshold
+// in force at the wave's start (one block per wave of threads), kept blocks
+// are scored, and the wave's new (non-seed) scores join the running k largest
+// in LDS; a radix select then names the k-th largest, the next threshold.
+// The running k largest never leave LDS and the row needs no relaunch between
+// waves.  Every loop bound is uniform over the workgroup.
+constexpr int kScanThreads = 512;
+constexpr int kScanWaves = kScanThreads / kWave;
+constexpr int kMaxRun = 4096;  // k
+constexpr int kScanTiles = 6;  // 16-key tiles in flight per wave
+constexpr int kMaxTemporalLength = 32768;
+// Above this many waves of scan positions a step runs the persistent
+// per-row scan: one launch per wave costs a launch, a grid drain and a refresh
+// launch (~11 us at C3), against ~4.4 us per wave in LDS but with one CU per
+// row scoring (~130 us for a C3 row's kept keys).
+constexpr int kPersistentScanWaves = 16;
+
+template <class Tag, class KF>
+__global__ __launch_bounds__(kScanThreads) void temporal_scan_kernel(TemporalArgs a, int32_t wave_blocks) {
+  __shared__ uint32_t vals[kMaxMerge];  // [0, k): the running k largest; then the wave's new keys
+  __shared__ uint32_t kept[kMaxRun];    // the next running k largest, before it moves back to vals
+  __shared__ __align__(16) uint32_t digits[kDigitBinsT];
+  __shared__ uint32_t s_fill, s_digit, s_rem, s_above, s_floor, s_kept;
+  __shared__ int klist[kMaxMerge / 16];  // kept blocks of the current wave
+  __shared__ uint32_t order[kMaxTemporalBlocks];        // block at each scan position
+  __shared__ double upper[kMaxTemporalBlocks];          // its bound
+  __shared__ uint32_t seed_mask[kMaxTemporalLength / 32];  // keys scored as seeds
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int row = blockIdx.x;
+  const int k = a.k;
+  const int nb = a.blocks;
+  const int bs = a.block_size;
+  const int tiles_per_block = bs / 16;
+  const int words = (a.length + 31) / 32;
+  float* srow = a.scores + (size_t)row * a.length;
+  // The row's scan order, bounds and seed mask stay in LDS for the whole scan.
+  for (int i = tid; i < nb; i += kScanThreads) {
+    const uint32_t blk = a.ws.order[(size_t)row * nb + i];
+    order[i] = blk;
+    upper[i] = a.ws.upper[(size_t)row * nb + blk];  // the bound of the block at scan position i
+  }
+  for (int i = tid; i < words; i += kScanThreads) seed_mask[i] = a.ws.seed_mask[(size_t)row * words + i];
+  // The query tiles of the row stay in registers for the whole scan.
+  uint4 qa[4][4];
+  float wr[4][4];
+  load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads, r, g,
+                                          qa, wr);
+  const BufferRsrc keys = make_buffer(a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
+                                      (uint32_t)a.length * KF::kRowBytes);
+  if (tid == 0) {
+    s_fill = (uint32_t)k;
+    s_floor = 0xffffffffu;
+  }
+  __syncthreads();
+  uint32_t least = 0xffffffffu;
+  for (int i = tid; i < k; i += kScanThreads) {
+    const uint32_t v = a.ws.run[(size_t)row * k + i];
+    vals[i] = v;
+    least = min(least, v);
+  }
+  for (int off = 32; off > 0; off >>= 1) least = min(least, (uint32_t)__shfl_xor((int)least, off, kWave));
+  if (lane == 0) __hip_atomic_fetch_min(&s_floor, least, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  uint32_t tau = a.ws.tau[row];
+  __syncthreads();
+  // floor: the k-th largest of the running set (its minimum).  A new key at or
+  // below it cannot change the k largest, so only keys above it are merged.
+  uint32_t floor_key = s_floor;
+  for (int start = 0; start < nb; start += wave_blocks) {
+    const int len = min(wave_blocks, nb - start);
+    const double bound = (double)ordered_to_float(tau);
+    // Decisions for the wave's blocks, kept ones listed in LDS.
+    if (tid == 0) s_kept = 0;
+    __syncthreads();
+    for (int p = tid; p < len; p += kScanThreads) {
+      const int blk = (int)order[start + p];
+      const bool keep = !(upper[start + p] < bound);
+      a.evaluated[(size_t)row * nb + blk] = keep ? 1 : 0;
+      if (keep) klist[__hip_atomic_fetch_add(&s_kept, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] = blk;
+    }
+    __syncthreads();
+    // The kept blocks' 16-key tiles, dealt round-robin to the waves, each wave
+    // issuing the loads of all its tiles of a round before using any.
+    const int tiles = (int)s_kept * tiles_per_block;
+    for (int base = 0; base < tiles; base += kScanWaves * kScanTiles) {
+      uint4 buf[kScanTiles][KF::kRaw];
+      int tkey[kScanTiles];
+#pragma unroll
+      for (int i = 0; i < kScanTiles; ++i) {
+        const int j = base + wave + kScanWaves * i;
+        int key0 = -1;
+        if (j < tiles) key0 = klist[j / tiles_per_block] * bs + 16 * (j % tiles_per_block);
+        tkey[i] = key0;
+        KF::load_buf(keys, (key0 >= 0 && key0 < a.length) ? key0 + r : (int)kFarKey, g, buf[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < kScanTiles; ++i) {
+        if (tkey[i] < 0) continue;  // uniform over the wave
+        float v = reduce_lane_groups(tile_contrib<Tag, 4, KF>(qa, wr, buf[i]));
+        const int key = tkey[i] + r;
+        if (g == 0 && key < a.length) {
+          if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
+          srow[key] = v;
+          const uint32_t o = float_to_ordered(v);
+          if (o > floor_key && !((seed_mask[key >> 5] >> (key & 31)) & 1u))
+            vals[__hip_atomic_fetch_add(&s_fill, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] = o;
+        }
+      }
+    }
+    __syncthreads();
+    if (start + wave_blocks >= nb) break;  // no refresh after the last wave
+    if (s_fill == (uint32_t)k) {
+      // nothing above the floor: the k largest are unchanged and the threshold
+      // is their minimum
+      tau = floor_key;
+      continue;
+    }
+    const uint32_t n = s_fill;
+    // Radix select of the k-th largest of vals[0, n): bits 31..21, 20..10, 9..0.
+    uint32_t prefix = 0;
+    uint32_t mask = 0;
+    uint32_t want = (uint32_t)k;
+#pragma unroll 1
+    for (int pass = 0; pass < 3; ++pass) {
+      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+      const uint32_t dmask = pass < 2 ? 0x7ffu : 0x3ffu;
+      for (int i = tid; i < kDigitBinsT; i += kScanThreads) digits[i] = 0;
+      __syncthreads();
+      for (uint32_t i = tid; i < n; i += kScanThreads) {
+        const uint32_t v = vals[i];
+        if ((v & mask) == prefix)
+          __hip_atomic_fetch_add(&digits[(v >> shift) & dmask], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const Locate loc = wave_locate<kDigitBinsT / kWave>(digits, want, false);
+        if (lane == 0) {
+          s_digit = loc.digit;
+          s_rem = loc.rem;
+        }
+      }
+      if (tid == 0) s_above = 0;
+      __syncthreads();
+      prefix |= s_digit << shift;
+      mask |= dmask << shift;
+      want = s_rem;
+    }
+    // prefix is the k-th largest; `want` of its copies belong to the k largest.
+    const uint32_t above = (uint32_t)k - want;
+    for (uint32_t i = tid; i < n; i += kScanThreads) {
+      const uint32_t v = vals[i];
+      if (v > prefix) kept[__hip_atomic_fetch_add(&s_above, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] = v;
+    }
+    for (uint32_t j = tid; j < want; j += kScanThreads) kept[above + j] = prefix;
+    __syncthreads();
+    for (int i = tid; i < k; i += kScanThreads) vals[i] = kept[i];
+    if (tid == 0) s_fill = (uint32_t)k;
+    tau = prefix;
+    floor_key = prefix;
+    __syncthreads();
+  }
+  if (tid == 0) a.ws.tau[row] = tau;
+}
+
 // After the scan: the 4096-bin histogram (top 12 bits of the ordered key)
 // of the step's scores for the select kernels, keys never scored (-inf)
 // included in their own bin so that the row's count is its length, and the
@@ -422,6 +590,14 @@ int launch_scan(TemporalArgs& a, int32_t wave, hipStream_t stream) {
   hipLaunchKernelGGL((temporal_seed_kernel<Tag, KF>), dim3(a.rows * ((a.k + 255) / 256)), dim3(256), 0, stream, a);
   if (int st = check_launch("temporal_seed_kernel")) return st;
   const int step = wave > 0 ? wave : a.blocks;
+  const int waves = (a.blocks + step - 1) / step;
+  if (wave > 0 && waves > kPersistentScanWaves) {
+    // many refreshes: the whole scan of a row in one workgroup, no relaunch per wave
+    hipLaunchKernelGGL((temporal_scan_kernel<Tag, KF>), dim3(a.rows), dim3(kScanThreads), 0, stream, a, wave);
+    return check_launch("temporal_scan_kernel");
+  }
+  // few refreshes (or none): each wave of scan positions is scored by the
+  // whole grid, and a refresh launch merges the running k largest after it
   for (int start = 0; start < a.blocks; start += step) {
     a.wave_start = start;
     a.wave_len = min(step, a.blocks - start);
@@ -480,11 +656,11 @@ int check_step(const void* queries, const void* keys, int64_t key_stride, const 
   DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(block_size == 16 || block_size == 32 || block_size == 64 || block_size == 128,
               "block_size %d not in {16, 32, 64, 128}", block_size);
-  DSA_REQUIRE(length > 0 && length <= 32768, "length %lld outside [1, 32768]", (long long)length);
+  DSA_REQUIRE(length > 0 && length <= kMaxTemporalLength, "length %lld outside [1, 32768]", (long long)length);
   DSA_REQUIRE(key_stride >= length, "key_stride < length");
   DSA_REQUIRE(prev_length > 0 && prev_length <= length, "prev_length %lld outside [1, length]",
               (long long)prev_length);
-  DSA_REQUIRE(k > 0 && k <= 4096 && k <= prev_length, "k=%lld must be in [1, min(4096, prev_length)]",
+  DSA_REQUIRE(k > 0 && k <= kMaxRun && k <= prev_length, "k=%lld must be in [1, min(4096, prev_length)]",
               (long long)k);
   DSA_REQUIRE(wave >= 0, "wave must be >= 0");
   DSA_REQUIRE(k + int64_t(wave) * block_size <= kMaxMerge, "k + wave * block_size exceeds %d", kMaxMerge);
