@@ -95,8 +95,8 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     } else {
       const bool fresh = grown && b >= first_new;
       const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
-      upper = fresh ? HUGE_VAL : (double)pm + (double)a.gamma[row];
-      rank_value = upper;
+      upper = fresh ? HUGE_VAL : (double)pm + (a.gamma_d ? a.gamma_d[row] : (double)a.gamma[row]);
+      rank_value = a.scan_order == 3 ? (double)a.order_key[(size_t)row * nb + b] : upper;
       group = hot_first && !hot[b] ? 0x80000000u : 0u;
     }
     a.ws.upper[(size_t)row * nb + b] = upper;
@@ -104,7 +104,10 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     l[j] = group | (uint32_t)b;
   }
   if (!sorted) {
-    for (int b = tid; b < nb; b += 1024) a.ws.order[(size_t)row * nb + b] = b;
+    for (int b = tid; b < nb; b += 1024) {
+      a.ws.order[(size_t)row * nb + b] = b;
+      if (a.order_out) a.order_out[(size_t)row * nb + b] = b;
+    }
     return;
   }
   int n = 2;
@@ -126,7 +129,10 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j)
-    if (2 * tid + j < nb) a.ws.order[(size_t)row * nb + 2 * tid + j] = l[j] & 0x7fffffffu;
+    if (2 * tid + j < nb) {
+      a.ws.order[(size_t)row * nb + 2 * tid + j] = l[j] & 0x7fffffffu;
+      if (a.order_out) a.order_out[(size_t)row * nb + 2 * tid + j] = (int32_t)(l[j] & 0x7fffffffu);
+    }
 }
 
 
@@ -149,15 +155,22 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
     const int64_t key = i < a.k ? seeds[i] : -1;
     tile_key[t] = (key >= 0 && key < a.length) ? (int)key : (int)kFarKey;
   }
-  float v = score_unit<Tag, KF>(a, row, tile_key, r, g);
   const int i = base + lane;
+  float v;
+  if (a.source) {  // recorded scores: lane l reads its own seed's
+    const int64_t key = i < a.k ? seeds[i] : -1;
+    v = (key >= 0 && key < a.length) ? a.source[(size_t)row * a.source_stride + key] : 0.f;
+  } else {
+    v = score_unit<Tag, KF>(a, row, tile_key, r, g);
+  }
   uint32_t least = 0xffffffffu;  // this lane's seed key (none: neutral for the min)
   if (i < a.k) {
     const int64_t key = seeds[i];
     if (key < 0 || key >= a.length) {
       a.ws.run[(size_t)row * a.k + i] = 0;  // below every score
     } else {
-      if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
+      if constexpr (KF::kScaled)
+        if (!a.source) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
       a.scores[(size_t)row * a.length + key] = v;
       const int words = (a.length + 31) / 32;
       __hip_atomic_fetch_or(a.ws.seed_mask + (size_t)row * words + (key >> 5), 1u << (key & 31),
@@ -199,10 +212,15 @@ __global__ __launch_bounds__(256) void temporal_block_kernel(TemporalArgs a) {
       const int tile = u * 64 + 16 * t;  // blocks are whole 16-key tiles
       tile_key[t] = (tile >= first && tile < first + a.block_size) ? tile + r : (int)kFarKey;
     }
-    float v = score_unit<Tag, KF>(a, row, tile_key, r, g);
     const int key = u * 64 + lane;
+    float v;
+    if (a.source)  // recorded scores: lane l reads key u * 64 + l
+      v = (key >= first && key < end) ? a.source[(size_t)row * a.source_stride + key] : 0.f;
+    else
+      v = score_unit<Tag, KF>(a, row, tile_key, r, g);
     if (key >= first && key < end) {
-      if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
+      if constexpr (KF::kScaled)
+        if (!a.source) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
       a.scores[(size_t)row * a.length + key] = v;
     }
   }
@@ -329,12 +347,14 @@ __global__ __launch_bounds__(kScanThreads) void temporal_scan_kernel(TemporalArg
   }
   for (int i = tid; i < words; i += kScanThreads) seed_mask[i] = a.ws.seed_mask[(size_t)row * words + i];
   // The query tiles of the row stay in registers for the whole scan.
-  uint4 qa[4][4];
-  float wr[4][4];
-  load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads, r, g,
-                                          qa, wr);
-  const BufferRsrc keys = make_buffer(a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
-                                      (uint32_t)a.length * KF::kRowBytes);
+  uint4 qa[4][4] = {};
+  float wr[4][4] = {};
+  if (!a.source)
+    load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads, r, g,
+                                            qa, wr);
+  // recorded scores: an empty key buffer (every load reads 0 without touching memory)
+  const BufferRsrc keys = make_buffer(a.source ? nullptr : a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
+                                      a.source ? 0u : (uint32_t)a.length * KF::kRowBytes);
   if (tid == 0) {
     s_fill = (uint32_t)k;
     s_floor = 0xffffffffu;
@@ -383,10 +403,12 @@ __global__ __launch_bounds__(kScanThreads) void temporal_scan_kernel(TemporalArg
 #pragma unroll
       for (int i = 0; i < kScanTiles; ++i) {
         if (tkey[i] < 0) continue;  // uniform over the wave
-        float v = reduce_lane_groups(tile_contrib<Tag, 4, KF>(qa, wr, buf[i]));
         const int key = tkey[i] + r;
+        float v = a.source ? (key < a.length ? a.source[(size_t)row * a.source_stride + key] : 0.f)
+                           : reduce_lane_groups(tile_contrib<Tag, 4, KF>(qa, wr, buf[i]));
         if (g == 0 && key < a.length) {
-          if constexpr (KF::kScaled) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
+          if constexpr (KF::kScaled)
+            if (!a.source) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
           srow[key] = v;
           const uint32_t o = float_to_ordered(v);
           if (o > floor_key && !((seed_mask[key >> 5] >> (key & 31)) & 1u))
@@ -725,6 +747,50 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
   a.scan_order = scan_order;
   a.ws = ws;
   return run_step(a, wave, key_dtype, out_topk, stream);
+}
+
+extern "C" int dsa_temporal_replay_step(const float* current_scores, int64_t score_stride,
+                                        const float* prev_block_max, int64_t prev_length, const int64_t* prev_topk,
+                                        const double* gamma, const float* order_key, float* scores,
+                                        uint8_t* evaluated_blocks,
+                                        int32_t* scan_order_out, int64_t* out_topk, int32_t* qk_scored, int64_t batch,
+                                        int64_t length, int64_t k, int32_t block_size, int32_t scan_order,
+                                        int32_t wave, void* workspace, int64_t workspace_bytes, void* stream) {
+  DSA_REQUIRE(current_scores && prev_block_max && prev_topk && gamma && scores && evaluated_blocks && out_topk &&
+                  qk_scored,
+              "null pointer argument");
+  DSA_REQUIRE(score_stride == 0 || score_stride >= length, "score_stride must be 0 or >= length");
+  if (int st = check_step(nullptr, nullptr, length, nullptr, prev_length, batch, length, k, block_size, wave,
+                          DSA_DTYPE_BF16, workspace))
+    return st;
+  DSA_REQUIRE(scan_order >= 0 && scan_order <= 3, "scan_order %d not in {0, 1, 2, 3}", scan_order);
+  DSA_REQUIRE(scan_order != 3 || order_key, "scan order 3 needs order_key");
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the replay step needs %lld workspace bytes", (long long)ws.bytes);
+  TemporalArgs a = {};
+  a.source = current_scores;
+  a.source_stride = score_stride;
+  a.order_out = scan_order_out;
+  a.order_key = order_key;
+  a.key_stride = length;
+  a.prev_max = prev_block_max;
+  a.seeds = prev_topk;
+  a.gamma_d = gamma;
+  a.scores = scores;
+  a.evaluated = evaluated_blocks;
+  a.qk_scored = qk_scored;
+  a.rows = (int32_t)batch;
+  a.length = (int32_t)length;
+  a.k = (int32_t)k;
+  a.block_size = block_size;
+  a.blocks = (int32_t)blocks;
+  a.prev_length = (int32_t)prev_length;
+  a.prev_blocks = (int32_t)((prev_length + block_size - 1) / block_size);
+  a.scan_order = scan_order;
+  a.ws = ws;
+  return run_step(a, wave, DSA_DTYPE_BF16, out_topk, stream);
 }
 
 extern "C" int dsa_approx_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,

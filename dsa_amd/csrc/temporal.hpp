@@ -71,11 +71,16 @@ struct TemporalArgs {
   const float* prev_max;  // [rows][prev_blocks]
   const int64_t* seeds;   // [rows][k]
   const float* gamma;     // [rows]
+  const double* gamma_d;  // [rows] or null: a float64 margin (replay over recorded scores)
+  const float* source;    // [rows][source_stride] or null: recorded scores read instead of scoring keys
+  int64_t source_stride;
+  int32_t* order_out;     // [rows][blocks] or null: the scan order, for the caller
+  const float* order_key; // [rows][blocks]: the sort key of scan order 3 (larger first, then address)
   float* scores;          // [rows][length]
   uint8_t* evaluated;     // [rows][blocks]
   int32_t* qk_scored;     // [rows]
   int32_t rows, length, k, block_size, blocks, prev_length, prev_blocks;
-  int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper
+  int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper, 3 order_key
   int32_t wave_start, wave_len;
   int32_t policy_mode;    // 0: bound prev_max + gamma (replay filter); 1: own-trajectory policy
   ApproxDev ap;

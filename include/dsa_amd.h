@@ -364,6 +364,25 @@ int dsa_approx_init_state(const float* scores, int64_t score_stride, const int64
                           int64_t state_stride, int64_t batch, int64_t length, int64_t k, int32_t block_size,
                           void* stream);
 
+/* The filter of dsa_temporal_step replayed over recorded scores
+ * (replay.py:172-222 run_filter inside replay_transition :225-400): the
+ * scores of row r are read from current_scores [batch][score_stride] instead
+ * of being computed from keys (score_stride 0: every row reads the same
+ * scores), gamma is float64 per sequence (the reference's gamma_sigma *
+ * sigma), and scan_order_out [batch][blocks] (nullable) receives the scan
+ * order.  scan_order 3 visits blocks by larger order_key [batch][blocks]
+ * (fp32), then lower address: the reference's "oracle_current" order with the
+ * current block maxima as the key.  Its "oracle" method is that order with
+ * the current maxima also as prev_block_max, gamma 0 and
+ * prev_length = length.  Other arguments, outputs and limits as
+ * dsa_temporal_step. */
+int dsa_temporal_replay_step(const float* current_scores, int64_t score_stride, const float* prev_block_max,
+                             int64_t prev_length, const int64_t* prev_topk, const double* gamma,
+                             const float* order_key, float* scores, uint8_t* evaluated_blocks,
+                             int32_t* scan_order_out, int64_t* out_topk, int32_t* qk_scored, int64_t batch,
+                             int64_t length, int64_t k, int32_t block_size, int32_t scan_order, int32_t wave,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Two-path verifier step (verifier.py:173-392 verifier_step with
  * apply_rescue_to_state :103-170; the reference replays it offline over
