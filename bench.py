@@ -45,12 +45,13 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--config", choices=("c2", "c3", "c4", "c5", "progressive", "sidecar", "verifier"), default="c2",
+    parser.add_argument("--config", choices=("c2", "c3", "c4", "c5", "progressive", "sidecar", "verifier", "replay"), default="c2",
                         help="c2: the headline decode step (default); c3: temporal replay over 256 decode steps; "
                         "c4: causal prefill indexer + top-512; c5: fp8 long-context decode; "
                         "progressive: the reference's method comparison (full / H8 / two-pass / fused); "
                         "sidecar: the indexer's query/key encoders at the decode and prefill shapes; "
-                        "verifier: the live two-path verifier step against the dense step (C3 shape)")
+                        "verifier: the live two-path verifier step against the dense step (C3 shape); "
+                        "replay: the reference's trace replay sweep over a GPU-collected C3-shape trace")
     parser.add_argument("--out", default=None, help="c4/c5/progressive: also write the full table (JSON) here")
     parser.add_argument("--flush", choices=("read", "write"), default="read",
                         help="c4/c5/progressive: cache flush before each timed replay: read 512 MiB (default) or "
@@ -122,9 +123,9 @@ def main() -> None:
     if args.config == "c3":
         run_c3(args)
         return
-    if args.config in ("c4", "c5", "progressive", "sidecar", "verifier"):
+    if args.config in ("c4", "c5", "progressive", "sidecar", "verifier", "replay"):
         {"c4": run_c4, "c5": run_c5, "progressive": run_progressive, "sidecar": run_sidecar,
-         "verifier": run_verifier}[args.config](args)
+         "verifier": run_verifier, "replay": run_replay}[args.config](args)
         return
     import torch
 
@@ -1305,6 +1306,96 @@ def run_verifier(args) -> None:
     }
     write_table(args, line, rows)
     print(json.dumps(line), flush=True)
+
+
+
+# --------------------------------------------------------------------------
+# Trace replay (the reference's analysis sweep) on a GPU-collected trace
+# --------------------------------------------------------------------------
+REPLAY_STEPS = 9
+REPLAY_K = (2048,)
+REPLAY_GAMMAS = (0.0, 0.25, 0.5, 1.0)
+
+
+def run_replay(args) -> None:
+    """The reference's replay_trace sweep (replay.py:476-627; configs/pilot.yaml:
+    K=2048, blocks 16/32/64/128, gamma_sigma 0/0.25/0.5/1, every method and
+    order, threshold refreshed after every block as the reference does) over a
+    dense score trace of one sequence collected on the GPU (C3 shape: 16384
+    keys + one per step, AR(1) queries rho=0.95, N(0,1) bf16 keys).  Reports
+    transitions per second of the GPU replay (every filter in the HIP temporal
+    kernels) and of the CPU restatement of the reference's replay on a
+    bounded sample of the same transitions."""
+
+    import numpy as np
+    import torch
+
+    from dsa_amd import _lib, replay
+    from dsa_amd.trace import collect_trace
+
+    _lib.load()
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    gen = torch.Generator().manual_seed(SEED)
+    steps = REPLAY_STEPS
+    keys = torch.randn(C3_LENGTH + steps - 1, 128, generator=gen).to(torch.bfloat16).to(device)
+    w = (torch.randn(64, generator=gen) / 8.0).to(device)
+    q = torch.randn(64, 128, generator=gen) / math.sqrt(128)
+    qs = []
+    for _ in range(steps):
+        qs.append(q.to(torch.bfloat16))
+        q = C3_RHO * q + math.sqrt(1 - C3_RHO * C3_RHO) * torch.randn(64, 128, generator=gen) / math.sqrt(128)
+    trace = collect_trace(torch.stack(qs).to(device), w, keys, np.arange(C3_LENGTH, C3_LENGTH + steps))
+    kwargs = dict(k_values=list(REPLAY_K), block_sizes=list(C3_BLOCKS), gamma_sigma_values=list(REPLAY_GAMMAS))
+    # warm the workspaces and kernels on the first transition
+    first = type(trace)(trace.scores[:2], trace.lengths[:2], 0, "synthetic", "0", {})
+    replay.replay_trace_rows(first, **kwargs)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rows = replay.replay_trace_rows(trace, **kwargs)
+    torch.cuda.synchronize()
+    gpu_s = time.perf_counter() - t0
+    transitions = steps - 1
+    per_transition = len(rows) // transitions
+    summary = replay.aggregate_rows(__import__("pandas").DataFrame(rows))
+    best = summary[summary.recall >= 0.999].sort_values("net_byte_reduction", ascending=False).head(1).to_dict("records")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import os
+
+        from oracle import replay as R
+
+        rows_h = [trace.row(0), trace.row(1)]
+        c0 = time.perf_counter()
+        sample_rows = R.replay_trace_rows(rows_h, **kwargs)
+        cpu_s = time.perf_counter() - c0
+        cpu = {"value": round(len(sample_rows) / cpu_s, 2), "unit": "replay rows/s", "cores": 1, "kind": "port",
+               "sample": f"the {len(sample_rows)} rows of the trace's first transition (the same sweep) in "
+                         f"{cpu_s:.1f} s on 1 of {os.cpu_count()} host threads (oracle/replay.py, the reference's "
+                         "replay restated)"}
+    line = {
+        "metric": "trace replay: replay rows per second (the reference's replay_trace sweep, C3-shape trace)",
+        "value": round(len(rows) / gpu_s, 2),
+        "unit": "replay rows/s",
+        "n_gpus": 1,
+        "steps": transitions,
+        "warmup": 1,
+        "ms_per_step": round(gpu_s / transitions * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": f"replay_trace over a GPU-collected trace: L {C3_LENGTH}+t, {transitions} transitions, "
+                   f"K {list(REPLAY_K)}, blocks {list(C3_BLOCKS)}, gamma_sigma {list(REPLAY_GAMMAS)}, "
+                   f"{per_transition} rows per transition, wave 1"},
+        "gpu_seconds": round(gpu_s, 3),
+        "rows": len(rows),
+        "best_at_recall_0.999": best[0] if best else None,
+        "cpu_baseline": cpu,
+    }
+    write_table(args, line, rows)
+    print(json.dumps(line, default=float), flush=True)
 
 
 if __name__ == "__main__":
