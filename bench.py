@@ -234,6 +234,21 @@ def main() -> None:
     traffic_file = ROOT / "profiles" / "dense_scores_c2_traffic.json"
     if traffic_file.exists():
         traffic = json.loads(traffic_file.read_text()).get("traffic_bytes")
+    # Measured streaming ceiling: a read-only launch with the scoring kernel's
+    # grid and load pattern over the same key sets, timed like the scoring
+    # kernel (events the kernel records at its own start and end).
+    sink = torch.empty(256, device=device, dtype=torch.float32)
+    key_bytes = keys_per_step * 256
+    smarks = [torch.cuda.Event(enable_timing=True) for _ in range(2 * timed)]
+    for m in smarks:
+        m.record(stream)
+    torch.cuda.synchronize()
+    for i in range(timed):
+        _lib.call("dsa_stream_read", key_sets[i % ROTATIONS].data_ptr(), key_bytes, 256, sink.data_ptr(),
+                  stream.cuda_stream, smarks[2 * i].cuda_event, smarks[2 * i + 1].cuda_event)
+    torch.cuda.synchronize()
+    stream_us = sum(smarks[2 * i].elapsed_time(smarks[2 * i + 1]) for i in range(timed)) * 1e3 / timed
+    stream_gbs = key_bytes / (stream_us * 1e-6) / 1e9
     # Whole-step algorithmic bytes (keys + q + w + K index/score outputs).
     step_bytes = keys_per_step * 256 + BATCH * (64 * 128 * 2 + 64 * 4) + BATCH * TOPK * (4 + 4)
 
@@ -276,6 +291,10 @@ def main() -> None:
             "kernel": "dense_scores_kernel<bf16, M=4, hist, lists>",
             "kernel_avg_us": round(score_avg_ms * 1e3, 3),
             "algorithmic_bytes": score_bytes,
+            "measured_peak": round(stream_gbs, 1),
+            "frac_of_measured": round(achieved / stream_gbs, 4),
+            "measured_peak_kernel": f"dsa_stream_read: the same {key_bytes} key bytes, grid and load pattern, "
+            f"read only ({stream_us:.2f} us per launch)",
         },
         "step": {
             "score_us": round(score_avg_ms * 1e3, 3),

@@ -523,6 +523,19 @@ int dsa_encode_queries_epilogue(const void* proj, const float* proj_weights, con
                                 float* out_weights, int64_t tokens, int32_t heads, int32_t dim,
                                 int32_t dtype, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement utility (no counterpart in the reference; it serves the
+ * roofline's measured peak): one launch that only reads `bytes` of device
+ * memory with the decode scoring kernel's grid shape and load pattern
+ * (`workgroups` workgroups of 4 waves, 64-key units of 256-byte rows, two
+ * units in flight per wave).  bytes must split into whole 16 KiB units per
+ * workgroup; sink is 256 floats that are practically never written.  When
+ * start_event / stop_event (hipEvent_t, nullable) are given the kernel records
+ * them at its own start and end, like the *_timed entry points.
+ * ------------------------------------------------------------------------ */
+int dsa_stream_read(const void* data, int64_t bytes, int32_t workgroups, float* sink, void* stream,
+                    void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif
