@@ -261,6 +261,8 @@ struct VerifierArgs {
   int32_t promotion;       // 0: global budget, 1: fixed threshold
   double fraction;
   float threshold;
+  const float* vsource;    // [rows][vsource_stride] or null: recorded verifier scores (trace replay)
+  int64_t vsource_stride;
 };
 
 // Cold keys of a block: count, and whether key `key` is cold.
@@ -374,6 +376,35 @@ __global__ __launch_bounds__(256) void verifier_dim_scan_kernel(TemporalArgs a, 
   }
 }
 
+// Recorded verifier scores (trace replay): one wave per block takes the
+// cold keys' scores from the recorded row instead of scoring them.
+__global__ __launch_bounds__(256) void verifier_source_scan_kernel(TemporalArgs a, VerifierArgs v) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int per_row = (a.blocks + 3) / 4;
+  const int row = blockIdx.x / per_row;
+  const int blk = (blockIdx.x % per_row) * 4 + wave;
+  if (blk >= a.blocks) return;
+  const int first = blk * a.block_size;
+  const int end = min(a.length, first + a.block_size);
+  const float* srow = a.scores + (size_t)row * a.length;
+  const float* vrow = v.vsource + (size_t)row * v.vsource_stride;
+  int cold = 0;
+  float best = -__builtin_inff();
+  for (int key = first + lane; key - lane < end; key += 64) {
+    const bool c = is_cold(srow, key, end);
+    cold += __popcll(__ballot(c));
+    const float s = c ? vrow[key] : -__builtin_inff();
+    best = fmaxf(best, s);
+    if (key < end && v.verifier_scores) v.verifier_scores[(size_t)row * a.length + key] = s;
+  }
+  best = wave_max(best);
+  if (lane == 0) {
+    v.block_scores[(size_t)row * a.blocks + blk] = cold ? best : -__builtin_inff();
+    v.cold_count[(size_t)row * a.blocks + blk] = (uint8_t)cold;
+  }
+}
+
 // Rescue ranking, one 1024-thread workgroup per row (blocks <= kSortN).
 // Sort entries: cold blocks first (group bit), larger verifier block score,
 // lower block id.
@@ -459,10 +490,15 @@ __global__ __launch_bounds__(256) void verifier_rescue_kernel(TemporalArgs a, Ve
       const int tile = u * 64 + 16 * t;  // blocks are whole 16-key tiles
       tile_key[t] = (tile >= first && tile < first + a.block_size) ? tile + r : (int)kFarKey;
     }
-    float s = score_unit<Tag, KF>(a, row, tile_key, r, g);
     const int key = u * 64 + lane;
+    float s;
+    if (a.source)  // trace replay: the recorded score
+      s = (key >= first && key < end) ? a.source[(size_t)row * a.source_stride + key] : 0.f;
+    else
+      s = score_unit<Tag, KF>(a, row, tile_key, r, g);
     if (key >= first && key < end && srow[key] == -__builtin_inff()) {
-      if constexpr (KF::kScaled) s *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
+      if constexpr (KF::kScaled)
+        if (!a.source) s *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
       srow[key] = s;
     }
   }
@@ -484,7 +520,10 @@ int launch_verifier(TemporalArgs& a, VerifierArgs& v, int32_t path, int32_t wave
                     int64_t* out_topk, hipStream_t stream) {
   if (int st = temporal_scan(a, wave, key_dtype, stream)) return st;
   const dim3 grid((unsigned)(a.rows * ((a.blocks + 3) / 4)));
-  if (path == DSA_VERIFIER_HEAD) {
+  if (v.vsource) {
+    hipLaunchKernelGGL(verifier_source_scan_kernel, grid, dim3(256), 0, stream, a, v);
+    if (int st = check_launch("verifier_source_scan_kernel")) return st;
+  } else if (path == DSA_VERIFIER_HEAD) {
     if (int st = launch_head_scan<Tag, KF>(a, v, grid, stream)) return st;
   } else {
     switch ((v.width + 31) / 32) {
@@ -708,4 +747,72 @@ extern "C" int dsa_verifier_step(const void* queries, const float* weights, cons
     case DSA_DTYPE_F16: return launch_verifier<F16Tag, KeysB16>(a, v, spec->path, wave, key_dtype, out_topk, s);
     default: return launch_verifier<Bf16Tag, KeysFP8>(a, v, spec->path, wave, key_dtype, out_topk, s);
   }
+}
+
+extern "C" int dsa_verifier_replay_step(const float* current_scores, int64_t score_stride,
+                                        const float* recorded_verifier_scores, int64_t verifier_stride,
+                                        const dsa_approx_policy* policy, const double* gamma_rows,
+                                        int64_t prev_length, const int64_t* prev_topk, float* last_max, float* ema,
+                                        float* volatility, int16_t* age, int16_t* cold_streak, int64_t state_stride,
+                                        const dsa_verifier_spec* spec, float* scores, float* verifier_scores,
+                                        float* block_scores, uint8_t* cold_count, uint8_t* evaluated_blocks,
+                                        uint8_t* rescued_blocks, int32_t* ranking, int64_t* out_topk,
+                                        int32_t* qk_scored, int32_t* counts, int64_t batch, int64_t length,
+                                        int64_t k, int32_t block_size, int32_t wave, void* workspace,
+                                        int64_t workspace_bytes, void* stream) {
+  DSA_REQUIRE(current_scores && recorded_verifier_scores && policy && spec && prev_topk && last_max && ema &&
+                  volatility && age && cold_streak && scores && block_scores && cold_count && evaluated_blocks &&
+                  rescued_blocks && out_topk && qk_scored && counts,
+              "null pointer argument");
+  DSA_REQUIRE(score_stride >= length && verifier_stride >= length, "score rows shorter than length");
+  if (int st = check_step(nullptr, nullptr, length, nullptr, prev_length, batch, length, k, block_size, wave,
+                          DSA_DTYPE_BF16, workspace))
+    return st;
+  DSA_REQUIRE(policy->risk_model == DSA_RISK_LAST_MAX || policy->risk_model == DSA_RISK_EMA,
+              "risk_model %d unknown", policy->risk_model);
+  DSA_REQUIRE(policy->order >= DSA_ORDER_ADDRESS && policy->order <= DSA_ORDER_BUCKET, "order %d unknown",
+              policy->order);
+  DSA_REQUIRE(policy->order != DSA_ORDER_BUCKET || policy->buckets >= 1, "bucket order needs buckets >= 1");
+  DSA_REQUIRE(policy->recent_window >= 0, "recent_window must be >= 0");
+  DSA_REQUIRE(spec->promotion == 0 || spec->promotion == 1, "promotion %d unknown", spec->promotion);
+  DSA_REQUIRE(spec->rescue_fraction >= 0.0 && spec->rescue_fraction <= 1.0, "rescue_fraction outside [0, 1]");
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  DSA_REQUIRE(state_stride >= blocks, "state_stride %lld < %lld blocks", (long long)state_stride, (long long)blocks);
+  const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the verifier replay step needs %lld workspace bytes",
+                (long long)ws.bytes);
+  TemporalArgs a = {};
+  a.source = current_scores;
+  a.source_stride = score_stride;
+  a.key_stride = length;
+  a.seeds = prev_topk;
+  a.scores = scores;
+  a.evaluated = evaluated_blocks;
+  a.qk_scored = qk_scored;
+  a.rows = (int32_t)batch;
+  a.length = (int32_t)length;
+  a.k = (int32_t)k;
+  a.block_size = block_size;
+  a.blocks = (int32_t)blocks;
+  a.prev_length = (int32_t)prev_length;
+  a.prev_blocks = (int32_t)((prev_length + block_size - 1) / block_size);
+  a.policy_mode = 1;
+  a.ap = ApproxDev{last_max, ema, volatility, age, cold_streak, state_stride, gamma_rows, *policy};
+  a.ws = ws;
+  VerifierArgs v = {};
+  v.width = spec->width;
+  v.verifier_scores = verifier_scores;
+  v.block_scores = block_scores;
+  v.cold_count = cold_count;
+  v.rescued = rescued_blocks;
+  v.ranking = ranking;
+  v.counts = counts;
+  v.promotion = spec->promotion;
+  v.fraction = spec->rescue_fraction;
+  v.threshold = spec->promotion_threshold;
+  v.vsource = recorded_verifier_scores;
+  v.vsource_stride = verifier_stride;
+  return launch_verifier<Bf16Tag, KeysB16>(a, v, spec->path, wave, DSA_DTYPE_BF16, out_topk,
+                                           static_cast<hipStream_t>(stream));
 }

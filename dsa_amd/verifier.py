@@ -499,3 +499,143 @@ def verifier_metrics(
         "physical_b64_key_byte_reduction": physical[64],
         "physical_b128_key_byte_reduction": physical[128],
     }
+
+
+# ---------------------------------------------------------------------------
+# Replay over recorded score rows (the reference's offline driver).
+# ---------------------------------------------------------------------------
+def verifier_replay_step(
+    state: ApproxState,
+    current_scores: torch.Tensor,
+    verifier_scores: torch.Tensor,
+    *,
+    policy: ApproxPolicy,
+    config: VerifierConfig,
+    step: int,
+    promotion_threshold: float | None = None,
+    wave: int = 1,
+) -> VerifierStep:
+    """One verifier step over recorded rows (reference verifier.py:173-392 as
+    ``replay_verifier_trace`` drives it): the dense scores ``[B, L]`` and the
+    verifier scores ``[B, L]`` (only cold keys are read) come from a trace
+    instead of from keys.  Advances ``state`` in place like
+    :func:`verifier_step`."""
+
+    _lib.load()
+    if current_scores.ndim != 2 or verifier_scores.shape != current_scores.shape:
+        raise ValueError("expected score rows [batch, L] and verifier rows of the same shape")
+    if not (current_scores.is_cuda and verifier_scores.is_cuda):
+        raise ValueError("HIP kernels require GPU tensors")
+    batch, length = current_scores.shape
+    block_size = state.block_size
+    if block_size != config.block_size:
+        raise ValueError("the state and the verifier config disagree on block_size")
+    if block_size not in BLOCK_SIZES:
+        raise ValueError(f"block_size must be one of {BLOCK_SIZES}")
+    if state.topk.shape[0] != batch:
+        raise ValueError("state and rows disagree on the batch")
+    if policy.risk_model not in RISK_MODELS:
+        raise ValueError(f"unknown risk model: {policy.risk_model}")
+    order, buckets = _order_code(policy.order)
+    previous_length = state.length
+    if length < previous_length:
+        raise ValueError("rows are shorter than the state's context")
+    blocks = math.ceil(length / block_size)
+    cap_blocks = state.last_max.shape[1]
+    if blocks > cap_blocks:
+        raise ValueError(f"context of {length} keys exceeds the state's capacity of {cap_blocks} blocks")
+    k = state.topk.shape[1]
+    wave = wave if policy.dynamic_threshold else 0
+    if policy.dynamic_threshold and wave < 1:
+        raise ValueError("a dynamic policy needs wave >= 1")
+    device = current_scores.device
+    spec = _lib.VerifierSpecC(
+        path=PATHS[config.path], width=int(config.width), promotion=0 if promotion_threshold is None else 1,
+        sketch_codes=0, rescue_fraction=float(config.rescue_fraction),
+        promotion_threshold=0.0 if promotion_threshold is None else float(promotion_threshold), sketch_scale=0.0,
+    )
+    full_refresh = bool(policy.name == "full" or (policy.refresh_interval and step % policy.refresh_interval == 0))
+    pol = _lib.ApproxPolicyC(
+        gamma=float(policy.gamma), age_slope=float(policy.age_slope), ema_alpha=float(policy.ema_alpha),
+        volatility_lambda=float(policy.volatility_lambda), risk_model=RISK_MODELS[policy.risk_model], order=order,
+        buckets=buckets, cold_streak=int(policy.cold_streak), age_cap=-1 if policy.age_cap is None else int(policy.age_cap),
+        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), reserved=0,
+    )
+    cur = current_scores.to(torch.float32).contiguous()
+    ver = verifier_scores.to(torch.float32).contiguous()
+    f32 = dict(device=device, dtype=torch.float32)
+    out = VerifierStep(
+        topk=torch.empty((batch, k), device=device, dtype=torch.int64),
+        scores=torch.empty((batch, length), **f32),
+        verifier_scores=torch.empty((batch, length), **f32),
+        block_scores=torch.empty((batch, blocks), **f32),
+        cold_count=torch.empty((batch, blocks), device=device, dtype=torch.uint8),
+        evaluated_blocks=torch.empty((batch, blocks), device=device, dtype=torch.uint8),
+        rescued_blocks=torch.empty((batch, blocks), device=device, dtype=torch.uint8),
+        ranking=torch.empty((batch, blocks), device=device, dtype=torch.int32),
+        qk_scored=torch.empty(batch, device=device, dtype=torch.int32),
+        counts=torch.empty((batch, 4), device=device, dtype=torch.int32),
+    )
+    stream = _lib.stream_of(cur)
+    ws = _workspace(device, stream, batch, length, k, block_size)
+    _lib.call(
+        "dsa_verifier_replay_step", _lib.ptr(cur), length, _lib.ptr(ver), length, ctypes.addressof(pol), None,
+        previous_length, _lib.ptr(state.topk), _lib.ptr(state.last_max), _lib.ptr(state.ema),
+        _lib.ptr(state.volatility), _lib.ptr(state.age), _lib.ptr(state.cold_streak), cap_blocks,
+        ctypes.addressof(spec), _lib.ptr(out.scores), _lib.ptr(out.verifier_scores), _lib.ptr(out.block_scores),
+        _lib.ptr(out.cold_count), _lib.ptr(out.evaluated_blocks), _lib.ptr(out.rescued_blocks), _lib.ptr(out.ranking),
+        _lib.ptr(out.topk), _lib.ptr(out.qk_scored), _lib.ptr(out.counts), batch, length, k, block_size, wave,
+        _lib.ptr(ws), ws.numel(), stream,
+    )
+    out.evaluated_blocks = out.evaluated_blocks.view(torch.bool)
+    out.rescued_blocks = out.rescued_blocks.view(torch.bool)
+    state.topk = out.topk
+    state.length = length
+    return out
+
+
+def replay_verifier_trace(
+    trace,
+    verifier_scores,
+    *,
+    policy: ApproxPolicy,
+    config: VerifierConfig,
+    k: int = 2048,
+    max_transitions: int | None = None,
+    tail_labels: dict | None = None,
+    detail_callback=None,
+    promotion_threshold=None,
+    wave: int = 1,
+):
+    """Replay one trace with recorded or lazily generated verifier scores
+    (reference verifier.py:395-432): every step on the GPU, and a pandas
+    DataFrame of the reference's per-step metrics.  ``verifier_scores`` is an
+    array ``[steps, >= L_t]`` or a callable ``(step, length) -> [length]``;
+    ``promotion_threshold`` a float, None or a callable of the same form."""
+
+    import pandas as pd
+
+    from .approx import initialize_state
+
+    device = torch.device("cuda", torch.cuda.current_device())
+    lengths = np.asarray(trace.lengths, dtype=np.int64)
+    row0 = torch.from_numpy(trace.row(0)).to(device).reshape(1, -1)
+    state = initialize_state(row0, k=k, block_size=config.block_size, capacity=int(lengths.max()))
+    stop = trace.scores.shape[0] if max_transitions is None else min(trace.scores.shape[0], max_transitions + 1)
+    rows = []
+    for step in range(1, stop):
+        length = int(lengths[step])
+        partial = verifier_scores(step, length) if callable(verifier_scores) else verifier_scores[step, :length]
+        threshold = promotion_threshold(step, length) if callable(promotion_threshold) else promotion_threshold
+        cur = torch.from_numpy(trace.row(step)).to(device).reshape(1, -1)
+        ver = torch.as_tensor(np.asarray(partial, dtype=np.float32)[:length]).to(device).reshape(1, -1)
+        out = verifier_replay_step(state, cur, ver, policy=policy, config=config, step=step,
+                                   promotion_threshold=threshold, wave=wave)
+        metrics = verifier_metrics(out, cur, config=config, policy=policy, step=step, promotion_threshold=threshold,
+                                   tail_critical_blocks=None if tail_labels is None else tail_labels.get(step))
+        metrics.update({"layer": trace.layer, "workload": trace.workload, "prompt_id": trace.prompt_id,
+                        "base_context_length": int(lengths[0]) - 1})
+        rows.append(metrics)
+        if detail_callback is not None:
+            detail_callback(step, out)
+    return pd.DataFrame(rows)

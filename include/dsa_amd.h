@@ -436,6 +436,22 @@ int dsa_verifier_step(const void* queries, const float* weights, const void* key
                       int32_t* counts, int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
                       int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The verifier step replayed over recorded rows (verifier.py:173-392 as
+ * replay_verifier_trace :395-432 drives it): the dense scores of row r come
+ * from current_scores [batch][score_stride] and the verifier scores of its
+ * cold keys from recorded_verifier_scores [batch][verifier_stride] instead of
+ * being computed from keys.  Other arguments, outputs and limits as
+ * dsa_verifier_step (spec->path and the sketch fields are not used). */
+int dsa_verifier_replay_step(const float* current_scores, int64_t score_stride,
+                             const float* recorded_verifier_scores, int64_t verifier_stride,
+                             const dsa_approx_policy* policy, const double* gamma_rows, int64_t prev_length,
+                             const int64_t* prev_topk, float* last_max, float* ema, float* volatility, int16_t* age,
+                             int16_t* cold_streak, int64_t state_stride, const dsa_verifier_spec* spec, float* scores,
+                             float* verifier_scores, float* block_scores, uint8_t* cold_count,
+                             uint8_t* evaluated_blocks, uint8_t* rescued_blocks, int32_t* ranking, int64_t* out_topk,
+                             int32_t* qk_scored, int32_t* counts, int64_t batch, int64_t length, int64_t k,
+                             int32_t block_size, int32_t wave, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Dimension sketch of rows x [rows][dim] (verifier_scoring.py:9-41, 95-139):
  * the normalized Walsh-Hadamard transform over dim (a power of two <= 128;
  * when rotate != 0), each butterfly sum and the final multiply by dim^-0.5
