@@ -21,6 +21,7 @@ import ctypes
 import math
 from dataclasses import dataclass, replace
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -71,6 +72,8 @@ class ApproxState:
     cold_streak: torch.Tensor  # int16 [B, capacity_blocks]
     length: int
     block_size: int
+    baseline_topk: torch.Tensor | None = None  # the dense top-k of the last step (replay over recorded rows)
+    seed_order: np.ndarray | None = None  # topk in rank order (larger score, then lower index), host
 
     @property
     def blocks(self) -> int:
@@ -141,6 +144,7 @@ def initialize_state(scores: torch.Tensor, *, k: int, block_size: int, capacity:
         cold_streak=torch.empty((batch, cap_blocks), device=dev, dtype=torch.int16),
         length=length,
         block_size=block_size,
+        baseline_topk=device_topk(rows, k, sorted=True),  # rank order: the first seeds of a replay
     )
     _lib.call(
         "dsa_approx_init_state", _lib.ptr(rows), length, _lib.ptr(top), _lib.ptr(state.last_max),
@@ -263,3 +267,181 @@ def approx_step(
     state.topk = topk
     state.length = length
     return TemporalStep(topk, scores, evaluated.view(torch.bool), qk)
+
+
+def _policy_struct(policy: ApproxPolicy, full_refresh: bool) -> "_lib.ApproxPolicyC":
+    order, buckets = (3, 0) if policy.order == "oracle_current" else _order_code(policy.order)
+    return _lib.ApproxPolicyC(
+        gamma=float(policy.gamma), age_slope=float(policy.age_slope), ema_alpha=float(policy.ema_alpha),
+        volatility_lambda=float(policy.volatility_lambda), risk_model=RISK_MODELS[policy.risk_model], order=order,
+        buckets=buckets, cold_streak=int(policy.cold_streak), age_cap=-1 if policy.age_cap is None else int(policy.age_cap),
+        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), reserved=0,
+    )
+
+
+def _rank_order(indices: np.ndarray, scores: np.ndarray) -> np.ndarray:
+    """indices ordered by larger score, then lower index."""
+
+    indices = np.asarray(indices, dtype=np.int64)
+    return indices[np.lexsort((indices, -scores[indices]))]
+
+
+def _metadata_bytes_per_block(policy: ApproxPolicy) -> int:
+    raw = 6 + (1 if policy.order.startswith("bucket") else 0) + (8 if policy.risk_model == "ema" else 0)
+    return int(math.ceil(raw / 4) * 4)
+
+
+def replay_step(
+    state: ApproxState,
+    current_scores,
+    *,
+    policy: ApproxPolicy,
+    k: int,
+    block_size: int,
+    step: int,
+    history_mode: str = "own",
+    previous_length: int | None = None,
+    fallback_value: float | None = None,
+    wave: int = 1,
+):
+    """One transition replayed over a recorded score row (reference
+    approx.py:129-364, ``history_mode="own"``): the pruning scan, the top-k of
+    the evaluated keys and the state update run in the HIP kernels with the
+    row as the score source; returns ``(state, metrics, details)`` with the
+    reference's metrics dict and details.  ``state`` (one sequence) is
+    advanced in place.  The teacher history needs the reference's dense
+    bookkeeping of every transition and stays with the reference.  The
+    ``oracle_current`` order is available here (the row is known)."""
+
+    if history_mode not in {"own", "teacher"}:
+        raise ValueError("history_mode must be 'own' or 'teacher'")
+    if history_mode == "teacher":
+        raise ValueError("the device replay runs history_mode='own'")
+    _lib.load()
+    if state.topk.shape[0] != 1:
+        raise ValueError("replay_step takes a one-sequence state")
+    if block_size != state.block_size:
+        raise ValueError("block_size differs from the state's")
+    device = state.topk.device
+    host = np.asarray(current_scores.cpu() if isinstance(current_scores, torch.Tensor) else current_scores,
+                      dtype=np.float32)
+    length = host.size
+    if k > length:
+        raise ValueError("K cannot exceed the current trace length")
+    previous_length = state.length if previous_length is None else int(previous_length)
+    blocks = math.ceil(length / block_size)
+    cap_blocks = state.last_max.shape[1]
+    if blocks > cap_blocks:
+        raise ValueError(f"context of {length} keys exceeds the state's capacity of {cap_blocks} blocks")
+    seed_host = state.seed_order
+    if seed_host is None:  # right after initialize_state: its top-k in rank order
+        seed_host = state.baseline_topk[0].cpu().numpy() if state.baseline_topk is not None else state.topk[0].cpu().numpy()
+    seed_host = seed_host[seed_host < length].astype(np.int64)
+    if seed_host.size != k or np.unique(seed_host).size != k:
+        raise RuntimeError(f"previous Top-K seed has {seed_host.size} unique keys, expected {k}")
+    fallback = bool(policy.fallback_threshold is not None and fallback_value is not None
+                    and fallback_value > policy.fallback_threshold)
+    full_refresh = bool(policy.name == "full" or (policy.refresh_interval and step % policy.refresh_interval == 0)
+                        or fallback)
+    if policy.dynamic_threshold and wave < 1:
+        raise ValueError("a dynamic policy needs wave >= 1")
+    pol = _policy_struct(policy, full_refresh)
+    row = torch.from_numpy(host).to(device).reshape(1, -1)
+    scores = torch.empty((1, length), device=device, dtype=torch.float32)
+    evaluated = torch.empty((1, blocks), device=device, dtype=torch.uint8)
+    top = torch.empty((1, k), device=device, dtype=torch.int64)
+    qk = torch.empty(1, device=device, dtype=torch.int32)
+    stream = _lib.stream_of(row)
+    ws = _workspace(device, stream, 1, length, k, block_size)
+    from .temporal import block_max
+
+    current_max = block_max(row, block_size) if policy.order == "oracle_current" else None
+    _lib.call(
+        "dsa_approx_replay_step", _lib.ptr(row), length, _lib.ptr(current_max), ctypes.addressof(pol), None,
+        previous_length,
+        _lib.ptr(state.topk), _lib.ptr(state.last_max), _lib.ptr(state.ema), _lib.ptr(state.volatility),
+        _lib.ptr(state.age), _lib.ptr(state.cold_streak), cap_blocks, _lib.ptr(scores), _lib.ptr(evaluated),
+        _lib.ptr(top), _lib.ptr(qk), 1, length, k, block_size, wave if policy.dynamic_threshold else 0, _lib.ptr(ws),
+        ws.numel(), stream,
+    )
+    baseline = device_topk(row, k, sorted=True)[0].cpu().numpy()
+    scored = np.flatnonzero(np.isfinite(scores[0].cpu().numpy()))
+    approximate = _rank_order(top[0].cpu().numpy(), host)
+    refreshed = evaluated[0].cpu().numpy().astype(bool)
+    approx_mask = np.zeros(length, dtype=bool)
+    approx_mask[approximate] = True
+    base_mask = np.zeros(length, dtype=bool)
+    base_mask[baseline] = True
+    previous_baseline = state.baseline_topk.reshape(-1).cpu().numpy() if state.baseline_topk is not None else baseline
+    newly_hot = np.setdiff1d(baseline, previous_baseline)
+    newly_missed = int((~approx_mask[newly_hot]).sum()) if newly_hot.size else 0
+    missed_rank = np.flatnonzero(~approx_mask[baseline]) + 1
+    seed_blocks = np.unique(seed_host // block_size)
+    meta_bpb = _metadata_bytes_per_block(policy)
+    meta = blocks * meta_bpb
+
+    def keep(count: int) -> float:
+        count = min(count, baseline.size)
+        return float(np.isin(baseline[:count], approximate).sum() / count)
+
+    shift = float(np.max(host[baseline]))
+    mass = float(np.exp(host[approximate].astype(np.float64) - shift).sum()
+                 / max(np.exp(host[baseline].astype(np.float64) - shift).sum(), 1e-300))
+    metrics = {
+        "step": step, "context_length": length, "history_mode": history_mode, "policy": policy.name,
+        "gamma": policy.gamma, "k": k, "block_size": block_size, "qk_scored": int(scored.size),
+        "qk_reduction": float(1.0 - scored.size / length),
+        "exact_match": bool(np.array_equal(np.sort(approximate), np.sort(baseline))),
+        "recall": float(base_mask[approximate].sum() / k),
+    }
+    for count in (128, 256, 512, 1024, 2048):
+        metrics[f"top{count}_recall"] = keep(count)
+    metrics.update({
+        "index_mass_ratio": mass,
+        "newly_hot_count": int(newly_hot.size),
+        "newly_hot_missed": newly_missed,
+        "newly_hot_miss_rate": float(newly_missed / newly_hot.size) if newly_hot.size else 0.0,
+        "missed_count": int(missed_rank.size),
+        "worst_missed_rank": int(missed_rank.min()) if missed_rank.size else 0,
+        "tau_seed": float(np.min(host[seed_host])),
+        "tau_final": float(np.min(host[approximate])),
+        "full_refresh": full_refresh,
+        "fallback": fallback,
+        "blocks_refreshed": int(refreshed.sum()),
+        "blocks_skipped": int(blocks - refreshed.sum()),
+        "seed_blocks_touched": int(seed_blocks.size),
+        "seed_block_fraction": float(seed_blocks.size / blocks),
+        "metadata_bytes_per_block": meta_bpb,
+        "metadata_bytes": meta,
+        "ideal_bf16_bytes": int(scored.size * 256 + meta),
+        "ideal_fp8_bytes": int(scored.size * 128 + meta),
+        "net_bf16_reduction": float(1.0 - (scored.size * 256 + meta) / (length * 256)),
+        "net_fp8_reduction": float(1.0 - (scored.size * 128 + meta) / (length * 128)),
+    })
+    for physical in (16, 32, 64, 128):
+        touched = np.unique(scored // physical).size
+        total = (length + physical - 1) // physical
+        metrics[f"physical_b{physical}_blocks"] = int(touched)
+        metrics[f"physical_b{physical}_reduction"] = float(1.0 - touched / total)
+    evaluated_keys = np.zeros(length, dtype=bool)
+    evaluated_keys[scored] = True
+    for entries in (0, 256, 512, 1024, 2048):
+        uncached = evaluated_keys.copy()
+        uncached[seed_host[: min(entries, seed_host.size)]] = False
+        hbm = int(uncached.sum())
+        metrics[f"cache{entries}_hbm_keys"] = hbm
+        metrics[f"cache{entries}_net_bf16_reduction"] = float(1.0 - (hbm * 256 + meta) / (length * 256))
+    details = {
+        "approximate": approximate,
+        "baseline": baseline,
+        "evaluated": scored,
+        "seed": seed_host.copy(),
+        "refreshed_blocks": np.flatnonzero(refreshed).astype(np.int32),
+        "skipped_blocks": np.flatnonzero(~refreshed).astype(np.int32),
+        "missed_ranks": missed_rank.astype(np.int32),
+    }
+    state.topk = torch.from_numpy(approximate).to(device).reshape(1, -1)
+    state.seed_order = approximate
+    state.baseline_topk = torch.from_numpy(baseline).to(device).reshape(1, -1)
+    state.length = length
+    return state, metrics, details

@@ -89,9 +89,11 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
       const int cold = stored ? a.ap.cold[at] : 1;
       const int recent_first = p.recent_window > 0 ? max(0, L - p.recent_window) / bs : nb;
       rank_value = policy_risk(p, gamma, last, ema, vol, age);
+      const double risk = rank_value;
+      if (p.order == DSA_ORDER_CURRENT_MAX) rank_value = (double)a.order_key[(size_t)row * nb + b];
       const bool forced = p.full_refresh || (grown && b >= first_new) || b >= recent_first ||
                           (p.age_cap >= 0 && age >= p.age_cap) || cold < p.cold_streak;
-      upper = forced ? HUGE_VAL : rank_value;
+      upper = forced ? HUGE_VAL : risk;
     } else {
       const bool fresh = grown && b >= first_new;
       const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
@@ -839,6 +841,57 @@ extern "C" int dsa_approx_step(const void* queries, const float* weights, const 
   a.ap = ApproxDev{last_max, ema, volatility, age, cold_streak, state_stride, gamma_rows, *policy};
   a.ws = ws;
   return run_step(a, wave, key_dtype, out_topk, stream);
+}
+
+extern "C" int dsa_approx_replay_step(const float* current_scores, int64_t score_stride,
+                                      const float* current_block_max, const dsa_approx_policy* policy,
+                                      const double* gamma_rows, int64_t prev_length,
+                                      const int64_t* prev_topk, float* last_max, float* ema, float* volatility,
+                                      int16_t* age, int16_t* cold_streak, int64_t state_stride, float* scores,
+                                      uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
+                                      int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
+  DSA_REQUIRE(current_scores && policy && prev_topk && last_max && ema && volatility && age && cold_streak && scores &&
+                  evaluated_blocks && out_topk && qk_scored,
+              "null pointer argument");
+  DSA_REQUIRE(score_stride >= length, "score_stride < length");
+  if (int st = check_step(nullptr, nullptr, length, nullptr, prev_length, batch, length, k, block_size, wave,
+                          DSA_DTYPE_BF16, workspace))
+    return st;
+  DSA_REQUIRE(policy->risk_model == DSA_RISK_LAST_MAX || policy->risk_model == DSA_RISK_EMA,
+              "risk_model %d unknown", policy->risk_model);
+  DSA_REQUIRE(policy->order >= DSA_ORDER_ADDRESS && policy->order <= DSA_ORDER_CURRENT_MAX, "order %d unknown",
+              policy->order);
+  DSA_REQUIRE(policy->order != DSA_ORDER_CURRENT_MAX || current_block_max,
+              "the current-max order needs current_block_max");
+  DSA_REQUIRE(policy->order != DSA_ORDER_BUCKET || policy->buckets >= 1, "bucket order needs buckets >= 1");
+  DSA_REQUIRE(policy->recent_window >= 0, "recent_window must be >= 0");
+  const int64_t blocks = (length + block_size - 1) / block_size;
+  DSA_REQUIRE(state_stride >= blocks, "state_stride %lld < %lld blocks", (long long)state_stride, (long long)blocks);
+  const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
+  if (!workspace || workspace_bytes < ws.bytes)
+    return fail(DSA_STATUS_WORKSPACE_TOO_SMALL, "the approximate replay step needs %lld workspace bytes",
+                (long long)ws.bytes);
+  TemporalArgs a = {};
+  a.source = current_scores;
+  a.source_stride = score_stride;
+  a.order_key = current_block_max;
+  a.key_stride = length;
+  a.seeds = prev_topk;
+  a.scores = scores;
+  a.evaluated = evaluated_blocks;
+  a.qk_scored = qk_scored;
+  a.rows = (int32_t)batch;
+  a.length = (int32_t)length;
+  a.k = (int32_t)k;
+  a.block_size = block_size;
+  a.blocks = (int32_t)blocks;
+  a.prev_length = (int32_t)prev_length;
+  a.prev_blocks = (int32_t)((prev_length + block_size - 1) / block_size);
+  a.policy_mode = 1;
+  a.ap = ApproxDev{last_max, ema, volatility, age, cold_streak, state_stride, gamma_rows, *policy};
+  a.ws = ws;
+  return run_step(a, wave, DSA_DTYPE_BF16, out_topk, stream);
 }
 
 extern "C" int dsa_approx_init_state(const float* scores, int64_t score_stride, const int64_t* topk,

@@ -331,6 +331,7 @@ int dsa_temporal_step(const void* queries, const float* weights, const void* key
 #define DSA_ORDER_ADDRESS 0
 #define DSA_ORDER_PREVIOUS_MAX 1 /* also "predicted_risk" */
 #define DSA_ORDER_BUCKET 2
+#define DSA_ORDER_CURRENT_MAX 3 /* "oracle_current": replay over recorded rows only */
 
 typedef struct dsa_approx_policy {
   double gamma;
@@ -354,6 +355,19 @@ int dsa_approx_step(const void* queries, const float* weights, const void* keys,
                     float* scores, uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
                     int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
                     int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The own-trajectory step replayed over recorded score rows (approx.py:129-364
+ * replay_step, history_mode "own"): row r's scores come from current_scores
+ * [batch][score_stride] instead of being computed from keys.  The order
+ * DSA_ORDER_CURRENT_MAX (the reference's "oracle_current") visits blocks by
+ * larger current_block_max [batch][blocks] (fp32, nullable otherwise), then
+ * lower address.  Other arguments, outputs and limits as dsa_approx_step. */
+int dsa_approx_replay_step(const float* current_scores, int64_t score_stride, const float* current_block_max,
+                           const dsa_approx_policy* policy, const double* gamma_rows, int64_t prev_length, const int64_t* prev_topk, float* last_max,
+                           float* ema, float* volatility, int16_t* age, int16_t* cold_streak, int64_t state_stride,
+                           float* scores, uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
+                           int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave, void* workspace,
+                           int64_t workspace_bytes, void* stream);
 
 /* initialize_state (approx.py:112-126) from dense score rows [batch, length]
  * (row stride score_stride) and their top-k (any order): last_max = ema =
