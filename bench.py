@@ -1133,6 +1133,30 @@ def run_sidecar(args) -> None:
                     if it >= 10:
                         ms.append(e0.elapsed_time(e1))
                 timings[label] = time_stats(ms)
+            # The same calls captured in a HIP graph and replayed: GPU time
+            # without the host's per-launch cost (one sequence of launches per
+            # replay, a cache flush before each).
+            for label, fn in (("library", library), ("torch_formula", formula)):
+                graph = torch.cuda.CUDAGraph()
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    fn()  # warm the allocator on the capture stream
+                torch.cuda.current_stream().wait_stream(side)
+                with torch.cuda.graph(graph):
+                    fn()
+                ms = []
+                for it in range(60):
+                    flush()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    graph.replay()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    if it >= 10:
+                        ms.append(e0.elapsed_time(e1))
+                timings[f"{label}_graph"] = time_stats(ms)
+                del graph
         weight_bytes = (module.wq.weight.numel() + module.wk.weight.numel()) * 2 + module.weights_proj.weight.numel() * 4
         epi_bytes = tokens * (128 * 2 * 2 + 64 * 128 * 2 * 2 + 64 * 4 * 2 + 8 + 8)
         results[name] = {

@@ -172,6 +172,29 @@ class LightningIndexerSidecar(nn.Module):
         nn.init.normal_(self.wk.weight, mean=0.0, std=self.hidden_size**-0.5)
         nn.init.normal_(self.weights_proj.weight, mean=0.0, std=self.hidden_size**-0.5)
 
+    def _project(self, hidden: torch.Tensor, weight: torch.Tensor, *, fp32: bool = False) -> torch.Tensor:
+        """A Linear without bias: ``hidden @ weight.T`` (bf16, or on
+        ``hidden.float()`` in fp32 for ``weights_proj``).  A decode step (at
+        most 16 tokens, bf16 hidden) streams the weights in the HIP projection
+        kernel (``dsa_project_rows``); larger batches use the platform GEMM."""
+
+        tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
+        kdim = hidden.shape[-1]
+        fits = (0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0 and not torch.is_grad_enabled()
+                and (weight.dtype == torch.float32 if fp32 else (weight.dtype == torch.bfloat16 and weight.shape[0] % 16 == 0)))
+        if not fits:
+            return F.linear(hidden.float(), weight.float()) if fp32 else F.linear(hidden, weight)
+        flat = hidden.reshape(tokens, kdim)
+        if flat.stride(-1) != 1 or flat.stride(0) % 8 or flat.data_ptr() % 16:
+            flat = flat.contiguous()
+        w = weight.detach().contiguous()
+        features = w.shape[0]
+        out = torch.empty((tokens, features), device=hidden.device, dtype=torch.float32 if fp32 else torch.bfloat16)
+        _lib.call("dsa_project_rows", _lib.ptr(flat), flat.stride(0), tokens, _lib.ptr(w),
+                  _lib.DTYPE_F32 if fp32 else _lib.DTYPE_BF16, features, kdim, _lib.ptr(out), features,
+                  _lib.stream_of(flat))
+        return out.reshape(*hidden.shape[:-1], features)
+
     def encode_keys(
         self,
         hidden: torch.Tensor,
@@ -191,7 +214,7 @@ class LightningIndexerSidecar(nn.Module):
 
         if not hidden.is_cuda:
             raise ValueError("HIP kernels require GPU tensors")
-        proj = F.linear(hidden, self.wk.weight)
+        proj = self._project(hidden, self.wk.weight)
         tokens_shape = proj.shape[:-1]
         tokens = math.prod(tokens_shape)
         flat = proj.reshape(tokens, self.head_dim).contiguous()
@@ -226,8 +249,8 @@ class LightningIndexerSidecar(nn.Module):
 
         if not hidden.is_cuda:
             raise ValueError("HIP kernels require GPU tensors")
-        proj = F.linear(hidden, self.wq.weight)
-        proj_w = F.linear(hidden.float(), self.weights_proj.weight.float())
+        proj = self._project(hidden, self.wq.weight)
+        proj_w = self._project(hidden, self.weights_proj.weight, fp32=True)
         tokens_shape = proj.shape[:-1]
         tokens = math.prod(tokens_shape)
         flat = proj.reshape(tokens, self.heads * self.head_dim).contiguous()

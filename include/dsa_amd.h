@@ -531,6 +531,16 @@ int dsa_temporal_score_radius(const float* q_now, const float* q_prev, const flo
 int dsa_rope(const void* x, void* out, const int64_t* positions, int64_t tokens, int32_t heads,
              int32_t dim, int32_t rope_dim, float theta, int32_t dtype, void* stream);
 
+/* Decode-step projections (sidecar.py:74-88: wq / wk on bf16 hidden,
+ * weights_proj on hidden.float()) for 1..16 tokens, weight-streaming:
+ * out[t][n] = sum_k hidden[t][k] * weight[n][k] with hidden bf16
+ * [tokens][hidden_stride], weight [features][kdim] row-major (a Linear's
+ * weight) and fp32 accumulation.  weight_dtype DSA_DTYPE_BF16: MFMA, features
+ * a multiple of 16, out bf16 (rounded once); DSA_DTYPE_F32: fp32 FMAs, out
+ * fp32.  kdim a multiple of 32. */
+int dsa_project_rows(const void* hidden, int64_t hidden_stride, int64_t tokens, const void* weight,
+                     int32_t weight_dtype, int64_t features, int64_t kdim, void* out, int64_t out_stride, void* stream);
+
 /* encode_keys after wk (sidecar.py:74-76 and 67-72): LayerNorm over dim
  * (fp32 weight/bias, biased variance, eps), then RoPE on the first rope_dim
  * dims, written to out row out_rows[t] (or t when out_rows is NULL) so that a

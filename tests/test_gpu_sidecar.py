@@ -203,3 +203,25 @@ def test_forward_scores_match_float64(device) -> None:
     want = (np.maximum(dots, 0) * wn[..., None]).sum(axis=2)
     scale = (np.abs(dots) * np.abs(wn)[..., None]).sum(axis=2)
     assert np.all(np.abs(scores - want) <= 1e-5 * scale + 1e-6)
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 16])
+def test_decode_projection_kernel_matches_float64(device, tokens) -> None:
+    """dsa_project_rows (the decode-step projections): bf16 outputs within one
+    bf16 rounding of the float64 product, fp32 weights_proj to 1e-5; a batch
+    above 16 tokens takes the platform GEMM path with the same result."""
+
+    torch.manual_seed(tokens)
+    module = sidecar.LightningIndexerSidecar(hidden_size=2048).to(device=device, dtype=torch.bfloat16).eval()
+    hidden = torch.randn(tokens, 2048, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        q = module._project(hidden, module.wq.weight).float().cpu().numpy().astype(np.float64)
+        k = module._project(hidden, module.wk.weight).float().cpu().numpy().astype(np.float64)
+        w = module._project(hidden, module.weights_proj.weight, fp32=True).cpu().numpy().astype(np.float64)
+    h64 = hidden.float().cpu().numpy().astype(np.float64)
+    for got, weight in ((q, module.wq.weight), (k, module.wk.weight)):
+        want = h64 @ weight.detach().float().cpu().numpy().astype(np.float64).T
+        # one bf16 rounding of the exact product (plus fp32 accumulation error)
+        np.testing.assert_allclose(got, want, rtol=2 ** -8, atol=1e-4 * np.abs(want).max())
+    want_w = h64 @ module.weights_proj.weight.detach().float().cpu().numpy().astype(np.float64).T
+    np.testing.assert_allclose(w, want_w, rtol=1e-5, atol=1e-6 * np.abs(want_w).max())
