@@ -3,8 +3,9 @@
 //
 // One workgroup per (virtual) row: 1024 threads, or 256 when many short rows
 // (at most 4096 entries) make throughput matter more than latency.  Thread t owns the contiguous
-// slice [t * EPT, t * EPT + EPT) of the row in registers, so a single
-// exclusive scan over threads enumerates elements in index order.  The k-th
+// slice [t * ept, t * ept + ept) of the row in registers (ept <= EPT, sized to
+// the row's length), so a single exclusive scan over threads enumerates
+// elements in index order.  The k-th
 // largest (value, index) pair is found by a value-linear bucket select whose
 // crowded-bucket or degenerate cases fall back to an exact radix select; the
 // chosen elements are written in index order, or bitonic-sorted in LDS by
@@ -17,6 +18,7 @@ namespace {
 
 constexpr int kTopkThreads = 1024;  // widest workgroup (long rows)
 constexpr int kMaxK = 4096;
+constexpr int kSmallCap = 1024;  // candidate buffer of the short-row kernel
 constexpr int kBins = 2048;
 
 struct TopkArgs {
@@ -33,17 +35,18 @@ struct TopkArgs {
   float* out_val;
 };
 
-template <int THREADS>
+template <int THREADS, int CAP>
 struct TopkShared {
   static constexpr int kWaves = THREADS / kWave;
   uint32_t hist[kBins];
   uint32_t wave_sums[kWaves];
+  uint32_t wave_valid[kWaves];
   float wave_lo[kWaves];
   float wave_hi[kWaves];
   uint32_t digit;
   uint32_t krem;
   uint64_t cstar;
-  uint64_t sort_keys[kMaxK + 1];  // slot kMaxK is a write sink for unchosen lanes
+  uint64_t sort_keys[CAP + 1];  // slot CAP is a write sink for unchosen lanes
 };
 
 // Exclusive prefix sum over the workgroup in thread order; returns the total
@@ -118,8 +121,8 @@ __device__ __forceinline__ int value_bucket(uint32_t key, float lo, float scale)
 // Finds the bin holding the want-th largest element of the histogram in
 // sh.hist; leaves it in sh.digit and the remaining rank inside it in sh.krem.
 // Thread t scans bins [t * B, t * B + B), B = kBins / THREADS.
-template <int THREADS>
-__device__ __forceinline__ void locate_bin(TopkShared<THREADS>& sh, uint32_t want) {
+template <int THREADS, int CAP>
+__device__ __forceinline__ void locate_bin(TopkShared<THREADS, CAP>& sh, uint32_t want) {
   constexpr int B = kBins / THREADS;
   const int tid = threadIdx.x;
   uint32_t c[B];
@@ -153,14 +156,15 @@ __device__ __forceinline__ void locate_bin(TopkShared<THREADS>& sh, uint32_t wan
 //      11+11+10-bit radix select over the ordered keys for the k-th value,
 //      whose ties are ranked by position with a prefix scan.
 // All per-element work is branch-free (predicated adds and sink-slot writes).
-template <int THREADS, int EPT>
+template <int THREADS, int EPT, int CAP>
 __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
   constexpr int kWaves = THREADS / kWave;
-  __shared__ TopkShared<THREADS> sh;
+  __shared__ TopkShared<THREADS, CAP> sh;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t v = blockIdx.x;
+  // Last virtual rows first: under causal row lengths they are the longest.
+  const int64_t v = (int64_t)gridDim.x - 1 - blockIdx.x;
   const int64_t row = v / a.chunks;
   const int chunk = (int)(v % a.chunks);
   int row_len = a.length;
@@ -173,12 +177,19 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
 
   // Load this thread's slice as ordered keys; 0 marks an invalid slot.  The
   // buffer bounds check turns reads past n into zeros, which are masked.
+  // Each thread owns ept <= EPT contiguous slots, ept a multiple of 4 just
+  // large enough for the row's n entries, so short rows cost little: every
+  // per-slot loop stops at ept (a workgroup-uniform bound).
   uint32_t key[EPT];
-  const int e0 = tid * EPT;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) key[e] = 0u;
+  const int ept = min(EPT, (n + 4 * THREADS - 1) / (4 * THREADS) * 4);
+  const int e0 = tid * ept;
   {
     const BufferRsrc rsrc = make_buffer(a.scores + base, (uint32_t)n * 4u);
 #pragma unroll
     for (int c = 0; c < EPT / 4; ++c) {
+      if (4 * c >= ept) break;
       const uint4 raw = buffer_load_16(rsrc, (uint32_t)(e0 + 4 * c) * 4u);
       const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -188,8 +199,10 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
     if (a.in_idx) {
       const int64_t* ids = a.in_idx + base;
 #pragma unroll
-      for (int e = 0; e < EPT; ++e)
+      for (int e = 0; e < EPT; ++e) {
+        if (e >= ept) break;
         if (e0 + e < n && ids[e0 + e] < 0) key[e] = 0;
+      }
     }
   }
 
@@ -197,29 +210,29 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
   // valid slot (key >= 1) is chosen.
   uint64_t cstar = uint64_t(1) << 32;
   uint32_t n_valid = 0;
+  float lo = __builtin_inff();
+  float hi = -__builtin_inff();
   if (n > k) {
+    // Valid count and finite range of the row in one pass and one barrier;
+    // the histogram is cleared in the same phase.
     uint32_t mine = 0;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) mine += key[e] != 0 ? 1u : 0u;
-    block_exclusive_scan<kWaves>(mine, sh.wave_sums, n_valid);
-  }
-  if (n_valid > (uint32_t)k) {
-    bool resolved = false;
-    float lo = __builtin_inff();
-    float hi = -__builtin_inff();
-#pragma unroll
     for (int e = 0; e < EPT; ++e) {
+      if (e >= ept) break;
       const float f = ordered_to_float(key[e]);
       const bool fin = key[e] != 0 && __builtin_isfinite(f);
+      mine += key[e] != 0 ? 1u : 0u;
       lo = fminf(lo, fin ? f : __builtin_inff());
       hi = fmaxf(hi, fin ? f : -__builtin_inff());
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
+      mine += __shfl_xor(mine, off, kWave);
       lo = fminf(lo, __shfl_xor(lo, off, kWave));
       hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
     }
     if (lane == 0) {
+      sh.wave_valid[wave] = mine;
       sh.wave_lo[wave] = lo;
       sh.wave_hi[wave] = hi;
     }
@@ -227,40 +240,63 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) {
+      n_valid += sh.wave_valid[i];
       lo = fminf(lo, sh.wave_lo[i]);
       hi = fmaxf(hi, sh.wave_hi[i]);
     }
+  }
+  if (n_valid > (uint32_t)k) {
+    bool resolved = false;
     const float scale = (float)kBins / (hi - lo);
     if (lo < hi && __builtin_isfinite(scale) && scale > 0.f) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e)
+      for (int e = 0; e < EPT; ++e) {
+        if (e >= ept) break;
         lds_add(&sh.hist[value_bucket(key[e], lo, scale)], key[e] != 0 ? 1u : 0u);
+      }
       __syncthreads();
       locate_bin(sh, (uint32_t)k);
       const int bucket = (int)sh.digit;
       const uint32_t need = sh.krem;
       const uint32_t crowd = sh.hist[bucket];
-      if (crowd <= (uint32_t)kMaxK) {
+      if (crowd <= (uint32_t)CAP) {
         // Gather bucket T's composites at scan-assigned slots, sort them and
         // read the need-th largest.
         uint32_t mine = 0;
 #pragma unroll
-        for (int e = 0; e < EPT; ++e)
+        for (int e = 0; e < EPT; ++e) {
+          if (e >= ept) break;
           mine += (key[e] != 0 && value_bucket(key[e], lo, scale) == bucket) ? 1u : 0u;
+        }
         uint32_t total;
         uint32_t slot = block_exclusive_scan<kWaves>(mine, sh.wave_sums, total);
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
+          if (e >= ept) break;
           const bool in_t = key[e] != 0 && value_bucket(key[e], lo, scale) == bucket;
-          sh.sort_keys[in_t ? slot : kMaxK] = composite(key[e], e0 + e);
+          sh.sort_keys[in_t ? slot : CAP] = composite(key[e], e0 + e);
           slot += in_t ? 1u : 0u;
         }
-        int width = 1;
-        while (width < (int)crowd) width <<= 1;
-        for (int i = (int)crowd + tid; i < width; i += THREADS) sh.sort_keys[i] = 0;
-        __syncthreads();
-        bitonic_sort_desc<THREADS>(sh.sort_keys, width);
-        cstar = sh.sort_keys[need - 1];
+        if (crowd <= (uint32_t)kWave) {
+          // Few candidates: the one with need - 1 larger composites is cstar
+          // (composites are distinct).
+          __syncthreads();
+          if (tid < (int)crowd) {
+            const uint64_t c = sh.sort_keys[tid];
+            uint32_t larger = 0;
+            for (int j = 0; j < (int)crowd; ++j) larger += sh.sort_keys[j] > c ? 1u : 0u;
+            if (larger + 1 == need) sh.cstar = c;
+          }
+          __syncthreads();
+          cstar = sh.cstar;
+        } else {
+          int width = 1;
+          while (width < (int)crowd) width <<= 1;
+          for (int i = (int)crowd + tid; i < width; i += THREADS) sh.sort_keys[i] = 0;
+          __syncthreads();
+          bitonic_sort_desc<THREADS>(sh.sort_keys, width);
+          cstar = sh.sort_keys[need - 1];
+        }
         resolved = true;
       }
     }
@@ -277,9 +313,11 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
         for (int i = tid; i < kBins; i += THREADS) sh.hist[i] = 0;
         __syncthreads();
 #pragma unroll
-        for (int e = 0; e < EPT; ++e)
+        for (int e = 0; e < EPT; ++e) {
+          if (e >= ept) break;
           lds_add(&sh.hist[(key[e] >> shift) & dmask],
                   (key[e] != 0 && (key[e] & prefix_mask) == prefix) ? 1u : 0u);
+        }
         __syncthreads();
         locate_bin(sh, want);
         prefix |= sh.digit << shift;
@@ -289,11 +327,15 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
       const uint32_t threshold = prefix;
       uint32_t mine = 0;
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) mine += key[e] == threshold ? 1u : 0u;
+      for (int e = 0; e < EPT; ++e) {
+        if (e >= ept) break;
+        mine += key[e] == threshold ? 1u : 0u;
+      }
       uint32_t ties;
       uint32_t rank = block_exclusive_scan<kWaves>(mine, sh.wave_sums, ties);
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
+        if (e >= ept) break;
         const bool tie = key[e] == threshold;
         if (tie && rank + 1 == want) sh.cstar = composite(threshold, e0 + e);
         rank += tie ? 1u : 0u;
@@ -304,34 +346,52 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
     __syncthreads();
   }
 
-  // Chosen elements (composite >= cstar) in index order.
+  // Chosen elements (composite >= cstar) in index order: thread slices are
+  // contiguous, so the exclusive scan of the per-thread counts is each
+  // element's output slot.
   uint32_t n_sel = 0;
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) n_sel += composite(key[e], e0 + e) >= cstar ? 1u : 0u;
+  for (int e = 0; e < EPT; ++e) {
+    if (e >= ept) break;
+    n_sel += composite(key[e], e0 + e) >= cstar ? 1u : 0u;
+  }
   uint32_t sel_total;
   uint32_t p = block_exclusive_scan<kWaves>(n_sel, sh.wave_sums, sel_total);
   // Exactly min(valid, k) elements are chosen; the clamp only guards buffers.
   sel_total = min(sel_total, (uint32_t)k);
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const uint64_t c = composite(key[e], e0 + e);
-    const bool chosen = c >= cstar;
-    sh.sort_keys[(chosen && p < sel_total) ? p : kMaxK] = c;
-    p += chosen ? 1u : 0u;
-  }
-  __syncthreads();
-
   if (a.sorted) {
+    // Stage the chosen composites (at most k <= CAP) and sort them by (value desc, index asc).
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (e >= ept) break;
+      const uint64_t c = composite(key[e], e0 + e);
+      const bool chosen = c >= cstar;
+      sh.sort_keys[(chosen && p < sel_total) ? p : CAP] = c;
+      p += chosen ? 1u : 0u;
+    }
+    __syncthreads();
     int width = 1;
     while (width < (int)sel_total) width <<= 1;
     for (int i = (int)sel_total + tid; i < width; i += THREADS) sh.sort_keys[i] = 0;
     __syncthreads();
     bitonic_sort_desc<THREADS>(sh.sort_keys, width);
-  }
-  for (int i = tid; i < (int)sel_total; i += THREADS) {
-    const uint32_t pos = ~(uint32_t)(sh.sort_keys[i] & 0xffffffffu);
-    if (a.out_idx) a.out_idx[out_base + i] = a.in_idx ? a.in_idx[base + pos] : (int64_t)(start + pos);
-    if (a.out_val) a.out_val[out_base + i] = a.scores[base + pos];
+    for (int i = tid; i < (int)sel_total; i += THREADS) {
+      const uint32_t pos = ~(uint32_t)(sh.sort_keys[i] & 0xffffffffu);
+      if (a.out_idx) a.out_idx[out_base + i] = a.in_idx ? a.in_idx[base + pos] : (int64_t)(start + pos);
+      if (a.out_val) a.out_val[out_base + i] = a.scores[base + pos];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (e >= ept) break;
+      const bool chosen = composite(key[e], e0 + e) >= cstar && p < sel_total;
+      if (chosen) {
+        const int pos = e0 + e;
+        if (a.out_idx) a.out_idx[out_base + p] = a.in_idx ? a.in_idx[base + pos] : (int64_t)(start + pos);
+        if (a.out_val) a.out_val[out_base + p] = a.scores[base + pos];
+      }
+      p += chosen ? 1u : 0u;
+    }
   }
   // Padding when fewer than k valid entries exist.
   for (int i = (int)sel_total + tid; i < k; i += THREADS) {
@@ -343,19 +403,20 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
 int launch_topk(const TopkArgs& a, int64_t virtual_rows, hipStream_t stream) {
   const int n = a.chunk_len;
   const dim3 grid((unsigned)virtual_rows);
-  if (virtual_rows >= 1024 && n <= 256 * 16) {
-    // Many short rows: 256-thread workgroups, four per CU.
+  if (virtual_rows >= 1024 && n <= 256 * 16 && (!a.sorted || a.k <= kSmallCap)) {
+    // Many short rows: 256-thread workgroups with a small candidate buffer
+    // (about 17 KB of LDS), eight per CU.
     const dim3 block(256);
-    if (n <= 256 * 4) hipLaunchKernelGGL((topk_kernel<256, 4>), grid, block, 0, stream, a);
-    else if (n <= 256 * 8) hipLaunchKernelGGL((topk_kernel<256, 8>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((topk_kernel<256, 16>), grid, block, 0, stream, a);
+    if (n <= 256 * 4) hipLaunchKernelGGL((topk_kernel<256, 4, kSmallCap>), grid, block, 0, stream, a);
+    else if (n <= 256 * 8) hipLaunchKernelGGL((topk_kernel<256, 8, kSmallCap>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((topk_kernel<256, 16, kSmallCap>), grid, block, 0, stream, a);
     return check_launch("topk_kernel");
   }
   const dim3 block(kTopkThreads);
-  if (n <= kTopkThreads * 4) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 4>), grid, block, 0, stream, a);
-  else if (n <= kTopkThreads * 8) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 8>), grid, block, 0, stream, a);
-  else if (n <= kTopkThreads * 16) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 16>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((topk_kernel<kTopkThreads, 32>), grid, block, 0, stream, a);
+  if (n <= kTopkThreads * 4) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 4, kMaxK>), grid, block, 0, stream, a);
+  else if (n <= kTopkThreads * 8) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 8, kMaxK>), grid, block, 0, stream, a);
+  else if (n <= kTopkThreads * 16) hipLaunchKernelGGL((topk_kernel<kTopkThreads, 16, kMaxK>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((topk_kernel<kTopkThreads, 32, kMaxK>), grid, block, 0, stream, a);
   return check_launch("topk_kernel");
 }
 

@@ -46,10 +46,12 @@ def test_topk_matches_oracle(device, kind, length, k) -> None:
 
 
 @pytest.mark.parametrize("kind", ["normal", "ties", "zeros", "neginf"])
-@pytest.mark.parametrize("length,k", [(300, 17), (2048, 256), (4096, 512)])
+@pytest.mark.parametrize("length,k", [(300, 17), (2048, 256), (4096, 512), (4096, 2048)])
 def test_many_short_rows(device, kind, length, k) -> None:
-    # Enough rows of at most 4096 entries for the 256-thread workgroups; every
-    # row checked, with ragged row lengths on half of them.
+    # Enough rows of at most 4096 entries for the 256-thread workgroups (a
+    # sorted k above their 1024-entry candidate buffer takes the 1024-thread
+    # kernel); every row checked, values bit for bit, with ragged row lengths
+    # on half of them.
     print(f"topk many rows kind={kind} L={length} k={k}", flush=True)
     rows = 1536
     host = rows_for(kind, rows, length, seed=7 * length + k)
@@ -58,11 +60,17 @@ def test_many_short_rows(device, kind, length, k) -> None:
     x = torch.from_numpy(host).to(device)
     lens = torch.from_numpy(lengths).to(device)
     idx_sorted = metrics.topk(x, k, sorted=True, row_lengths=lens).cpu().numpy()
-    idx_index = metrics.topk(x, k, sorted=False, row_lengths=lens).cpu().numpy()
+    idx_index, val_index = metrics.topk(x, k, sorted=False, row_lengths=lens, return_values=True)
+    idx_index = idx_index.cpu().numpy()
+    val_bits = val_index.cpu().numpy().view(np.uint32)
     for r in range(rows):
         n = int(lengths[r])
         assert idx_sorted[r].tolist() == T.topk_sorted_padded(host[r], k, n).tolist(), r
-        assert idx_index[r].tolist() == T.topk_index_order(host[r], k, n).tolist(), r
+        want = T.topk_index_order(host[r], k, n)
+        assert idx_index[r].tolist() == want.tolist(), r
+        chosen = want >= 0
+        np.testing.assert_array_equal(val_bits[r][chosen], host[r][want[chosen]].view(np.uint32))
+        assert np.all(np.isneginf(val_index[r].cpu().numpy()[~chosen]))
 
 
 @pytest.mark.parametrize("kind", ["normal", "ties", "neginf"])
