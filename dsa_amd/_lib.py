@@ -91,6 +91,7 @@ _SIGNATURES: dict[str, list] = {
         _p,
     ],
     "dsa_project_rows": [_p, _i64, _i64, _p, _i32, _i64, _i64, _p, _i64, _p],
+    "dsa_project_rows_pair": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
     "dsa_dim_sketch": [_p, _i64, _i32, _i32, _p, _i32, _i32, _i32, ctypes.c_float, _p, _i32, _p],
     "dsa_abs_max": [_p, _i64, _i32, _p, _p],
     "dsa_fake_quantize": [_p, _i64, _i32, _i32, ctypes.c_float, _p, _p, _p],

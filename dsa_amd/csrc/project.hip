@@ -17,6 +17,10 @@
 // project_f32_kernel: weights_proj in fp32 (the reference runs it on
 // hidden.float()), one workgroup per output feature, 16 tokens per thread,
 // fp32 FMAs and a block reduction.
+//
+// project_pair_kernel: wq and weights_proj of one hidden batch in one launch
+// (the two grids side by side), each workgroup running the same code as in
+// its own kernel, so the outputs are identical.
 #include "common.hpp"
 #include "dsa_amd.h"
 #include "status.hpp"
@@ -35,15 +39,15 @@ __device__ __forceinline__ uint16_t to_bf16_bits(float x) {
   return (uint16_t)(u >> 16);
 }
 
-__global__ __launch_bounds__(256) void project_bf16_kernel(const uint16_t* hidden, int64_t hidden_stride, int tokens,
-                                                           const uint16_t* weight, int kdim, uint16_t* out,
-                                                           int64_t out_stride) {
-  __shared__ floatx4 part[kSplitK][64];
+// Output features [16 * block, 16 * block + 16) of the bf16 projection.
+__device__ __forceinline__ void project_bf16_block(const uint16_t* hidden, int64_t hidden_stride, int tokens,
+                                                   const uint16_t* weight, int kdim, uint16_t* out,
+                                                   int64_t out_stride, int block, floatx4 (&part)[kSplitK][64]) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = block * 16;
   const BufferRsrc w = make_buffer(weight + (size_t)n0 * kdim, 16u * (uint32_t)kdim * 2u);
   // hidden rows past `tokens` read as zeros (range-checked buffer)
   const uint32_t h_bytes = (uint32_t)((tokens - 1) * hidden_stride + kdim) * 2u;
@@ -81,12 +85,11 @@ __global__ __launch_bounds__(256) void project_bf16_kernel(const uint16_t* hidde
   }
 }
 
-__global__ __launch_bounds__(256) void project_f32_kernel(const uint16_t* hidden, int64_t hidden_stride, int tokens,
-                                                          const float* weight, int kdim, float* out,
-                                                          int64_t out_stride) {
-  __shared__ float partial[4][kMaxProjTokens];
+// Output feature n of the fp32 projection.
+__device__ __forceinline__ void project_f32_block(const uint16_t* hidden, int64_t hidden_stride, int tokens,
+                                                  const float* weight, int kdim, float* out, int64_t out_stride,
+                                                  int n, float (&partial)[4][kMaxProjTokens]) {
   const int tid = threadIdx.x;
-  const int n = blockIdx.x;
   const float* wrow = weight + (size_t)n * kdim;
   float acc[kMaxProjTokens];
 #pragma unroll
@@ -108,6 +111,35 @@ __global__ __launch_bounds__(256) void project_f32_kernel(const uint16_t* hidden
     for (int t = 0; t < kMaxProjTokens; ++t) partial[tid >> 6][t] = acc[t];
   __syncthreads();
   if (tid < tokens) out[(size_t)tid * out_stride + n] = (partial[0][tid] + partial[1][tid]) + (partial[2][tid] + partial[3][tid]);
+}
+
+__global__ __launch_bounds__(256) void project_bf16_kernel(const uint16_t* hidden, int64_t hidden_stride, int tokens,
+                                                           const uint16_t* weight, int kdim, uint16_t* out,
+                                                           int64_t out_stride) {
+  __shared__ floatx4 part[kSplitK][64];
+  project_bf16_block(hidden, hidden_stride, tokens, weight, kdim, out, out_stride, blockIdx.x, part);
+}
+
+__global__ __launch_bounds__(256) void project_f32_kernel(const uint16_t* hidden, int64_t hidden_stride, int tokens,
+                                                          const float* weight, int kdim, float* out,
+                                                          int64_t out_stride) {
+  __shared__ float partial[4][kMaxProjTokens];
+  project_f32_block(hidden, hidden_stride, tokens, weight, kdim, out, out_stride, blockIdx.x, partial);
+}
+
+// Both projections of one hidden batch in one grid: workgroups [0, bf16_blocks)
+// take the bf16 projection's 16-feature groups, the rest one fp32 feature each.
+__global__ __launch_bounds__(256) void project_pair_kernel(const uint16_t* hidden, int64_t hidden_stride, int tokens,
+                                                           int kdim, const uint16_t* weight_a, int bf16_blocks,
+                                                           uint16_t* out_a, int64_t out_a_stride,
+                                                           const float* weight_b, float* out_b, int64_t out_b_stride) {
+  __shared__ floatx4 part[kSplitK][64];
+  __shared__ float partial[4][kMaxProjTokens];
+  const int b = blockIdx.x;
+  if (b < bf16_blocks)
+    project_bf16_block(hidden, hidden_stride, tokens, weight_a, kdim, out_a, out_a_stride, b, part);
+  else
+    project_f32_block(hidden, hidden_stride, tokens, weight_b, kdim, out_b, out_b_stride, b - bf16_blocks, partial);
 }
 
 }  // namespace
@@ -143,4 +175,30 @@ extern "C" int dsa_project_rows(const void* hidden, int64_t hidden_stride, int64
   hipLaunchKernelGGL(project_f32_kernel, dim3((unsigned)features), dim3(256), 0, s, h, hidden_stride, (int)tokens,
                      static_cast<const float*>(weight), (int)kdim, static_cast<float*>(out), out_stride);
   return check_launch("project_f32_kernel");
+}
+
+extern "C" int dsa_project_rows_pair(const void* hidden, int64_t hidden_stride, int64_t tokens, int64_t kdim,
+                                     const void* weight_bf16, int64_t features_bf16, void* out_bf16,
+                                     int64_t out_bf16_stride, const float* weight_f32, int64_t features_f32,
+                                     float* out_f32, int64_t out_f32_stride, void* stream) {
+  DSA_REQUIRE(hidden && weight_bf16 && out_bf16 && weight_f32 && out_f32, "null pointer argument");
+  DSA_REQUIRE(tokens >= 1 && tokens <= kMaxProjTokens, "tokens %lld outside [1, 16]", (long long)tokens);
+  DSA_REQUIRE(kdim >= 32 && kdim % 32 == 0 && kdim <= (1 << 20), "kdim %lld must be a multiple of 32",
+              (long long)kdim);
+  DSA_REQUIRE(hidden_stride >= kdim && hidden_stride % 8 == 0, "hidden_stride must be >= kdim and a multiple of 8");
+  DSA_REQUIRE(features_bf16 >= 16 && features_bf16 % 16 == 0, "bf16 features %lld must be a multiple of 16",
+              (long long)features_bf16);
+  DSA_REQUIRE(features_f32 >= 1, "fp32 features out of range");
+  DSA_REQUIRE(features_bf16 / 16 + features_f32 <= 0x7fffffffLL, "too many features");
+  DSA_REQUIRE(out_bf16_stride >= features_bf16 && out_f32_stride >= features_f32, "output stride < features");
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(hidden) % 16 == 0 && reinterpret_cast<uintptr_t>(weight_bf16) % 16 == 0,
+              "hidden and weight must be 16-byte aligned");
+  DSA_REQUIRE((tokens - 1) * hidden_stride + kdim < (int64_t(1) << 30), "hidden too large");
+  DSA_REQUIRE(16 * kdim * 2 < (int64_t(1) << 31), "weight rows too long");
+  const int bf16_blocks = (int)(features_bf16 / 16);
+  hipLaunchKernelGGL(project_pair_kernel, dim3((unsigned)(bf16_blocks + features_f32)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(hidden), hidden_stride, (int)tokens,
+                     (int)kdim, static_cast<const uint16_t*>(weight_bf16), bf16_blocks, static_cast<uint16_t*>(out_bf16),
+                     out_bf16_stride, weight_f32, out_f32, out_f32_stride);
+  return check_launch("project_pair_kernel");
 }

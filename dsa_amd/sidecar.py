@@ -195,6 +195,30 @@ class LightningIndexerSidecar(nn.Module):
                   _lib.stream_of(flat))
         return out.reshape(*hidden.shape[:-1], features)
 
+    def _project_pair(self, hidden: torch.Tensor, weight: torch.Tensor, weight_f32: torch.Tensor):
+        """``(hidden @ weight.T, hidden.float() @ weight_f32.T)`` in one
+        launch (``dsa_project_rows_pair``) for a decode step that fits the
+        projection kernel, else ``None``; identical to two :meth:`_project`
+        calls."""
+
+        tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
+        kdim = hidden.shape[-1]
+        if not (0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0 and not torch.is_grad_enabled()
+                and weight.dtype == torch.bfloat16 and weight.shape[0] % 16 == 0 and weight_f32.dtype == torch.float32):
+            return None
+        flat = hidden.reshape(tokens, kdim)
+        if flat.stride(-1) != 1 or flat.stride(0) % 8 or flat.data_ptr() % 16:
+            flat = flat.contiguous()
+        w = weight.detach().contiguous()
+        wf = weight_f32.detach().contiguous()
+        out = torch.empty((tokens, w.shape[0]), device=hidden.device, dtype=torch.bfloat16)
+        out_f = torch.empty((tokens, wf.shape[0]), device=hidden.device, dtype=torch.float32)
+        _lib.call("dsa_project_rows_pair", _lib.ptr(flat), flat.stride(0), tokens, kdim, _lib.ptr(w), w.shape[0],
+                  _lib.ptr(out), w.shape[0], _lib.ptr(wf), wf.shape[0], _lib.ptr(out_f), wf.shape[0],
+                  _lib.stream_of(flat))
+        lead = hidden.shape[:-1]
+        return out.reshape(*lead, w.shape[0]), out_f.reshape(*lead, wf.shape[0])
+
     def encode_keys(
         self,
         hidden: torch.Tensor,
@@ -249,8 +273,12 @@ class LightningIndexerSidecar(nn.Module):
 
         if not hidden.is_cuda:
             raise ValueError("HIP kernels require GPU tensors")
-        proj = self._project(hidden, self.wq.weight)
-        proj_w = self._project(hidden, self.weights_proj.weight, fp32=True)
+        pair = self._project_pair(hidden, self.wq.weight, self.weights_proj.weight)
+        if pair is None:
+            proj = self._project(hidden, self.wq.weight)
+            proj_w = self._project(hidden, self.weights_proj.weight, fp32=True)
+        else:
+            proj, proj_w = pair
         tokens_shape = proj.shape[:-1]
         tokens = math.prod(tokens_shape)
         flat = proj.reshape(tokens, self.heads * self.head_dim).contiguous()

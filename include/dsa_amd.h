@@ -541,6 +541,17 @@ int dsa_rope(const void* x, void* out, const int64_t* positions, int64_t tokens,
 int dsa_project_rows(const void* hidden, int64_t hidden_stride, int64_t tokens, const void* weight,
                      int32_t weight_dtype, int64_t features, int64_t kdim, void* out, int64_t out_stride, void* stream);
 
+/* encode_queries' two projections of one hidden batch (sidecar.py:78-79:
+ * wq(hidden) and weights_proj(hidden.float())) in one launch: out_bf16 as
+ * dsa_project_rows with a bf16 weight [features_bf16][kdim], out_f32 as
+ * dsa_project_rows with an fp32 weight [features_f32][kdim]; the outputs are
+ * identical to the two separate calls.  The reference computes them as two
+ * Linear calls; the pairing saves a launch per decode step. */
+int dsa_project_rows_pair(const void* hidden, int64_t hidden_stride, int64_t tokens, int64_t kdim,
+                          const void* weight_bf16, int64_t features_bf16, void* out_bf16, int64_t out_bf16_stride,
+                          const float* weight_f32, int64_t features_f32, float* out_f32, int64_t out_f32_stride,
+                          void* stream);
+
 /* encode_keys after wk (sidecar.py:74-76 and 67-72): LayerNorm over dim
  * (fp32 weight/bias, biased variance, eps), then RoPE on the first rope_dim
  * dims, written to out row out_rows[t] (or t when out_rows is NULL) so that a

@@ -225,3 +225,23 @@ def test_decode_projection_kernel_matches_float64(device, tokens) -> None:
         np.testing.assert_allclose(got, want, rtol=2 ** -8, atol=1e-4 * np.abs(want).max())
     want_w = h64 @ module.weights_proj.weight.detach().float().cpu().numpy().astype(np.float64).T
     np.testing.assert_allclose(w, want_w, rtol=1e-5, atol=1e-6 * np.abs(want_w).max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens", [1, 5, 16])
+def test_paired_projection_matches_separate_calls(device, tokens) -> None:
+    """dsa_project_rows_pair (wq and weights_proj in one launch) gives the
+    same bits as the two dsa_project_rows calls, and encode_queries takes it."""
+
+    print(f"sidecar pair projection tokens={tokens}", flush=True)
+    torch.manual_seed(100 + tokens)
+    module = sidecar.LightningIndexerSidecar(hidden_size=2048).to(device=device, dtype=torch.bfloat16).eval()
+    module.weights_proj.to(torch.float32)
+    hidden = torch.randn(tokens, 2048, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        pair = module._project_pair(hidden, module.wq.weight, module.weights_proj.weight)
+        assert pair is not None
+        q = module._project(hidden, module.wq.weight)
+        w = module._project(hidden, module.weights_proj.weight, fp32=True)
+    assert torch.equal(pair[0].view(torch.int16), q.view(torch.int16))
+    assert torch.equal(pair[1].view(torch.int32), w.view(torch.int32))
