@@ -213,6 +213,39 @@ def stream_of(tensor: torch.Tensor) -> int:
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
 
+_workspace_cache: dict[tuple, torch.Tensor] = {}
+_workspace_lock = threading.Lock()
+
+
+def workspace(kind: str, device: torch.device, stream: int, need: int, *, zeroed: bool) -> torch.Tensor:
+    """A device workspace of at least ``need`` bytes shared by every call of
+    one ``kind`` on one stream (calls on a stream are ordered, so they never
+    overlap).
+
+    The entry points accept any workspace at least as large as they ask for,
+    so one buffer serves every shape.  It grows geometrically (at least
+    doubling), so a decode loop whose context grows by one key per step
+    reallocates O(log L) times instead of keeping a buffer per length.
+    ``zeroed`` buffers are zero-filled when allocated; the entry points that
+    need zeros there leave them zeroed after every call.
+    """
+
+    key = (kind, device.index, stream)
+    with _workspace_lock:
+        ws = _workspace_cache.get(key)
+        if ws is None or ws.numel() < need:
+            size = max(int(need), 256, 2 * ws.numel() if ws is not None else 0)
+            ws = (torch.zeros if zeroed else torch.empty)(size, device=device, dtype=torch.uint8)
+            _workspace_cache[key] = ws
+        return ws
+
+
+def workspace_count() -> int:
+    """Number of cached workspaces (one per kind, device and stream)."""
+
+    return len(_workspace_cache)
+
+
 def dtype_code(dtype: torch.dtype) -> int:
     try:
         return _TORCH_DTYPES[dtype]

@@ -4,7 +4,9 @@ Mirrors ``temporal_dsa.certified`` (reference ``src/temporal_dsa/certified.py``)
 for the two functions that feed pruning bounds: ``block_key_norms``
 (certified.py:51-62) and ``temporal_score_radius`` (certified.py:18-48).  The
 reference's float64 score oracle ``relu_index_score`` is a test oracle and
-lives in ``oracle/``.  Results are fp32 (the reference computes in float64).
+lives in ``oracle/``.  Both compute in float64 and return float64, as the
+reference does; the radius is rounded up so that it never falls below the
+reference's float64 value.
 """
 
 from __future__ import annotations
@@ -31,7 +33,7 @@ def block_key_norms(keys: torch.Tensor, block_size: int) -> torch.Tensor:
     tokens, heads, dim = keys.shape
     keys = keys.contiguous()
     blocks = (tokens + block_size - 1) // block_size
-    out = torch.empty((blocks, heads), device=keys.device, dtype=torch.float32)
+    out = torch.empty((blocks, heads), device=keys.device, dtype=torch.float64)
     if tokens == 0:
         return out
     _lib.call(
@@ -48,9 +50,11 @@ def temporal_score_radius(
     w_prev: torch.Tensor,
     block_key_norm: torch.Tensor,
 ) -> torch.Tensor:
-    """Certified |I_t - I_(t-1)| radius for every key block, fp32 ``[blocks]``.
+    """Certified |I_t - I_(t-1)| radius for every key block, float64 ``[blocks]``.
 
     radius_b = sum_h norm[b,h] * (|w_now-w_prev|_h ||q_prev,h|| + |w_now|_h ||q_now,h-q_prev,h||)
+    (reference certified.py:43-47), evaluated in float64 and scaled by
+    (1 + 2^-36) so that it is never below the reference's float64 value.
     """
 
     tensors = (q_now, q_prev, w_now, w_prev, block_key_norm)
@@ -63,12 +67,14 @@ def temporal_score_radius(
     if block_key_norm.ndim != 2 or block_key_norm.shape[1] != q_now.shape[0]:
         raise ValueError("block_key_norm must have shape [blocks,heads]")
     heads, dim = q_now.shape
-    f32 = [t.to(torch.float32).contiguous() for t in tensors]
-    out = torch.empty(block_key_norm.shape[0], device=q_now.device, dtype=torch.float32)
+    if heads > 1024 or dim + heads > 8188:
+        raise ValueError("temporal_score_radius supports heads <= 1024 and dim + heads <= 8188")
+    f64 = [t.to(torch.float64).contiguous() for t in tensors]
+    out = torch.empty(block_key_norm.shape[0], device=q_now.device, dtype=torch.float64)
     if out.numel() == 0:
         return out
     _lib.call(
-        "dsa_temporal_score_radius", *(_lib.ptr(t) for t in f32), block_key_norm.shape[0], heads,
+        "dsa_temporal_score_radius", *(_lib.ptr(t) for t in f64), block_key_norm.shape[0], heads,
         dim, _lib.ptr(out), _lib.stream_of(q_now),
     )
     return out

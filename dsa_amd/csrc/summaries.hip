@@ -38,10 +38,12 @@ __device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dty
   }
 }
 
-// One wave per (block, head).
+// One wave per (block, head).  Squares and sums are taken in float64 (the
+// reference works in float64), so the norm does not round below the float64
+// value by more than one rounding of the final sqrt.
 __global__ __launch_bounds__(256) void block_key_norms_kernel(const void* keys, int64_t tokens,
                                                               int heads, int dim, int bs,
-                                                              int dtype, float* out) {
+                                                              int dtype, double* out) {
   const int lane = threadIdx.x & 63;
   const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nb = (tokens + bs - 1) / bs;
@@ -50,47 +52,57 @@ __global__ __launch_bounds__(256) void block_key_norms_kernel(const void* keys, 
   const int head = (int)(wid % heads);
   const int64_t start = block * bs;
   const int64_t stop = min(tokens, start + bs);
-  float best = 0.f;
+  double best = 0.0;
   for (int64_t t = start; t < stop; ++t) {
     const int64_t row = (t * heads + head) * dim;
-    float acc = 0.f;
+    double acc = 0.0;
     for (int d = lane; d < dim; d += kWave) {
-      const float x = load_as_float(keys, row + d, dtype);
-      acc = fmaf(x, x, acc);
+      const double x = load_as_float(keys, row + d, dtype);
+      acc = fma(x, x, acc);
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-    best = fmaxf(best, sqrtf(acc));
+    best = fmax(best, sqrt(acc));
   }
   if (lane == 0) out[block * heads + head] = best;
 }
 
 constexpr int kMaxRadiusHeads = 1024;
 
-__global__ __launch_bounds__(256) void temporal_radius_kernel(const float* q_now,
-                                                              const float* q_prev,
-                                                              const float* w_now,
-                                                              const float* w_prev,
-                                                              const float* norms, int64_t blocks,
-                                                              int heads, int dim, float* out) {
-  __shared__ float coef[kMaxRadiusHeads];
+// Relative rounding allowance of the radius.  Any float64 evaluation of the
+// formula (numpy's norm and matrix product included) is within about
+// (dim + heads + 4) * 2^-53 of the exact value, so two of them differ by less
+// than 2^-38 when dim + heads <= 8188 (the entry point's limit); scaling the
+// result by (1 + 2^-36) keeps it at or above the reference's float64 value.
+constexpr int kMaxRadiusTerms = 8188;
+constexpr double kRadiusRoundUp = 1.0 + 0x1p-36;
+
+// Per head: c_h = |w_now - w_prev| ||q_prev,h|| + |w_now| ||q_now,h - q_prev,h||
+// (certified.py:43-47), then out[b] = sum_h norm[b, h] * c_h, all in float64.
+__global__ __launch_bounds__(256) void temporal_radius_kernel(const double* q_now,
+                                                              const double* q_prev,
+                                                              const double* w_now,
+                                                              const double* w_prev,
+                                                              const double* norms, int64_t blocks,
+                                                              int heads, int dim, double* out) {
+  __shared__ double coef[kMaxRadiusHeads];
   for (int h = threadIdx.x; h < heads; h += blockDim.x) {
-    float prev_sq = 0.f;
-    float diff_sq = 0.f;
+    double prev_sq = 0.0;
+    double diff_sq = 0.0;
     for (int d = 0; d < dim; ++d) {
-      const float p = q_prev[h * dim + d];
-      const float c = q_now[h * dim + d];
-      prev_sq = fmaf(p, p, prev_sq);
-      diff_sq = fmaf(c - p, c - p, diff_sq);
+      const double p = q_prev[(int64_t)h * dim + d];
+      const double c = q_now[(int64_t)h * dim + d];
+      prev_sq = fma(p, p, prev_sq);
+      diff_sq = fma(c - p, c - p, diff_sq);
     }
-    coef[h] = fabsf(w_now[h] - w_prev[h]) * sqrtf(prev_sq) + fabsf(w_now[h]) * sqrtf(diff_sq);
+    coef[h] = fabs(w_now[h] - w_prev[h]) * sqrt(prev_sq) + fabs(w_now[h]) * sqrt(diff_sq);
   }
   __syncthreads();
   for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < blocks;
        b += (int64_t)gridDim.x * blockDim.x) {
-    float r = 0.f;
-    for (int h = 0; h < heads; ++h) r = fmaf(norms[b * heads + h], coef[h], r);
-    out[b] = r;
+    double r = 0.0;
+    for (int h = 0; h < heads; ++h) r = fma(norms[b * heads + h], coef[h], r);
+    out[b] = r * kRadiusRoundUp;
   }
 }
 
@@ -114,7 +126,7 @@ extern "C" int dsa_block_max(const float* scores, int64_t rows, int64_t length,
 }
 
 extern "C" int dsa_block_key_norms(const void* keys, int64_t tokens, int64_t heads, int64_t dim,
-                                   int32_t block_size, int32_t key_dtype, float* out,
+                                   int32_t block_size, int32_t key_dtype, double* out,
                                    void* stream) {
   DSA_REQUIRE(keys && out, "null pointer argument");
   DSA_REQUIRE(tokens > 0 && heads > 0 && dim > 0, "bad shape");
@@ -128,12 +140,13 @@ extern "C" int dsa_block_key_norms(const void* keys, int64_t tokens, int64_t hea
   return check_launch("block_key_norms_kernel");
 }
 
-extern "C" int dsa_temporal_score_radius(const float* q_now, const float* q_prev,
-                                         const float* w_now, const float* w_prev,
-                                         const float* block_key_norm, int64_t blocks,
-                                         int64_t heads, int64_t dim, float* out, void* stream) {
+extern "C" int dsa_temporal_score_radius(const double* q_now, const double* q_prev,
+                                         const double* w_now, const double* w_prev,
+                                         const double* block_key_norm, int64_t blocks,
+                                         int64_t heads, int64_t dim, double* out, void* stream) {
   DSA_REQUIRE(q_now && q_prev && w_now && w_prev && block_key_norm && out, "null pointer");
   DSA_REQUIRE(blocks > 0 && heads > 0 && heads <= kMaxRadiusHeads && dim > 0, "bad shape");
+  DSA_REQUIRE(dim + heads <= kMaxRadiusTerms, "dim + heads must be at most %d", kMaxRadiusTerms);
   const int64_t want = (blocks + 255) / 256;
   const unsigned grid = (unsigned)(want < 1024 ? want : 1024);
   hipLaunchKernelGGL(temporal_radius_kernel, dim3(grid), dim3(256), 0,

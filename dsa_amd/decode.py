@@ -12,29 +12,20 @@ sequence in ascending index order.
 from __future__ import annotations
 
 import math
-import threading
 
 import torch
 
 from . import _lib
 from .progressive_kernel import HEAD_DIM, HEADS
 
-_workspaces: dict[tuple, torch.Tensor] = {}
-_lock = threading.Lock()
-
 
 def _workspace(device: torch.device, stream: int, batch: int, length: int) -> torch.Tensor:
-    """Zero-initialised workspace reused by calls on one stream (each call
-    leaves it ready for the next; calls on one stream are ordered)."""
+    """Zero-initialised workspace shared by calls on one stream: each call
+    leaves its histogram zeroed for the next, and calls on a stream are
+    ordered.  One buffer, grown geometrically, serves every shape."""
 
-    key = (device.index, stream, batch, length)
-    with _lock:
-        ws = _workspaces.get(key)
-        if ws is None:
-            need = int(_lib.query("dsa_score_topk_workspace_bytes", batch, length))
-            ws = torch.zeros(need, device=device, dtype=torch.uint8)
-            _workspaces[key] = ws
-        return ws
+    need = int(_lib.query("dsa_score_topk_workspace_bytes", batch, length))
+    return _lib.workspace("score_topk", device, stream, need, zeroed=True)
 
 
 def indexer_topk(

@@ -73,6 +73,10 @@ def topk(
         from .decode import _workspace
 
         matrix = matrix.contiguous()
+        if matrix.data_ptr() % 16:
+            # A contiguous slice that starts mid-row (x[1:3] with L % 4 != 0)
+            # is not 16-byte aligned, as the distributed kernels need.
+            matrix = matrix.clone()
         workspace = _workspace(matrix.device, stream, rows, length)
         _lib.call(
             "dsa_topk_distributed", _lib.ptr(matrix), rows, length, k, _lib.ptr(indices), _lib.ptr(values),

@@ -25,7 +25,6 @@ reference's schedule is ``wave=1``).
 from __future__ import annotations
 
 import math
-import threading
 from dataclasses import asdict, dataclass
 
 import numpy as np
@@ -47,8 +46,6 @@ SWEEP_VARIANTS = (
 )
 CALIBRATED_VARIANTS = SWEEP_VARIANTS[:5]
 
-_workspaces: dict[tuple, torch.Tensor] = {}
-_lock = threading.Lock()
 
 
 @dataclass(frozen=True)
@@ -84,15 +81,9 @@ class ReplayResult:
     net_byte_reduction: float
 
 
-def _workspace(device, rows, length, k, block_size) -> torch.Tensor:
-    key = (device.index, rows, length, k, block_size)
-    with _lock:
-        ws = _workspaces.get(key)
-        if ws is None:
-            need = int(_lib.query("dsa_temporal_workspace_bytes", rows, length, k, block_size))
-            ws = torch.empty(need, device=device, dtype=torch.uint8)
-            _workspaces[key] = ws
-        return ws
+def _workspace(device, stream, rows, length, k, block_size) -> torch.Tensor:
+    need = int(_lib.query("dsa_temporal_workspace_bytes", rows, length, k, block_size))
+    return _lib.workspace("temporal", device, stream, need, zeroed=False)
 
 
 def _schedule(method: str, order: str) -> tuple[str, bool, bool]:
@@ -150,7 +141,7 @@ class _Transition:
         order_out = torch.empty((rows, self.blocks), device=dev, dtype=torch.int32)
         top = torch.empty((rows, self.k), device=dev, dtype=torch.int64)
         qk = torch.empty(rows, device=dev, dtype=torch.int32)
-        ws = _workspace(dev, rows, self.length, self.k, self.bs)
+        ws = _workspace(dev, _lib.stream_of(self.current), rows, self.length, self.k, self.bs)
         _lib.call(
             "dsa_temporal_replay_step", _lib.ptr(self.current), 0, _lib.ptr(bound_rows), prev_length,
             _lib.ptr(seeds), _lib.ptr(g), _lib.ptr(key_rows), _lib.ptr(scores), _lib.ptr(kept), _lib.ptr(order_out), _lib.ptr(top),

@@ -180,7 +180,11 @@ class LightningIndexerSidecar(nn.Module):
 
         tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
         kdim = hidden.shape[-1]
-        fits = (0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0 and not torch.is_grad_enabled()
+        # The projection kernel takes no weight width: a weight that is not
+        # [features, kdim] goes to F.linear, which raises its shape error on
+        # the host before anything is launched.
+        fits = (hidden.is_cuda and 0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0
+                and not torch.is_grad_enabled() and weight.ndim == 2 and weight.shape[1] == kdim
                 and (weight.dtype == torch.float32 if fp32 else (weight.dtype == torch.bfloat16 and weight.shape[0] % 16 == 0)))
         if not fits:
             return F.linear(hidden.float(), weight.float()) if fp32 else F.linear(hidden, weight)
@@ -203,7 +207,9 @@ class LightningIndexerSidecar(nn.Module):
 
         tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
         kdim = hidden.shape[-1]
-        if not (0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0 and not torch.is_grad_enabled()
+        if not (hidden.is_cuda and 0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0
+                and not torch.is_grad_enabled()
+                and weight.ndim == 2 and weight.shape[1] == kdim and weight_f32.ndim == 2 and weight_f32.shape[1] == kdim
                 and weight.dtype == torch.bfloat16 and weight.shape[0] % 16 == 0 and weight_f32.dtype == torch.float32):
             return None
         flat = hidden.reshape(tokens, kdim)

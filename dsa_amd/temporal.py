@@ -21,7 +21,6 @@ replay.py:562-590): a live step cannot use the current step's score drift.
 from __future__ import annotations
 
 import math
-import threading
 from dataclasses import dataclass
 
 import torch
@@ -32,9 +31,6 @@ from .progressive_kernel import HEAD_DIM, HEADS
 BLOCK_SIZES = (16, 32, 64, 128)
 SCAN_ORDERS = {"address": 0, "previous_hot": 1, "upper_hot": 2}
 METHODS = ("static", "static_hot_first", "dynamic")
-
-_workspaces: dict[tuple, torch.Tensor] = {}
-_lock = threading.Lock()
 
 
 @dataclass
@@ -48,14 +44,11 @@ class TemporalStep:
 
 
 def _workspace(device, stream, batch, length, k, block_size) -> torch.Tensor:
-    key = (device.index, stream, batch, length, k, block_size)
-    with _lock:
-        ws = _workspaces.get(key)
-        if ws is None:
-            need = int(_lib.query("dsa_temporal_workspace_bytes", batch, length, k, block_size))
-            ws = torch.empty(need, device=device, dtype=torch.uint8)
-            _workspaces[key] = ws
-        return ws
+    """Workspace shared by the temporal, own-trajectory and verifier steps on
+    one stream (no zero-fill needed: the steps clear what they use)."""
+
+    need = int(_lib.query("dsa_temporal_workspace_bytes", batch, length, k, block_size))
+    return _lib.workspace("temporal", device, stream, need, zeroed=False)
 
 
 def temporal_step(

@@ -506,16 +506,20 @@ int dsa_block_max(const float* scores, int64_t rows, int64_t length, int64_t row
 
 /* Per-block maximum key L2 norm (certified.py:51-62 block_key_norms) for keys
  * [tokens, heads, dim] (heads = 1 for the shared-key layout):
- * out[b, h] = max over tokens of the block of ||keys[t, h, :]||, fp32. */
+ * out[b, h] = max over tokens of the block of ||keys[t, h, :]||, float64
+ * (sums of squares in float64, as the reference computes them). */
 int dsa_block_key_norms(const void* keys, int64_t tokens, int64_t heads, int64_t dim,
-                        int32_t block_size, int32_t key_dtype, float* out, void* stream);
+                        int32_t block_size, int32_t key_dtype, double* out, void* stream);
 
 /* Certified temporal radius (certified.py:18-48 temporal_score_radius):
  * out[b] = sum_h block_key_norm[b, h] * (|w_now-w_prev|_h ||q_prev,h|| +
- * |w_now|_h ||q_now,h - q_prev,h||).  q: [heads, dim] fp32, w: [heads] fp32. */
-int dsa_temporal_score_radius(const float* q_now, const float* q_prev, const float* w_now,
-                              const float* w_prev, const float* block_key_norm, int64_t blocks,
-                              int64_t heads, int64_t dim, float* out, void* stream);
+ * |w_now|_h ||q_now,h - q_prev,h||), everything float64 (q: [heads, dim],
+ * w: [heads], norms: [blocks, heads]).  The result is scaled by (1 + 2^-36)
+ * so that it never falls below the reference's float64 value; requires
+ * heads <= 1024 and dim + heads <= 8188. */
+int dsa_temporal_score_radius(const double* q_now, const double* q_prev, const double* w_now,
+                              const double* w_prev, const double* block_key_norm, int64_t blocks,
+                              int64_t heads, int64_t dim, double* out, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sidecar encoder epilogues (sidecar.py:10-88).  The projections wq / wk /

@@ -64,9 +64,29 @@ def to_device_policy(policy: A.ApproxPolicy, gamma: float) -> approx.ApproxPolic
 
 @pytest.mark.parametrize("policy,block,wave,gamma_sigma", POLICIES, ids=[p[0].name for p in POLICIES])
 def test_approx_step_matches_oracle_trajectory(device, policy, block, wave, gamma_sigma) -> None:
-    batch, length, steps, k = 2, 4000, 6, 256
-    print(f"approx {policy.name} bs={block} wave={wave} gamma={gamma_sigma}sigma", flush=True)
-    qs, w, keys = trajectory(batch, length, steps, seed=block + 17 * wave)
+    run_trajectory(device, policy, block, wave, gamma_sigma, batch=2, length=4000, steps=6, k=256,
+                   seed=block + 17 * wave)
+
+
+C3_POLICIES = [
+    (A.ApproxPolicy(name="c3_dynamic_previous_max", dynamic_threshold=True, order="previous_max", cold_streak=0),
+     64, 4, -0.3),
+    (A.ApproxPolicy(name="c3_ema_bucket8", dynamic_threshold=True, order="bucket8", risk_model="ema", ema_alpha=0.9,
+                    volatility_lambda=2.0, age_cap=8, cold_streak=0), 32, 16, -0.3),
+]
+
+
+@pytest.mark.parametrize("policy,block,wave,gamma_sigma", C3_POLICIES, ids=[p[0].name for p in C3_POLICIES])
+def test_approx_step_c3_shape_trajectory(device, policy, block, wave, gamma_sigma) -> None:
+    # The C3 replay shape: B=4 sequences from L=16384, K=2048, 20 own-trajectory
+    # steps with the state carried on the device from step 0.
+    run_trajectory(device, policy, block, wave, gamma_sigma, batch=4, length=16384, steps=20, k=2048, seed=4242)
+
+
+def run_trajectory(device, policy, block, wave, gamma_sigma, *, batch, length, steps, k, seed) -> None:
+    print(f"approx {policy.name} bs={block} wave={wave} gamma={gamma_sigma}sigma B={batch} L={length} "
+          f"steps={steps} k={k}", flush=True)
+    qs, w, keys = trajectory(batch, length, steps, seed=seed)
     w, keys = w.to(device), keys.to(device)
     _, scores0 = decode.indexer_topk(qs[0].to(device), w, keys[:, :length].contiguous(), k, return_scores=True)
     gamma = float(gamma_sigma * scores0.std())

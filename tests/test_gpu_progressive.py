@@ -77,6 +77,15 @@ def test_compact_output_matches_dense_candidates(device) -> None:
     torch.testing.assert_close(compact.scores[order], dense.scores[indices])
 
 
+def block_tolerance(scale: np.ndarray, block_size: int) -> np.ndarray:
+    """Largest per-key score tolerance (1e-5 * S + 1e-6) of each block."""
+
+    blocks = math.ceil(scale.size / block_size)
+    padded = np.zeros(blocks * block_size)
+    padded[: scale.size] = scale
+    return 1e-5 * padded.reshape(blocks, block_size).max(axis=1) + 1e-6
+
+
 @pytest.mark.parametrize("block_size", [16, 32, 64, 128])
 @pytest.mark.parametrize("length", [100, 1000])
 def test_kernels_match_oracle_semantics(device, block_size, length) -> None:
@@ -110,6 +119,12 @@ def test_kernels_match_oracle_semantics(device, block_size, length) -> None:
     assert np.all(np.abs(got_part[fin] - h8_part[fin]) <= 1e-5 * scale[fin] + 1e-6)
     got_max = maxima.cpu().double().numpy()
     assert np.array_equal(np.isneginf(got_max), np.isneginf(h8_max))
+    # Block maxima (reference progressive_kernel.py:246): a maximum moves by at
+    # most its block's largest per-key error, so each finite maximum is held
+    # to the largest key tolerance of its block.
+    tol = block_tolerance(scale, block_size)
+    fin_b = np.isfinite(h8_max)
+    assert np.all(np.abs(got_max[fin_b] - h8_max[fin_b]) <= tol[fin_b]), "h8 block maxima"
 
     result = progressive_scores_triton(dq, dw, dk, selected, direct, threshold, block_size=block_size)
     assert result.accepted_blocks.cpu().bool().numpy().tolist() == ref_acc.tolist()
@@ -119,6 +134,10 @@ def test_kernels_match_oracle_semantics(device, block_size, length) -> None:
     assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * scale[fin] + 1e-6)
     bm = result.block_max.cpu().double().numpy()
     assert np.array_equal(np.isneginf(bm), np.isneginf(ref_max))
+    # ProgressiveResult.block_max (reference progressive_kernel.py:334): the H8
+    # maximum of every screened block, -inf for direct blocks.
+    fin_b = np.isfinite(ref_max)
+    assert np.all(np.abs(bm[fin_b] - ref_max[fin_b]) <= tol[fin_b]), "progressive block_max"
 
     masked = masked_full_scores_triton(dq, dw, dk, result.accepted_blocks, block_size=block_size).cpu().double().numpy()
     ref_masked = S.kernel_masked_full(qn, wn, kn, ref_acc, block_size)
@@ -132,14 +151,13 @@ def test_kernels_match_oracle_semantics(device, block_size, length) -> None:
     assert torch.equal(compact.scores.cpu(), result.scores.cpu()[idx])
 
 
-@pytest.mark.parametrize("block_size", [16, 64, 128])
-def test_fp8_keys_match_oracle_on_dequantised_keys(device, block_size) -> None:
+@pytest.mark.parametrize("block_size,length", [(16, 1000), (64, 1000), (128, 1000), (64, 131072)])
+def test_fp8_keys_match_oracle_on_dequantised_keys(device, block_size, length) -> None:
     # fp8 e4m3fn keys with one fp32 scale per 128 keys: every kernel's scores
     # (partial or full) equal the oracle's on the dequantised keys, since the
-    # ReLU commutes with a non-negative scale.
-    print(f"progressive fp8 bs={block_size}", flush=True)
-    length = 1000
-    gen = torch.Generator().manual_seed(7 * block_size)
+    # ReLU commutes with a non-negative scale.  131072 keys is the C5 length.
+    print(f"progressive fp8 bs={block_size} L={length}", flush=True)
+    gen = torch.Generator().manual_seed(7 * block_size + length)
     q = (torch.randn(64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
     w = torch.randn(64, generator=gen) / 8
     raw = torch.randn(length, 128, generator=gen)
@@ -151,14 +169,30 @@ def test_fp8_keys_match_oracle_on_dequantised_keys(device, block_size) -> None:
     direct = torch.rand(blocks, generator=gen) < 0.3
     selected, remaining = split_head_ids(dynamic_head_ids(w))
     qn, wn = q.float().numpy(), w.numpy()
-    _, h8_max = S.kernel_h8_block_max(qn, wn, deq, selected.numpy(), (~direct).numpy(), block_size)
+    h8_part, h8_max = S.kernel_h8_block_max(qn, wn, deq, selected.numpy(), (~direct).numpy(), block_size)
     finite = np.sort(h8_max[np.isfinite(h8_max)])
-    i = finite.size // 2 - 1
+    # A threshold in the widest gap between adjacent maxima near the median,
+    # so that fp32-vs-float64 rounding cannot flip a promotion decision.
+    mid = finite.size // 2
+    lo = max(0, mid - 32)
+    i = lo + int(np.argmax(np.diff(finite[lo : mid + 32])))
     threshold = float(0.5 * (finite[i] + finite[i + 1]))
     assert finite[i + 1] - finite[i] > 1e-4 * max(1.0, abs(threshold))
-    ref, ref_acc, _ = S.kernel_progressive(qn, wn, deq, selected.numpy(), remaining.numpy(), direct.numpy(), threshold, block_size)
+    ref, ref_acc, ref_max = S.kernel_progressive(qn, wn, deq, selected.numpy(), remaining.numpy(), direct.numpy(),
+                                                 threshold, block_size)
     scale = S.abs_weight_scale(qn, deq, wn)
+    tol = block_tolerance(scale, block_size)
     dq, dw, dk, ds = q.to(device), w.to(device), k8.to(device), scales.to(device)
+
+    part, maxima = h8_block_max_triton(dq, dw, dk, selected, ~direct, block_size=block_size, key_scales=ds)
+    got_part = part.cpu().double().numpy()
+    assert np.array_equal(np.isneginf(got_part), np.isneginf(h8_part))
+    fin = np.isfinite(h8_part)
+    assert np.all(np.abs(got_part[fin] - h8_part[fin]) <= 1e-5 * scale[fin] + 1e-6)
+    got_max = maxima.cpu().double().numpy()
+    fin_b = np.isfinite(h8_max)
+    assert np.array_equal(np.isneginf(got_max), ~fin_b)
+    assert np.all(np.abs(got_max[fin_b] - h8_max[fin_b]) <= tol[fin_b]), "fp8 h8 block maxima"
 
     full = full_scores_triton(dq, dw, dk, key_scales=ds).cpu().double().numpy()
     ref_full = S.relu_index_score(qn, deq, wn)
@@ -169,6 +203,10 @@ def test_fp8_keys_match_oracle_on_dequantised_keys(device, block_size) -> None:
     assert np.array_equal(np.isneginf(got), np.isneginf(ref))
     fin = np.isfinite(ref)
     assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * scale[fin] + 1e-6)
+    bm = result.block_max.cpu().double().numpy()
+    fin_b = np.isfinite(ref_max)
+    assert np.array_equal(np.isneginf(bm), ~fin_b)
+    assert np.all(np.abs(bm[fin_b] - ref_max[fin_b]) <= tol[fin_b]), "fp8 progressive block_max"
     two = two_pass_scores_triton(dq, dw, dk, selected, direct, threshold, block_size=block_size, key_scales=ds)
     assert torch.equal(two.accepted_blocks.cpu(), result.accepted_blocks.cpu())
     torch.testing.assert_close(two.scores.cpu(), result.scores.cpu(), rtol=1e-6, atol=1e-6)

@@ -85,3 +85,36 @@ def test_stable_topk_rejects_values_float32_cannot_hold() -> None:
     # them would create a tie the reference does not have.
     with pytest.raises(ValueError, match="float32"):
         metrics.stable_topk(np.array([1.0 + 2.0**-30, 1.0, 0.5]), 1)
+
+
+def test_workspace_cache_grows_geometrically() -> None:
+    # A decode loop whose context grows by one key per step must not keep a
+    # workspace per length: the shared buffer at least doubles when it grows,
+    # so 64 steps from L=16384 reallocate O(log L) times at most.
+    from dsa_amd import _lib
+
+    cpu = torch.device("cpu")
+    allocations = 0
+    last = None
+    for step in range(64):
+        need = 1000 * (16384 + step)
+        ws = _lib.workspace("test_growth", cpu, 0, need, zeroed=True)
+        assert ws.numel() >= need
+        if ws is not last:
+            allocations += 1
+            assert not ws.any()
+            last = ws
+    assert allocations <= 2
+    big = _lib.workspace("test_growth", cpu, 0, 10**6, zeroed=False)
+    assert big is last  # a smaller request reuses the buffer
+
+
+def test_projection_width_mismatch_raises_on_the_host() -> None:
+    # The HIP projection kernel takes no weight width, so a hidden state whose
+    # width differs from the weight's must never reach it: F.linear raises.
+    module = sidecar.LightningIndexerSidecar(hidden_size=64, heads=4, head_dim=32, rope_dim=8).to(torch.bfloat16)
+    hidden = torch.zeros(2, 96, dtype=torch.bfloat16)
+    with torch.no_grad(), pytest.raises(RuntimeError):
+        module._project(hidden, module.wq.weight)
+    with torch.no_grad():
+        assert module._project_pair(hidden, module.wq.weight, module.weights_proj.weight.float()) is None

@@ -120,6 +120,25 @@ def test_radius_closed_forms() -> None:
     assert r.tolist() == [0.5 * 3.0 * 4.0]
 
 
+def test_radius_asymmetric_closed_form() -> None:
+    # Query and weight both change, ||q_now|| = 10 != ||q_prev|| = 5 and
+    # |w_now| = 2 != |w_prev| = 1.  certified.py:43-47 fixes the form
+    # |w_now - w_prev| ||q_prev|| + |w_now| ||q_now - q_prev|| = 3*5 + 2*5 = 25.
+    # The plausible slips give other values: ||q_now|| in the first term 40,
+    # |w_prev| in the second 20, both 35.
+    q_now, q_prev = np.array([[6.0, 8.0]]), np.array([[3.0, 4.0]])
+    w_now, w_prev = np.array([2.0]), np.array([-1.0])
+    r = temporal_score_radius(q_now, q_prev, w_now, w_prev, np.array([[2.0], [0.5]]))
+    assert r.tolist() == [50.0, 12.5]
+    # Two heads with different block norms: the per-head coefficients are
+    # weighted by their own head's norm (norms @ coefficients, not transposed).
+    q_now2 = np.array([[6.0, 8.0], [0.0, 1.0]])
+    q_prev2 = np.array([[3.0, 4.0], [0.0, 1.0]])
+    r2 = temporal_score_radius(q_now2, q_prev2, np.array([2.0, 4.0]), np.array([-1.0, 1.0]), np.array([[2.0, 10.0]]))
+    # head 0: 25 * 2; head 1: |4 - 1| * 1 + 4 * 0 = 3, * 10
+    assert r2.tolist() == [50.0 + 30.0]
+
+
 def test_block_key_norms_closed_form() -> None:
     keys = np.zeros((5, 2, 2))
     keys[0, 0] = [3, 4]  # norm 5
