@@ -217,20 +217,23 @@ _workspace_cache: dict[tuple, torch.Tensor] = {}
 _workspace_lock = threading.Lock()
 
 
-def workspace(kind: str, device: torch.device, stream: int, need: int, *, zeroed: bool) -> torch.Tensor:
+def workspace(kind: str, device: torch.device, stream: int, need: int, *, zeroed: bool, rows: int = 0) -> torch.Tensor:
     """A device workspace of at least ``need`` bytes shared by every call of
     one ``kind`` on one stream (calls on a stream are ordered, so they never
     overlap).
 
     The entry points accept any workspace at least as large as they ask for,
-    so one buffer serves every shape.  It grows geometrically (at least
+    so one buffer serves every length.  It grows geometrically (at least
     doubling), so a decode loop whose context grows by one key per step
     reallocates O(log L) times instead of keeping a buffer per length.
     ``zeroed`` buffers are zero-filled when allocated; the entry points that
-    need zeros there leave them zeroed after every call.
+    need zeros there (a per-row region at the start of the buffer) leave them
+    zeroed after every call.  That region grows with the row count, over
+    space that calls with fewer rows use for other data, so zeroed buffers
+    are also kept per ``rows``.
     """
 
-    key = (kind, device.index, stream)
+    key = (kind, device.index, stream, rows if zeroed else 0)
     with _workspace_lock:
         ws = _workspace_cache.get(key)
         if ws is None or ws.numel() < need:

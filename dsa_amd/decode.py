@@ -20,12 +20,13 @@ from .progressive_kernel import HEAD_DIM, HEADS
 
 
 def _workspace(device: torch.device, stream: int, batch: int, length: int) -> torch.Tensor:
-    """Zero-initialised workspace shared by calls on one stream: each call
-    leaves its histogram zeroed for the next, and calls on a stream are
-    ordered.  One buffer, grown geometrically, serves every shape."""
+    """Zero-initialised workspace shared by calls on one stream with the same
+    batch: each call leaves its histogram zeroed for the next, and calls on a
+    stream are ordered.  One buffer per batch, grown geometrically, serves
+    every length."""
 
     need = int(_lib.query("dsa_score_topk_workspace_bytes", batch, length))
-    return _lib.workspace("score_topk", device, stream, need, zeroed=True)
+    return _lib.workspace("score_topk", device, stream, need, zeroed=True, rows=batch)
 
 
 def indexer_topk(

@@ -118,3 +118,17 @@ def test_projection_width_mismatch_raises_on_the_host() -> None:
         module._project(hidden, module.wq.weight)
     with torch.no_grad():
         assert module._project_pair(hidden, module.wq.weight, module.weights_proj.weight.float()) is None
+
+
+def test_zeroed_workspaces_are_kept_per_row_count() -> None:
+    # A zeroed workspace's zero region (per-row histograms at offset 0) grows
+    # with the row count over space that calls with fewer rows use for other
+    # data, so a buffer is never shared between row counts.
+    from dsa_amd import _lib
+
+    cpu = torch.device("cpu")
+    small = _lib.workspace("test_rows", cpu, 0, 1000, zeroed=True, rows=3)
+    small.fill_(7)  # what a 3-row call leaves past its histograms
+    large = _lib.workspace("test_rows", cpu, 0, 1000, zeroed=True, rows=16)
+    assert large is not small and not large.any()
+    assert _lib.workspace("test_rows", cpu, 0, 1000, zeroed=True, rows=3) is small
