@@ -41,6 +41,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "dsa_route_heads": [_p, _i64, _i64, _i64, _i32, _p, _p, _p],
     "dsa_score_topk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
+    "dsa_score_topk_noalloc": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p],
     "dsa_score_hist": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "dsa_select_topk": [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
     "dsa_score_hist_timed": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p],

@@ -253,6 +253,23 @@ int dsa_score_topk(const void* queries, const float* weights, const void* keys,
                    int64_t k, int32_t key_dtype, int64_t* out_indices, float* out_values,
                    void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of dsa_score_topk.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as dsa_score_topk minus the workspace, which lives in
+ * a file-scope device array of DSA_NOALLOC_SCRATCH_BYTES per GPU, held from
+ * module load until the process ends.  Shapes whose workspace
+ * (dsa_score_topk_workspace_bytes(batch, length), about 8 bytes per key plus
+ * 16 KiB per row) exceeds it are rejected with DSA_STATUS_WORKSPACE_TOO_SMALL.
+ * Calls no hipMalloc/hipFree.  All calls on one GPU share that GPU's array:
+ * calls ordered on one stream are safe, calls that overlap on one GPU race.
+ * The pointers and the stream must belong to the current device. */
+#define DSA_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int dsa_score_topk_noalloc(const void* queries, const float* weights, const void* keys,
+                           const float* key_scales, float* scores, int64_t batch, int64_t length,
+                           int64_t k, int32_t key_dtype, int64_t* out_indices, float* out_values,
+                           void* stream);
+
 /* ------------------------------------------------------------------------
  * Temporal pruning of one decode step (seeded, bounded block scan).
  * Device counterpart of the reference's replay filter: replay.py:172-222
