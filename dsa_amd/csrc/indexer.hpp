@@ -33,6 +33,15 @@ struct KeysB16 {  // bf16 or fp16 rows, 256 B
     for (int c = 0; c < kRaw; ++c) raw[c] = buffer_load_16(rsrc, off + 64 * c);
   }
   __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) { return raw[j]; }
+  // Byte offset of the lane's slice of tile t inside a 64-key unit, and the
+  // loads of that slice through a resource whose base is the unit's first key.
+  __device__ static __forceinline__ uint32_t lane_offset(int t, int r, int g) {
+    return (uint32_t)(16 * t + r) * kRowBytes + 16u * g;
+  }
+  __device__ static __forceinline__ void load_at(BufferRsrc unit, uint32_t off, uint4 (&raw)[kRaw]) {
+#pragma unroll
+    for (int c = 0; c < kRaw; ++c) raw[c] = buffer_load_16(unit, off + 64 * c);
+  }
 };
 
 struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
@@ -58,6 +67,13 @@ struct KeysFP8 {  // fp8 e4m3fn rows, 128 B, one fp32 scale per 128 keys
   __device__ static __forceinline__ uint4 step(const uint4 (&raw)[kRaw], int j) {
     const uint4 v = raw[j >> 1];
     return fp8x8_to_bf16x8((j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y));
+  }
+  __device__ static __forceinline__ uint32_t lane_offset(int t, int r, int g) {
+    return (uint32_t)(16 * t + r) * kRowBytes + 32u * g;
+  }
+  __device__ static __forceinline__ void load_at(BufferRsrc unit, uint32_t off, uint4 (&raw)[kRaw]) {
+    raw[0] = buffer_load_16(unit, off);
+    raw[1] = buffer_load_16(unit, off + 16);
   }
 };
 

@@ -56,15 +56,37 @@ struct DenseArgs {
   int32_t list_quota;
 };
 
-// Keys past the valid range read as zeros (buffer bounds check).  Scaled
-// keys also fetch the unit's scale (a 64-key unit lies in one 128-key scale
-// block) with the keys, so the compute never waits on it.
+// The key rows a wave streams: the key set's base, its valid bytes (below
+// 2^31), and the lane's offsets of the four tiles of a unit (loop-invariant
+// registers).
 template <class KF>
-__device__ __forceinline__ void dense_load_unit(BufferRsrc keys, int u, int r, int g,
-                                                uint4 (&buf)[4][KF::kRaw], const float* scales, int L,
-                                                float& scale) {
+struct KeyStream {
+  const uint8_t* base;
+  uint32_t valid_bytes;
+  uint32_t loff[4];
+  __device__ __forceinline__ KeyStream(const uint8_t* b, uint32_t bytes, int r, int g) : base(b), valid_bytes(bytes) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) KF::load_buf(keys, u * 64 + 16 * t + r, g, buf[t]);
+    for (int t = 0; t < 4; ++t) loff[t] = KF::lane_offset(t, r, g);
+  }
+};
+
+// Each unit is loaded through its own buffer resource, based at the unit's
+// first key and bounded by the valid keys (keys past them read as zeros).
+// The resource is wave-uniform (scalar registers) and the lane offsets never
+// change, so no address register of the loop is ever a load destination: the
+// compiler then has no reason to drain the loads in flight at the loop head.
+// Scaled keys also fetch the unit's scale (a 64-key unit lies in one 128-key
+// scale block) with the keys, so the compute never waits on it.
+template <class KF>
+__device__ __forceinline__ void dense_load_unit(const KeyStream<KF>& ks, int u, uint4 (&buf)[4][KF::kRaw],
+                                                const float* scales, int L, float& scale) {
+  const uint32_t ub = (uint32_t)u * 64u * KF::kRowBytes;
+  // Signed difference and max, which stay scalar (an unsigned saturating
+  // subtract becomes a vector instruction, and with it the resource).
+  const int rem = max((int)ks.valid_bytes - (int)ub, 0);
+  const BufferRsrc unit = make_buffer(ks.base + ub, (uint32_t)rem);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) KF::load_at(unit, ks.loff[t], buf[t]);
   if constexpr (KF::kScaled) scale = scales[min(u * 64, L - 1) >> 7];
 }
 
@@ -93,7 +115,8 @@ __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], cons
 template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists>
 __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int u_first, int u_stride,
                                              int64_t seq, int valid, int L, int lane, int r, int g,
-                                             BufferRsrc keys, BufferRsrc out, const float* scales,
+                                             const uint8_t* key_base, uint32_t key_bytes, BufferRsrc out,
+                                             const float* scales,
                                              uint32_t* hist, float* chunk_scores, int chunk_base) {
   uint4 qa[M][4];
   float wr[M][4];
@@ -111,19 +134,24 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
   // hit), so no load is conditional and the compiler's vmcnt waits cover
   // exactly the buffer being consumed.
   constexpr int NB = KF::kBuffers;
+  const KeyStream<KF> ks(key_base, key_bytes, r, g);
   const int u_last = u_first + u_stride * (count - 1);
   uint4 buf[NB][4][KF::kRaw];
   float scale[NB] = {};
 #pragma unroll
   for (int s = 0; s < NB - 1; ++s)
-    dense_load_unit<KF>(keys, min(u_first + u_stride * s, u_last), r, g, buf[s], scales, L, scale[s]);
+    dense_load_unit<KF>(ks, min(u_first + u_stride * s, u_last), buf[s], scales, L, scale[s]);
   for (int i = 0; i < count; i += NB) {
     const int u = u_first + u_stride * i;
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
       if (i + s >= count) break;
-      dense_load_unit<KF>(keys, min(u + u_stride * (s + NB - 1), u_last), r, g, buf[(s + NB - 1) % NB], scales, L,
+      dense_load_unit<KF>(ks, min(u + u_stride * (s + NB - 1), u_last), buf[(s + NB - 1) % NB], scales, L,
                           scale[(s + NB - 1) % NB]);
+      // The next unit's loads stay ahead of this unit's MFMAs: left to
+      // itself the scheduler sinks them below the first unit's compute, so
+      // every wave would start with a unit whose latency nothing hides.
+      __builtin_amdgcn_sched_barrier(0);
       dense_compute_unit<Tag, KF, M, kHist, kLists>(qa, wr, buf[s], u + u_stride * s, valid, L, lane, g,
                                                     scale[s], out, hist, chunk_scores, chunk_base);
     }
@@ -191,8 +219,8 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
   if (a.causal_offset >= 0)
     valid = min(L, (int)(seq % a.queries_per_keyset) + a.causal_offset + 1);
 
-  const BufferRsrc keys =
-      make_buffer(a.keys + keyset * a.key_stride * KF::kRowBytes, (uint32_t)valid * KF::kRowBytes);
+  const uint8_t* key_base = a.keys + keyset * a.key_stride * KF::kRowBytes;
+  const uint32_t key_bytes = (uint32_t)valid * KF::kRowBytes;
   float* out_ptr = a.out + seq * a.out_stride;
   const BufferRsrc out = make_buffer(out_ptr, (uint32_t)L * 4u);
   const float* scales = KF::kScaled ? a.scales + keyset * a.scale_stride : nullptr;
@@ -217,7 +245,8 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
     const int chunk_base = chunk * chunk_keys;
     if (count > 0)
       dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g,
-                                                       keys, out, scales, hist, chunk_scores, chunk_base);
+                                                       key_base, key_bytes, out, scales, hist, chunk_scores,
+                                                       chunk_base);
     __syncthreads();
     if constexpr (kLists) {
       // The chunk's list: every valid key whose bin is at least the bin of
@@ -268,8 +297,8 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
     return;
   }
   if (count == 0) return;
-  dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, keys,
-                                                   out, scales, hist, chunk_scores, 0);
+  dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, key_base,
+                                                   key_bytes, out, scales, hist, chunk_scores, 0);
 }
 
 
