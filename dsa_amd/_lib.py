@@ -88,8 +88,8 @@ _SIGNATURES: dict[str, list] = {
         _i64, _i64, _i64, _i32, _i32, _p, _i64, _p,
     ],
     "dsa_approx_replay_step": [
-        _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64,
-        _p,
+        _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p,
+        _i64, _p,
     ],
     "dsa_project_rows": [_p, _i64, _i64, _p, _i32, _i64, _i64, _p, _i64, _p],
     "dsa_project_rows_pair": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
@@ -121,7 +121,7 @@ class ApproxPolicyC(ctypes.Structure):
         ("age_cap", _i32),
         ("recent_window", _i32),
         ("full_refresh", _i32),
-        ("reserved", _i32),
+        ("history", _i32),
     ]
 
 

@@ -247,7 +247,7 @@ def approx_step(
         age_cap=-1 if policy.age_cap is None else int(policy.age_cap),
         recent_window=int(policy.recent_window),
         full_refresh=int(full_refresh),
-        reserved=0,
+        history=0,
     )
     queries = queries.contiguous()
     weights = weights.to(torch.float32).contiguous()
@@ -269,13 +269,16 @@ def approx_step(
     return TemporalStep(topk, scores, evaluated.view(torch.bool), qk)
 
 
-def _policy_struct(policy: ApproxPolicy, full_refresh: bool) -> "_lib.ApproxPolicyC":
+HISTORY_MODES = {"own": 0, "teacher": 1}
+
+
+def _policy_struct(policy: ApproxPolicy, full_refresh: bool, history_mode: str = "own") -> "_lib.ApproxPolicyC":
     order, buckets = (3, 0) if policy.order == "oracle_current" else _order_code(policy.order)
     return _lib.ApproxPolicyC(
         gamma=float(policy.gamma), age_slope=float(policy.age_slope), ema_alpha=float(policy.ema_alpha),
         volatility_lambda=float(policy.volatility_lambda), risk_model=RISK_MODELS[policy.risk_model], order=order,
         buckets=buckets, cold_streak=int(policy.cold_streak), age_cap=-1 if policy.age_cap is None else int(policy.age_cap),
-        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), reserved=0,
+        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), history=HISTORY_MODES[history_mode],
     )
 
 
@@ -305,18 +308,19 @@ def replay_step(
     wave: int = 1,
 ):
     """One transition replayed over a recorded score row (reference
-    approx.py:129-364, ``history_mode="own"``): the pruning scan, the top-k of
-    the evaluated keys and the state update run in the HIP kernels with the
-    row as the score source; returns ``(state, metrics, details)`` with the
-    reference's metrics dict and details.  ``state`` (one sequence) is
-    advanced in place.  The teacher history needs the reference's dense
-    bookkeeping of every transition and stays with the reference.  The
-    ``oracle_current`` order is available here (the row is known)."""
+    approx.py:129-364): the pruning scan, the top-k of the evaluated keys and
+    the state update run in the HIP kernels with the row as the score source;
+    returns ``(state, metrics, details)`` with the reference's metrics dict
+    and details.  ``state`` (one sequence) is advanced in place.  With
+    ``history_mode="own"`` the scan is seeded by the previous step's own top-k
+    and only refreshed blocks update the state; with ``"teacher"`` it is
+    seeded by the previous dense top-k and every block's state is reset from
+    the dense row (approx.py:143-158,270-280).  The ``oracle_current`` order is
+    available here (the row is known)."""
 
     if history_mode not in {"own", "teacher"}:
         raise ValueError("history_mode must be 'own' or 'teacher'")
-    if history_mode == "teacher":
-        raise ValueError("the device replay runs history_mode='own'")
+    teacher = history_mode == "teacher"
     _lib.load()
     if state.topk.shape[0] != 1:
         raise ValueError("replay_step takes a one-sequence state")
@@ -333,9 +337,13 @@ def replay_step(
     cap_blocks = state.last_max.shape[1]
     if blocks > cap_blocks:
         raise ValueError(f"context of {length} keys exceeds the state's capacity of {cap_blocks} blocks")
-    seed_host = state.seed_order
-    if seed_host is None:  # right after initialize_state: its top-k in rank order
-        seed_host = state.baseline_topk[0].cpu().numpy() if state.baseline_topk is not None else state.topk[0].cpu().numpy()
+    if teacher:  # the previous step's dense top-k, in rank order
+        seed_host = (state.baseline_topk if state.baseline_topk is not None else state.topk)[0].cpu().numpy()
+    else:
+        seed_host = state.seed_order
+        if seed_host is None:  # right after initialize_state: its top-k in rank order
+            seed_host = (state.baseline_topk[0].cpu().numpy() if state.baseline_topk is not None
+                         else state.topk[0].cpu().numpy())
     seed_host = seed_host[seed_host < length].astype(np.int64)
     if seed_host.size != k or np.unique(seed_host).size != k:
         raise RuntimeError(f"previous Top-K seed has {seed_host.size} unique keys, expected {k}")
@@ -345,8 +353,12 @@ def replay_step(
                         or fallback)
     if policy.dynamic_threshold and wave < 1:
         raise ValueError("a dynamic policy needs wave >= 1")
-    pol = _policy_struct(policy, full_refresh)
+    pol = _policy_struct(policy, full_refresh, history_mode)
     row = torch.from_numpy(host).to(device).reshape(1, -1)
+    # The current dense top-k in rank order (baseline); the teacher's state
+    # update takes its blocks as the hot ones.
+    baseline_dev = device_topk(row, k, sorted=True)
+    seeds_dev = torch.from_numpy(seed_host).to(device).reshape(1, -1)
     scores = torch.empty((1, length), device=device, dtype=torch.float32)
     evaluated = torch.empty((1, blocks), device=device, dtype=torch.uint8)
     top = torch.empty((1, k), device=device, dtype=torch.int64)
@@ -359,12 +371,12 @@ def replay_step(
     _lib.call(
         "dsa_approx_replay_step", _lib.ptr(row), length, _lib.ptr(current_max), ctypes.addressof(pol), None,
         previous_length,
-        _lib.ptr(state.topk), _lib.ptr(state.last_max), _lib.ptr(state.ema), _lib.ptr(state.volatility),
+        _lib.ptr(seeds_dev), _lib.ptr(baseline_dev) if teacher else None, _lib.ptr(state.last_max), _lib.ptr(state.ema), _lib.ptr(state.volatility),
         _lib.ptr(state.age), _lib.ptr(state.cold_streak), cap_blocks, _lib.ptr(scores), _lib.ptr(evaluated),
         _lib.ptr(top), _lib.ptr(qk), 1, length, k, block_size, wave if policy.dynamic_threshold else 0, _lib.ptr(ws),
         ws.numel(), stream,
     )
-    baseline = device_topk(row, k, sorted=True)[0].cpu().numpy()
+    baseline = baseline_dev[0].cpu().numpy()
     scored = np.flatnonzero(np.isfinite(scores[0].cpu().numpy()))
     approximate = _rank_order(top[0].cpu().numpy(), host)
     refreshed = evaluated[0].cpu().numpy().astype(bool)
@@ -442,6 +454,6 @@ def replay_step(
     }
     state.topk = torch.from_numpy(approximate).to(device).reshape(1, -1)
     state.seed_order = approximate
-    state.baseline_topk = torch.from_numpy(baseline).to(device).reshape(1, -1)
+    state.baseline_topk = baseline_dev
     state.length = length
     return state, metrics, details

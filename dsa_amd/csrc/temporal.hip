@@ -532,8 +532,10 @@ __global__ __launch_bounds__(256) void temporal_hist_kernel(TemporalArgs a) {
   }
 }
 
+enum StateMode { kStateOwn = 0, kStateInit = 1, kStateTeacher = 2 };
+
 struct StateArgs {
-  const float* scores;     // [rows][score_stride]
+  const float* scores;     // [rows][score_stride]: the step's scores (dense for init / teacher)
   int64_t score_stride;
   const int64_t* topk;     // [rows][k]: the step's top-k (hot blocks)
   const uint8_t* evaluated;  // [rows][blocks]: refreshed blocks (update only)
@@ -542,17 +544,23 @@ struct StateArgs {
   int32_t length, blocks, block_size, k, state_blocks;
 };
 
-// kInit: initialize_state (approx.py:112-126) from a dense step.  Otherwise
-// the own-mode update after a step (approx.py:253-287): refreshed blocks take
-// the block max of the current scores (all of their keys were scored), EMA
-// and volatility move by ema_alpha (float64, stored as float32; the
-// volatility's second term and sum are float32, as numpy evaluates
-// `float * float32 scalar`), every other block keeps stale values and ages;
-// the cold streak restarts at blocks holding a top-k key.  In place: each
-// thread reads and writes only its own blocks.
-template <bool kInit>
+// kStateInit: initialize_state (approx.py:112-126) from a dense step.
+// kStateOwn: the own-mode update after a step (approx.py:253-287): refreshed
+// blocks take the block max of the current scores (all of their keys were
+// scored), EMA and volatility move by ema_alpha (float64, stored as float32;
+// the volatility's second term and sum are float32, as numpy evaluates
+// `float * float32 scalar`), every other block keeps stale values and ages.
+// kStateTeacher: the teacher-mode update (approx.py:270-274): every block
+// takes the dense row's block max as last max and EMA, volatility 0, age 0.
+// In both updates the cold streak restarts at blocks holding a key of
+// s.topk (the step's own top-k, or the dense top-k for the teacher) and
+// grows elsewhere.  In place: each thread reads and writes only its own
+// blocks.
+template <int kMode>
 __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
 #pragma clang fp contract(off)
+  constexpr bool kInit = kMode == kStateInit;
+  constexpr bool kTeacher = kMode == kStateTeacher;
   __shared__ uint8_t hot[kMaxTemporalBlocks];
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
@@ -569,7 +577,8 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
   const dsa_approx_policy& p = s.ap.p;
   for (int b = tid; b < nb; b += 1024) {
     const size_t at = (size_t)row * s.ap.stride + b;
-    const bool refresh = kInit || s.evaluated[(size_t)row * nb + b] || (s.rescued && s.rescued[(size_t)row * nb + b]);
+    const bool refresh =
+        kInit || kTeacher || s.evaluated[(size_t)row * nb + b] || (s.rescued && s.rescued[(size_t)row * nb + b]);
     float seen = -__builtin_inff();
     if (refresh) {
       const int end = min(s.length, (b + 1) * bs);
@@ -581,6 +590,13 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
       s.ap.vol[at] = 0.f;
       s.ap.age[at] = 0;
       s.ap.cold[at] = hot[b] ? 0 : 1;
+    } else if constexpr (kTeacher) {
+      const int cold = b < s.state_blocks ? (int)s.ap.cold[at] : 1;
+      s.ap.last_max[at] = seen;
+      s.ap.ema[at] = seen;
+      s.ap.vol[at] = 0.f;
+      s.ap.age[at] = 0;
+      s.ap.cold[at] = (int16_t)(hot[b] ? 0 : min(cold + 1, 32767));
     } else {
       const bool stored = b < s.state_blocks;
       float last = stored ? s.ap.last_max[at] : -__builtin_inff();
@@ -670,7 +686,15 @@ int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, 
   s.block_size = a.block_size;
   s.k = a.k;
   s.state_blocks = a.prev_blocks;
-  hipLaunchKernelGGL(approx_state_kernel<false>, dim3(a.rows), dim3(1024), 0, stream, s);
+  if (a.ap.p.history == DSA_HISTORY_TEACHER) {
+    // The teacher resets every block from the dense row (the recorded scores).
+    s.scores = a.source;
+    s.score_stride = a.source_stride;
+    s.topk = a.teacher_topk;
+    hipLaunchKernelGGL(approx_state_kernel<kStateTeacher>, dim3(a.rows), dim3(1024), 0, stream, s);
+  } else {
+    hipLaunchKernelGGL(approx_state_kernel<kStateOwn>, dim3(a.rows), dim3(1024), 0, stream, s);
+  }
   return check_launch("approx_state_kernel");
 }
 
@@ -814,6 +838,7 @@ extern "C" int dsa_approx_step(const void* queries, const float* weights, const 
               policy->order);
   DSA_REQUIRE(policy->order != DSA_ORDER_BUCKET || policy->buckets >= 1, "bucket order needs buckets >= 1");
   DSA_REQUIRE(policy->recent_window >= 0, "recent_window must be >= 0");
+  DSA_REQUIRE(policy->history == DSA_HISTORY_OWN, "a live step runs the own history (the teacher's needs the dense trace)");
   const int64_t blocks = (length + block_size - 1) / block_size;
   DSA_REQUIRE(state_stride >= blocks, "state_stride %lld < %lld blocks", (long long)state_stride, (long long)blocks);
   const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
@@ -846,7 +871,8 @@ extern "C" int dsa_approx_step(const void* queries, const float* weights, const 
 extern "C" int dsa_approx_replay_step(const float* current_scores, int64_t score_stride,
                                       const float* current_block_max, const dsa_approx_policy* policy,
                                       const double* gamma_rows, int64_t prev_length,
-                                      const int64_t* prev_topk, float* last_max, float* ema, float* volatility,
+                                      const int64_t* prev_topk, const int64_t* teacher_topk, float* last_max,
+                                      float* ema, float* volatility,
                                       int16_t* age, int16_t* cold_streak, int64_t state_stride, float* scores,
                                       uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
                                       int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
@@ -866,6 +892,9 @@ extern "C" int dsa_approx_replay_step(const float* current_scores, int64_t score
               "the current-max order needs current_block_max");
   DSA_REQUIRE(policy->order != DSA_ORDER_BUCKET || policy->buckets >= 1, "bucket order needs buckets >= 1");
   DSA_REQUIRE(policy->recent_window >= 0, "recent_window must be >= 0");
+  DSA_REQUIRE(policy->history == DSA_HISTORY_OWN || policy->history == DSA_HISTORY_TEACHER, "history %d unknown",
+              policy->history);
+  DSA_REQUIRE(policy->history != DSA_HISTORY_TEACHER || teacher_topk, "the teacher history needs teacher_topk");
   const int64_t blocks = (length + block_size - 1) / block_size;
   DSA_REQUIRE(state_stride >= blocks, "state_stride %lld < %lld blocks", (long long)state_stride, (long long)blocks);
   const TemporalWorkspace ws = temporal_layout(workspace, batch, length, k, block_size);
@@ -890,6 +919,7 @@ extern "C" int dsa_approx_replay_step(const float* current_scores, int64_t score
   a.prev_blocks = (int32_t)((prev_length + block_size - 1) / block_size);
   a.policy_mode = 1;
   a.ap = ApproxDev{last_max, ema, volatility, age, cold_streak, state_stride, gamma_rows, *policy};
+  a.teacher_topk = teacher_topk;
   a.ws = ws;
   return run_step(a, wave, DSA_DTYPE_BF16, out_topk, stream);
 }
@@ -917,6 +947,6 @@ extern "C" int dsa_approx_init_state(const float* scores, int64_t score_stride, 
   s.block_size = block_size;
   s.k = (int32_t)k;
   s.state_blocks = (int32_t)blocks;
-  hipLaunchKernelGGL(approx_state_kernel<true>, dim3(batch), dim3(1024), 0, static_cast<hipStream_t>(stream), s);
+  hipLaunchKernelGGL(approx_state_kernel<kStateInit>, dim3(batch), dim3(1024), 0, static_cast<hipStream_t>(stream), s);
   return check_launch("approx_state_kernel");
 }

@@ -84,6 +84,7 @@ struct TemporalArgs {
   int32_t wave_start, wave_len;
   int32_t policy_mode;    // 0: bound prev_max + gamma (replay filter); 1: own-trajectory policy
   ApproxDev ap;
+  const int64_t* teacher_topk;  // [rows][k]: dense top-k of the step (teacher history only)
   TemporalWorkspace ws;
 };
 

@@ -212,7 +212,7 @@ def verifier_step(
         gamma=float(policy.gamma), age_slope=float(policy.age_slope), ema_alpha=float(policy.ema_alpha),
         volatility_lambda=float(policy.volatility_lambda), risk_model=RISK_MODELS[policy.risk_model], order=order,
         buckets=buckets, cold_streak=int(policy.cold_streak), age_cap=-1 if policy.age_cap is None else int(policy.age_cap),
-        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), reserved=0,
+        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), history=0,
     )
     queries = queries.contiguous()
     weights = weights.to(torch.float32).contiguous()
@@ -559,7 +559,7 @@ def verifier_replay_step(
         gamma=float(policy.gamma), age_slope=float(policy.age_slope), ema_alpha=float(policy.ema_alpha),
         volatility_lambda=float(policy.volatility_lambda), risk_model=RISK_MODELS[policy.risk_model], order=order,
         buckets=buckets, cold_streak=int(policy.cold_streak), age_cap=-1 if policy.age_cap is None else int(policy.age_cap),
-        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), reserved=0,
+        recent_window=int(policy.recent_window), full_refresh=int(full_refresh), history=0,
     )
     cur = current_scores.to(torch.float32).contiguous()
     ver = verifier_scores.to(torch.float32).contiguous()

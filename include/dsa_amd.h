@@ -349,6 +349,8 @@ int dsa_temporal_step(const void* queries, const float* weights, const void* key
 #define DSA_ORDER_PREVIOUS_MAX 1 /* also "predicted_risk" */
 #define DSA_ORDER_BUCKET 2
 #define DSA_ORDER_CURRENT_MAX 3 /* "oracle_current": replay over recorded rows only */
+#define DSA_HISTORY_OWN 0       /* approx.py history_mode "own": the state follows the step's own top-k */
+#define DSA_HISTORY_TEACHER 1   /* "teacher": seeds and state follow the dense trace (replay only) */
 
 typedef struct dsa_approx_policy {
   double gamma;
@@ -362,7 +364,7 @@ typedef struct dsa_approx_policy {
   int32_t age_cap;       /* < 0: no cap */
   int32_t recent_window; /* keys; 0: none */
   int32_t full_refresh;  /* policy "full", refresh interval or fallback hit */
-  int32_t reserved;
+  int32_t history;       /* DSA_HISTORY_OWN, or DSA_HISTORY_TEACHER (replay over recorded rows only) */
 } dsa_approx_policy;
 
 int dsa_approx_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
@@ -373,14 +375,23 @@ int dsa_approx_step(const void* queries, const float* weights, const void* keys,
                     int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave,
                     int32_t key_dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* The own-trajectory step replayed over recorded score rows (approx.py:129-364
- * replay_step, history_mode "own"): row r's scores come from current_scores
- * [batch][score_stride] instead of being computed from keys.  The order
- * DSA_ORDER_CURRENT_MAX (the reference's "oracle_current") visits blocks by
- * larger current_block_max [batch][blocks] (fp32, nullable otherwise), then
- * lower address.  Other arguments, outputs and limits as dsa_approx_step. */
+/* One step replayed over recorded score rows (approx.py:129-364
+ * replay_step): row r's scores come from current_scores [batch][score_stride]
+ * instead of being computed from keys.  The order DSA_ORDER_CURRENT_MAX (the
+ * reference's "oracle_current") visits blocks by larger current_block_max
+ * [batch][blocks] (fp32, nullable otherwise), then lower address.
+ * History (policy->history, approx.py:143-158,270-280):
+ *   DSA_HISTORY_OWN: prev_topk is the previous step's own top-k and the
+ *     state is updated for the refreshed blocks only;
+ *   DSA_HISTORY_TEACHER: prev_topk is the previous step's dense top-k, and
+ *     every block's state is reset from the dense row (last max = EMA = the
+ *     block's maximum, volatility 0, age 0), with the cold streak restarting
+ *     at the blocks of teacher_topk [batch][k], the current step's dense
+ *     top-k (required in this mode, nullable otherwise).
+ * Other arguments, outputs and limits as dsa_approx_step. */
 int dsa_approx_replay_step(const float* current_scores, int64_t score_stride, const float* current_block_max,
-                           const dsa_approx_policy* policy, const double* gamma_rows, int64_t prev_length, const int64_t* prev_topk, float* last_max,
+                           const dsa_approx_policy* policy, const double* gamma_rows, int64_t prev_length,
+                           const int64_t* prev_topk, const int64_t* teacher_topk, float* last_max,
                            float* ema, float* volatility, int16_t* age, int16_t* cold_streak, int64_t state_stride,
                            float* scores, uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
                            int64_t batch, int64_t length, int64_t k, int32_t block_size, int32_t wave, void* workspace,

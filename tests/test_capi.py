@@ -56,7 +56,7 @@ def test_approx_policy_struct_matches_the_header() -> None:
     # four doubles, then eight int32 fields, no padding: 64 bytes
     assert ctypes.sizeof(_lib.ApproxPolicyC) == 64
     assert _lib.ApproxPolicyC.risk_model.offset == 32
-    assert _lib.ApproxPolicyC.reserved.offset == 60
+    assert _lib.ApproxPolicyC.history.offset == 60
 
 
 def test_approx_step_rejects_bad_policies_without_a_device() -> None:

@@ -5,8 +5,10 @@
 over 10-step float32 trajectories for 7 policies (written by the reference
 itself, tests/golden/make_replay_vectors.py).  ``dsa_amd.approx.replay_step``
 runs each transition in the HIP kernels with the recorded row as the score
-source (``dsa_approx_replay_step``).  For history_mode "own", every metric,
-every detail array and the final state must match exactly.
+source (``dsa_approx_replay_step``).  For both history modes ("own": seeds
+and state follow the step's own top-k; "teacher": they follow the dense
+trace), every metric, every detail array and the final state must match
+exactly.
 """
 
 from __future__ import annotations
@@ -45,18 +47,20 @@ def same(expected, got) -> bool:
     return expected == got
 
 
+@pytest.mark.parametrize("history", ["own", "teacher"])
 @pytest.mark.parametrize("p", range(len(gen.APPROX_POLICIES)))
-def test_replay_step_matches_reference_vectors(device, p) -> None:
+def test_replay_step_matches_reference_vectors(device, p, history) -> None:
     spec = gen.APPROX_POLICIES[p]
     steps = gen.make_trace(2000 + p)
     policy = approx.ApproxPolicy(**spec)
-    rows = [r for r in RESULTS["approx"] if r["policy_index"] == p and r["history_mode"] == "own"]
+    rows = [r for r in RESULTS["approx"] if r["policy_index"] == p and r["history_mode"] == history]
+    assert len(rows) == len(steps) - 1
     state = approx.initialize_state(torch.from_numpy(steps[0]).to(device).reshape(1, -1), k=gen.APPROX_K,
                                     block_size=gen.APPROX_BLOCK, capacity=steps[-1].size)
     for i in range(1, len(steps)):
         state, metrics, details = approx.replay_step(
             state, steps[i], policy=policy, k=gen.APPROX_K, block_size=gen.APPROX_BLOCK, step=i,
-            previous_length=steps[i - 1].size)
+            history_mode=history, previous_length=steps[i - 1].size)
         row = rows[i - 1]
         for field, expected in row.items():
             if field == "policy_index":
@@ -64,9 +68,9 @@ def test_replay_step_matches_reference_vectors(device, p) -> None:
             assert same(expected, metrics[field]), (p, i, field, expected, metrics[field])
         assert set(metrics) == set(row) - {"policy_index"}
         for name in ("approximate", "evaluated", "refreshed_blocks", "skipped_blocks", "missed_ranks"):
-            np.testing.assert_array_equal(np.asarray(details[name]), ARRAYS[f"approx_{p}_own_{i}_{name}"],
+            np.testing.assert_array_equal(np.asarray(details[name]), ARRAYS[f"approx_{p}_{history}_{i}_{name}"],
                                           err_msg=f"{p} {i} {name}")
     host = state.host()
-    np.testing.assert_array_equal(state.seed_order, ARRAYS[f"approx_{p}_own_state_topk"])
+    np.testing.assert_array_equal(state.seed_order, ARRAYS[f"approx_{p}_{history}_state_topk"])
     for name in ("last_max", "age", "cold_streak"):
-        np.testing.assert_array_equal(host[name][0], ARRAYS[f"approx_{p}_own_state_{name}"], err_msg=name)
+        np.testing.assert_array_equal(host[name][0], ARRAYS[f"approx_{p}_{history}_state_{name}"], err_msg=name)
