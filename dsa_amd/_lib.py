@@ -20,6 +20,7 @@ DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
 DTYPE_FP8_E4M3 = 3
+DTYPE_F64 = 4  # score rows of dsa_topk_exact only
 
 _TORCH_DTYPES = {
     torch.float32: DTYPE_F32,
@@ -55,6 +56,7 @@ _SIGNATURES: dict[str, list] = {
     "dsa_promote_blocks": [_p, _p, _p, _p, _i64, _p],
     "dsa_topk": [_p, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p, _p],
     "dsa_topk_long": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
+    "dsa_topk_exact": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_block_max": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "dsa_rope": [_p, _p, _p, _i64, _i32, _i32, _i32, ctypes.c_float, _i32, _p],
     "dsa_encode_keys_epilogue": [_p, _i32, _i64, _p, _p, ctypes.c_float, _p, _i32, ctypes.c_float, _p, _i32, _i64,
@@ -102,6 +104,7 @@ _RESTYPES: dict[str, object] = {
     "dsa_topk_long_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "dsa_score_topk_workspace_bytes": (_i64, [_i64, _i64]),
     "dsa_temporal_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
+    "dsa_topk_exact_workspace_bytes": (_i64, [_i64, _i64, _i32]),
 }
 
 

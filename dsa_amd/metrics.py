@@ -3,9 +3,13 @@
 Mirrors ``temporal_dsa.metrics`` (reference ``src/temporal_dsa/metrics.py``).
 ``stable_topk`` keeps the reference's definition (metrics.py:9-22): the k
 largest values, ties at the cut-off resolved towards the lower index, returned
-sorted by (value desc, index asc).  It runs on the GPU radix-select kernel;
-host (numpy) inputs are copied to the current GPU and the result is returned as
-a numpy int64 array, like the reference.
+sorted by (value desc, index asc).  It runs on the GPU: float32 rows within
+the radix-select kernels' limits (k <= 4096) take those, and everything else
+(float64 values, integer arrays, any k up to the row length, any length)
+takes the exact 64-bit-key kernel (``dsa_topk_exact``).  Host (numpy) inputs
+are copied to the current GPU and the result is returned as a numpy int64
+array, like the reference.  NaN values are rejected with ValueError (the
+reference's partition-based result is not a top-k for them).
 """
 
 from __future__ import annotations
@@ -53,14 +57,25 @@ def topk(
     matrix = scores.reshape(1, -1) if squeeze else scores
     if matrix.ndim != 2:
         raise ValueError(f"expected a vector or a matrix, got {tuple(scores.shape)}")
-    matrix = matrix.to(torch.float32)
+    matrix = _exact_dtype(matrix)
     if matrix.stride(1) != 1:
         matrix = matrix.contiguous()
     rows, length = matrix.shape
-    if not 0 < k <= MAX_K:
-        raise ValueError(f"k={k} outside [1, {MAX_K}]")
     if length == 0:
         raise ValueError("cannot take top-k of an empty row")
+    if k <= 0:
+        raise ValueError(f"k={k} must be positive")
+    if matrix.dtype == torch.float64 or k > MAX_K:
+        # float64 rows, or k beyond the radix-select kernels: the exact kernel.
+        if row_lengths is not None:
+            raise ValueError(f"row_lengths is supported for float32 rows with k <= {MAX_K}")
+        if k > length:
+            raise ValueError(f"k={k} exceeds the row length {length} (padding needs float32 rows, k <= {MAX_K})")
+        indices, values = _exact_topk(matrix, k, sorted=sorted, return_values=return_values)
+        if squeeze:
+            indices = indices[0]
+            values = values[0] if values is not None else None
+        return (indices, values) if return_values else indices
     indices = torch.empty((rows, k), device=matrix.device, dtype=torch.int64)
     values = torch.empty((rows, k), device=matrix.device, dtype=torch.float32) if return_values else None
     stream = _lib.stream_of(matrix)
@@ -108,14 +123,47 @@ def topk(
     return (indices, values) if return_values else indices
 
 
+def _exact_dtype(matrix: torch.Tensor) -> torch.Tensor:
+    """The dtype the kernels compare in, without changing any value: float32
+    for float32/float16/bfloat16 (exact), float64 for float64 and integers
+    (integers beyond 2^53 in magnitude cannot be compared exactly and raise)."""
+
+    if matrix.dtype in (torch.float32, torch.float16, torch.bfloat16):
+        return matrix.to(torch.float32)
+    if matrix.dtype == torch.float64:
+        return matrix
+    if matrix.dtype == torch.bool or not matrix.dtype.is_floating_point:
+        if matrix.numel() and matrix.dtype == torch.int64 and int(matrix.abs().max()) > 2**53:
+            raise ValueError("integer values beyond 2^53 in magnitude cannot be ordered exactly")
+        return matrix.to(torch.float64)
+    raise ValueError(f"unsupported dtype {matrix.dtype}")
+
+
+def _exact_topk(matrix: torch.Tensor, k: int, *, sorted: bool, return_values: bool):
+    """dsa_topk_exact on a float32 or float64 GPU matrix (unit column stride)."""
+
+    rows, length = matrix.shape
+    code = _lib.DTYPE_F64 if matrix.dtype == torch.float64 else _lib.DTYPE_F32
+    indices = torch.empty((rows, k), device=matrix.device, dtype=torch.int64)
+    values = torch.empty((rows, k), device=matrix.device, dtype=matrix.dtype) if return_values else None
+    stream = _lib.stream_of(matrix)
+    need = int(_lib.query("dsa_topk_exact_workspace_bytes", rows, k, int(sorted)))
+    workspace = _lib.workspace("topk_exact", matrix.device, stream, need, zeroed=False) if need else None
+    _lib.call(
+        "dsa_topk_exact", _lib.ptr(matrix), code, rows, length, matrix.stride(0), k, int(sorted), _lib.ptr(indices),
+        _lib.ptr(values), _lib.ptr(workspace), need, stream,
+    )
+    return indices, values
+
+
 def stable_topk(values: np.ndarray | torch.Tensor, k: int) -> np.ndarray | torch.Tensor:
     """Descending top-k indices with the index as deterministic tie-breaker.
 
     Reference: metrics.py:9-22 (same validation and messages).  A GPU tensor
     yields a GPU int64 tensor; anything else is copied to the GPU and yields a
-    numpy int64 array.  The kernel compares float32 values, so inputs that
-    float32 cannot represent exactly are rejected with ValueError rather than
-    silently narrowed.
+    numpy int64 array.  Values are compared exactly in their own precision:
+    float32 and narrower in float32, float64 and integers with 64-bit keys.
+    NaN values raise ValueError.
     """
 
     on_gpu = isinstance(values, torch.Tensor) and values.is_cuda
@@ -131,20 +179,18 @@ def stable_topk(values: np.ndarray | torch.Tensor, k: int) -> np.ndarray | torch
     if not 0 < k <= size:
         raise ValueError(f"k={k} is invalid for {size} values")
     if on_gpu:
-        if values.dtype != torch.float32:
-            narrowed = values.float()
-            if not torch.equal(narrowed.to(values.dtype), values):
-                raise ValueError("stable_topk on the GPU compares float32 values; these do not fit float32 exactly")
-            values = narrowed
+        if values.dtype.is_floating_point and bool(torch.isnan(values).any()):
+            raise ValueError("stable_topk does not order NaN values")
         return topk(values, k, sorted=True)
     host = values.detach().cpu().numpy() if isinstance(values, torch.Tensor) else array
-    narrowed = np.ascontiguousarray(host, dtype=np.float32)
-    # The kernel orders float32 keys: a value that float32 cannot hold exactly
-    # could tie with a neighbour and change the selection.
-    if not np.array_equal(narrowed.astype(host.dtype, copy=False), host):
-        raise ValueError("stable_topk on the GPU compares float32 values; these do not fit float32 exactly")
+    if host.dtype.kind == "f" and np.isnan(host).any():
+        raise ValueError("stable_topk does not order NaN values")
+    if host.dtype.kind not in "fiub":
+        raise ValueError(f"unsupported dtype {host.dtype}")
+    if host.dtype == np.float16:
+        host = host.astype(np.float32)
     device = _device()
-    return topk(torch.from_numpy(narrowed).to(device), k, sorted=True).cpu().numpy()
+    return topk(torch.from_numpy(np.ascontiguousarray(host)).to(device), k, sorted=True).cpu().numpy()
 
 
 def topk_recall(predicted, target) -> float:

@@ -38,6 +38,7 @@ extern "C" {
 #define DSA_DTYPE_F16 1
 #define DSA_DTYPE_BF16 2
 #define DSA_DTYPE_FP8_E4M3 3 /* keys only; queries are bf16 */
+#define DSA_DTYPE_F64 4      /* score rows of dsa_topk_exact only */
 
 /* Message describing the last failure on the calling thread. */
 const char* dsa_last_error(void);
@@ -183,6 +184,21 @@ int64_t dsa_topk_long_workspace_bytes(int64_t rows, int64_t length, int64_t k);
 int dsa_topk_long(const float* scores, int64_t rows, int64_t length, int64_t k, int32_t sorted,
                   int64_t* out_indices, float* out_values, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/* Exact stable top-k of float64 or float32 rows with 64-bit order keys:
+ * stable_topk (metrics.py:9-22) for any 0 < k <= length, any length below
+ * 2^31, and float64 values that float32 cannot hold.  One workgroup per row:
+ * radix select of the cut, a gather in index order and, when `sorted`, a
+ * stable radix sort into (descending value, ascending index) order.
+ * values [rows][row_stride] (DSA_DTYPE_F64 or DSA_DTYPE_F32), out_indices
+ * [rows][k], out_values [rows][k] in the input dtype or NULL.  Sorted output
+ * needs dsa_topk_exact_workspace_bytes(rows, k, 1) bytes of workspace
+ * (16-byte aligned, no initialisation); unsorted output needs none.  NaN
+ * values are outside the contract (the Python mirror rejects them). */
+int64_t dsa_topk_exact_workspace_bytes(int64_t rows, int64_t k, int32_t sorted);
+int dsa_topk_exact(const void* values, int32_t value_dtype, int64_t rows, int64_t length, int64_t row_stride,
+                   int64_t k, int32_t sorted, int64_t* out_indices, void* out_values, void* workspace,
+                   int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused decode step: dense scores of `batch` sequences (as dsa_full_scores)

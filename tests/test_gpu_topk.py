@@ -124,3 +124,62 @@ def test_stable_topk_reference_cases(device) -> None:
     assert np.array_equal(metrics.stable_topk(np.ones(64, dtype=np.float32), 8), np.arange(8))
     gpu = metrics.stable_topk(torch.tensor([0.5, 2.0, 2.0], device=device), 2)
     assert gpu.is_cuda and gpu.cpu().tolist() == [1, 2]
+
+
+def _f64_rows(kind: str, rows: int, length: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    if kind == "f64_only":
+        # distinct in float64, equal once narrowed to float32
+        base = rng.integers(0, 50, size=(rows, length)).astype(np.float64)
+        return 1.0 + base * 2.0**-40
+    if kind == "ties":
+        return rng.integers(-3, 4, size=(rows, length)).astype(np.float64)
+    if kind == "zeros_inf":
+        x = rng.choice(np.array([-0.0, 0.0, 1e300, -1e300, np.inf, -np.inf, 5e-324]), size=(rows, length))
+        return x.astype(np.float64)
+    return rng.normal(size=(rows, length)) * 1e6
+
+
+@pytest.mark.parametrize("kind", ["f64_only", "ties", "zeros_inf", "normal"])
+@pytest.mark.parametrize("length,k", [(1, 1), (300, 17), (5000, 5000), (40000, 2048), (70000, 9000)])
+def test_float64_rows_exact(device, kind, length, k) -> None:
+    # stable_topk over float64 (the reference's replay calls it on float64
+    # score vectors): values that float32 would merge stay distinct, and the
+    # set and order equal the reference definition computed in float64.
+    print(f"topk exact f64 kind={kind} L={length} k={k}", flush=True)
+    host = _f64_rows(kind, 2, length, seed=length + k)
+    x = torch.from_numpy(host).to(device)
+    idx_sorted, val_sorted = metrics.topk(x, k, sorted=True, return_values=True)
+    idx_index = metrics.topk(x, k, sorted=False)
+    assert val_sorted.dtype == torch.float64
+    for r in range(2):
+        want = T.stable_topk(host[r], k)
+        assert idx_sorted[r].cpu().numpy().tolist() == want.tolist(), r
+        np.testing.assert_array_equal(val_sorted[r].cpu().numpy().view(np.uint64),
+                                      np.where(host[r][want] == 0, 0.0, host[r][want]).view(np.uint64)
+                                      if kind == "zeros_inf" else host[r][want].view(np.uint64))
+        assert idx_index[r].cpu().numpy().tolist() == np.sort(want).tolist(), r
+    # the reference's own API: a host float64 vector in, a numpy int64 array out
+    got = metrics.stable_topk(host[0], k)
+    assert isinstance(got, np.ndarray) and got.tolist() == T.stable_topk(host[0], k).tolist()
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+@pytest.mark.parametrize("length,k", [(9000, 4097), (50000, 20000), (300000, 100)])
+def test_float32_large_k_exact(device, kind, length, k) -> None:
+    # k above the radix-select kernels' 4096, or any length: the exact kernel.
+    print(f"topk exact f32 kind={kind} L={length} k={k}", flush=True)
+    host = rows_for(kind, 2, length, seed=length + 3 * k)
+    x = torch.from_numpy(host).to(device)
+    idx_sorted = metrics.topk(x, k, sorted=True) if k > 4096 else metrics._exact_topk(
+        x, k, sorted=True, return_values=False)[0]
+    for r in range(2):
+        want = T.stable_topk(host[r], k)
+        assert idx_sorted[r].cpu().numpy().tolist() == want.tolist(), r
+
+
+def test_integer_and_bool_inputs(device) -> None:
+    ints = np.array([5, -3, 2**52, 7, 7, -2**52, 0], dtype=np.int64)
+    assert metrics.stable_topk(ints, 4).tolist() == T.stable_topk(ints, 4).tolist()
+    with pytest.raises(ValueError, match="2\\^53"):
+        metrics.stable_topk(torch.tensor([2**60, 1], dtype=torch.int64, device=device), 1)

@@ -80,11 +80,12 @@ def test_reference_names_are_aliases() -> None:
     assert math.ceil(65 / 64) == 2
 
 
-def test_stable_topk_rejects_values_float32_cannot_hold() -> None:
-    # 1 + 2**-30 and 1.0 are distinct in float64 but equal in float32: narrowing
-    # them would create a tie the reference does not have.
-    with pytest.raises(ValueError, match="float32"):
-        metrics.stable_topk(np.array([1.0 + 2.0**-30, 1.0, 0.5]), 1)
+def test_stable_topk_rejects_nan_and_unsupported_inputs() -> None:
+    # NaN has no place in the reference's partition-based order.
+    with pytest.raises(ValueError, match="NaN"):
+        metrics.stable_topk(np.array([1.0, np.nan, 0.5]), 1)
+    with pytest.raises(ValueError, match="dtype"):
+        metrics.stable_topk(np.array(["a", "b"]), 1)
 
 
 def test_workspace_cache_grows_geometrically() -> None:
