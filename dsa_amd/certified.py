@@ -78,3 +78,54 @@ def temporal_score_radius(
         dim, _lib.ptr(out), _lib.stream_of(q_now),
     )
     return out
+
+
+def certified_margins(
+    q_now: torch.Tensor,
+    q_prev: torch.Tensor,
+    w_now: torch.Tensor,
+    w_prev: torch.Tensor,
+    keys: torch.Tensor,
+    previous_length: int,
+    block_size: int,
+) -> torch.Tensor:
+    """Certified per-block margins ``[B, ceil(previous_length / block_size)]``
+    (float64) of a temporal step over shared-key caches.
+
+    The reference's radius (certified.py:43-47) with every head's block norm
+    equal to the block's largest key norm, plus an allowance for the fp32
+    rounding of both steps' scores; with the previous step's dense block
+    maxima, ``temporal_step(..., block_margins=...)`` then keeps every key of
+    the dense top-k.  queries ``[B, 64, 128]`` and keys ``[B, C, 128]``
+    (bf16/fp16, the first ``previous_length`` keys are summarised), weights
+    ``[B, 64]``.
+    """
+
+    tensors = (q_now, q_prev, w_now, w_prev, keys)
+    if not all(t.is_cuda for t in tensors):
+        raise ValueError("HIP kernels require GPU tensors")
+    if q_now.ndim != 3 or q_now.shape[1:] != (64, 128) or q_prev.shape != q_now.shape:
+        raise ValueError("queries must be [batch,64,128]")
+    batch = q_now.shape[0]
+    if w_now.shape != (batch, 64) or w_prev.shape != (batch, 64):
+        raise ValueError("weights must be [batch,64]")
+    if keys.ndim != 3 or keys.shape[0] != batch or keys.shape[2] != 128:
+        raise ValueError("keys must be [batch,C,128]")
+    if keys.dtype not in (torch.bfloat16, torch.float16) or q_now.dtype != keys.dtype or q_prev.dtype != keys.dtype:
+        raise ValueError("queries and keys must share FP16/BF16 dtype")
+    if not 0 < previous_length <= keys.shape[1]:
+        raise ValueError("previous_length outside the key buffer")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    if keys.stride(2) != 1 or keys.stride(1) != 128:
+        keys = keys.contiguous()
+    key_stride = keys.stride(0) // 128
+    blocks = (previous_length + block_size - 1) // block_size
+    out = torch.empty((batch, blocks), device=keys.device, dtype=torch.float64)
+    qn, qp = q_now.contiguous(), q_prev.contiguous()
+    wn, wp = w_now.to(torch.float32).contiguous(), w_prev.to(torch.float32).contiguous()
+    _lib.call(
+        "dsa_certified_margins", _lib.ptr(qn), _lib.ptr(qp), _lib.ptr(wn), _lib.ptr(wp), _lib.ptr(keys), key_stride,
+        batch, previous_length, block_size, _lib.dtype_code(keys.dtype), _lib.ptr(out), _lib.stream_of(keys),
+    )
+    return out

@@ -106,10 +106,103 @@ __global__ __launch_bounds__(256) void temporal_radius_kernel(const double* q_no
   }
 }
 
+// Certified per-block margins of a temporal step over a shared-key cache (one
+// key row per token, seen by all 64 heads): the reference's radius
+// (certified.py:43-47) with every head's block norm equal to the block's
+// largest key norm n_b,
+//   radius_b = n_b * sum_h (|w_now - w_prev|_h ||q_prev,h|| + |w_now|_h ||q_now,h - q_prev,h||),
+// plus an allowance for the fp32 rounding of the two steps' scores: a score
+// computed from bf16/fp16 operands (exact products, fp32 sums over 128 dims
+// and 64 heads) is within (128 + 64 + 4) * 2^-24 < 2^-15 of
+// sum_h |w_h| ||q_h|| ||k|| of its exact value, so
+//   margin_b = n_b * (C + 2^-15 * sum_h (|w_now|_h ||q_now,h|| + |w_prev|_h ||q_prev,h||))
+// bounds |score_now - score_prev| of every key of the block as computed here.
+// Everything is float64 and the result is scaled by kRadiusRoundUp.  One wave
+// per block; each workgroup derives its row's two head sums first.
+constexpr double kScoreRoundingAllowance = 0x1p-15;
+
+__global__ __launch_bounds__(256) void certified_margins_kernel(const uint16_t* q_now, const uint16_t* q_prev,
+                                                                const float* w_now, const float* w_prev,
+                                                                const uint16_t* keys, int64_t key_stride,
+                                                                int prev_length, int block_size, int blocks_per_row,
+                                                                int q_dtype, double* margins) {
+  __shared__ double s_radius[kHeads];
+  __shared__ double s_slack[kHeads];
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x;
+  auto q_at = [&](const uint16_t* q, int i) -> double {
+    const uint16_t bits = q[(size_t)row * kHeads * kHeadDim + i];
+    return q_dtype == kBF16 ? (double)__uint_as_float(uint32_t(bits) << 16)
+                            : (double)(float)__builtin_bit_cast(_Float16, bits);
+  };
+  if (tid < kHeads) {
+    double prev_sq = 0.0, now_sq = 0.0, diff_sq = 0.0;
+    for (int d = 0; d < kHeadDim; ++d) {
+      const double p = q_at(q_prev, tid * kHeadDim + d);
+      const double c = q_at(q_now, tid * kHeadDim + d);
+      prev_sq = fma(p, p, prev_sq);
+      now_sq = fma(c, c, now_sq);
+      diff_sq = fma(c - p, c - p, diff_sq);
+    }
+    const double wn = (double)w_now[(size_t)row * kHeads + tid];
+    const double wp = (double)w_prev[(size_t)row * kHeads + tid];
+    s_radius[tid] = fabs(wn - wp) * sqrt(prev_sq) + fabs(wn) * sqrt(diff_sq);
+    s_slack[tid] = fabs(wn) * sqrt(now_sq) + fabs(wp) * sqrt(prev_sq);
+  }
+  __syncthreads();
+  double radius = 0.0, slack = 0.0;
+  for (int h = 0; h < kHeads; ++h) {
+    radius += s_radius[h];
+    slack += s_slack[h];
+  }
+  const double coef = radius + kScoreRoundingAllowance * slack;
+  const int lane = tid & 63;
+  const int b = blockIdx.x * 4 + (tid >> 6);
+  if (b >= blocks_per_row) return;
+  const int start = b * block_size;
+  const int stop = min(prev_length, start + block_size);
+  double best = 0.0;
+  for (int t = start; t < stop; ++t) {
+    // lane l holds dims 2l, 2l + 1 of the key row
+    const uint32_t two = reinterpret_cast<const uint32_t*>(keys + ((size_t)row * key_stride + t) * kHeadDim)[lane];
+    double x0, x1;
+    if (q_dtype == kBF16) {
+      x0 = (double)__uint_as_float(two << 16);
+      x1 = (double)__uint_as_float(two & 0xffff0000u);
+    } else {
+      x0 = (double)(float)__builtin_bit_cast(_Float16, (uint16_t)(two & 0xffffu));
+      x1 = (double)(float)__builtin_bit_cast(_Float16, (uint16_t)(two >> 16));
+    }
+    double acc = fma(x0, x0, x1 * x1);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    best = fmax(best, sqrt(acc));
+  }
+  if (lane == 0) margins[(size_t)row * blocks_per_row + b] = best * coef * kRadiusRoundUp;
+}
+
 }  // namespace
 }  // namespace dsa
 
 using namespace dsa;
+
+extern "C" int dsa_certified_margins(const void* q_now, const void* q_prev, const float* w_now, const float* w_prev,
+                                     const void* keys, int64_t key_stride, int64_t batch, int64_t prev_length,
+                                     int32_t block_size, int32_t key_dtype, double* margins, void* stream) {
+  DSA_REQUIRE(q_now && q_prev && w_now && w_prev && keys && margins, "null pointer argument");
+  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
+  DSA_REQUIRE(prev_length > 0 && prev_length <= key_stride && prev_length < (int64_t(1) << 31),
+              "prev_length %lld invalid", (long long)prev_length);
+  DSA_REQUIRE(block_size > 0, "block_size must be positive");
+  DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16, "certified margins take bf16/fp16 queries and keys");
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(keys) % 4 == 0, "keys must be 4-byte aligned");
+  const int64_t blocks = (prev_length + block_size - 1) / block_size;
+  hipLaunchKernelGGL(certified_margins_kernel, dim3((unsigned)((blocks + 3) / 4), (unsigned)batch), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q_now),
+                     static_cast<const uint16_t*>(q_prev), w_now, w_prev, static_cast<const uint16_t*>(keys),
+                     key_stride, (int)prev_length, (int)block_size, (int)blocks, (int)key_dtype, margins);
+  return check_launch("certified_margins_kernel");
+}
 
 extern "C" int dsa_block_max(const float* scores, int64_t rows, int64_t length,
                              int64_t row_stride, int32_t block_size, float* out, void* stream) {

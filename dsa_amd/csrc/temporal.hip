@@ -97,7 +97,9 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     } else {
       const bool fresh = grown && b >= first_new;
       const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
-      upper = fresh ? HUGE_VAL : (double)pm + (a.gamma_d ? a.gamma_d[row] : (double)a.gamma[row]);
+      const double margin = a.margins ? a.margins[(size_t)row * a.prev_blocks + min(b, a.prev_blocks - 1)]
+                                      : (a.gamma_d ? a.gamma_d[row] : (double)a.gamma[row]);
+      upper = fresh ? HUGE_VAL : (double)pm + margin;
       rank_value = a.scan_order == 3 ? (double)a.order_key[(size_t)row * nb + b] : upper;
       group = hot_first && !hot[b] ? 0x80000000u : 0u;
     }
@@ -312,7 +314,10 @@ constexpr int kScanThreads = 512;
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kMaxRun = 4096;  // k
 constexpr int kScanTiles = 6;  // 16-key tiles in flight per wave
-constexpr int kMaxTemporalLength = 32768;
+// Keys per row: the persistent scan keeps the row's seed mask (one bit per
+// key, 16 KiB at this length) in LDS; block counts are capped separately by
+// kMaxTemporalBlocks (131072 keys in blocks of 64 or more).
+constexpr int kMaxTemporalLength = 131072;
 // Above this many waves of scan positions a step runs the persistent
 // per-row scan: one launch per wave costs a launch, a grid drain and a refresh
 // launch (~11 us at C3), against ~4.4 us per wave in LDS but with one CU per
@@ -704,7 +709,8 @@ int check_step(const void* queries, const void* keys, int64_t key_stride, const 
   DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(block_size == 16 || block_size == 32 || block_size == 64 || block_size == 128,
               "block_size %d not in {16, 32, 64, 128}", block_size);
-  DSA_REQUIRE(length > 0 && length <= kMaxTemporalLength, "length %lld outside [1, 32768]", (long long)length);
+  DSA_REQUIRE(length > 0 && length <= kMaxTemporalLength, "length %lld outside [1, %d]", (long long)length,
+              kMaxTemporalLength);
   DSA_REQUIRE(key_stride >= length, "key_stride < length");
   DSA_REQUIRE(prev_length > 0 && prev_length <= length, "prev_length %lld outside [1, length]",
               (long long)prev_length);
@@ -735,13 +741,14 @@ extern "C" int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, i
 extern "C" int dsa_temporal_step(const void* queries, const float* weights, const void* keys,
                                  int64_t key_stride, const float* key_scales, const float* prev_block_max,
                                  int64_t prev_length,
-                                 const int64_t* prev_topk, const float* gamma, float* scores,
+                                 const int64_t* prev_topk, const float* gamma, const double* block_margins,
+                                 float* scores,
                                  uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
                                  int64_t batch, int64_t length, int64_t k, int32_t block_size,
                                  int32_t scan_order, int32_t wave, int32_t key_dtype, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
-  DSA_REQUIRE(queries && weights && keys && prev_block_max && prev_topk && gamma && scores && evaluated_blocks &&
-                  out_topk && qk_scored,
+  DSA_REQUIRE(queries && weights && keys && prev_block_max && prev_topk && (gamma || block_margins) && scores &&
+                  evaluated_blocks && out_topk && qk_scored,
               "null pointer argument");
   if (int st = check_step(queries, keys, key_stride, key_scales, prev_length, batch, length, k, block_size, wave,
                           key_dtype, workspace))
@@ -760,6 +767,7 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
   a.prev_max = prev_block_max;
   a.seeds = prev_topk;
   a.gamma = gamma;
+  a.margins = block_margins;
   a.scores = scores;
   a.evaluated = evaluated_blocks;
   a.qk_scored = qk_scored;

@@ -72,6 +72,7 @@ struct TemporalArgs {
   const int64_t* seeds;   // [rows][k]
   const float* gamma;     // [rows]
   const double* gamma_d;  // [rows] or null: a float64 margin (replay over recorded scores)
+  const double* margins;  // [rows][prev_blocks] or null: per-block margins (certified bound) in place of gamma
   const float* source;    // [rows][source_stride] or null: recorded scores read instead of scoring keys
   int64_t source_stride;
   int32_t* order_out;     // [rows][blocks] or null: the scan order, for the caller

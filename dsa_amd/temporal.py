@@ -65,6 +65,7 @@ def temporal_step(
     scan_order: str = "previous_hot",
     wave: int = 32,
     key_scales: torch.Tensor | None = None,
+    block_margins: torch.Tensor | None = None,
 ) -> TemporalStep:
     """One pruned decode step for ``B`` sequences.
 
@@ -74,7 +75,9 @@ def temporal_step(
     cache is read in place),
     ``previous_block_max`` ``[B, ceil(previous_length / block_size)]``,
     ``previous_topk`` ``[B, k]`` (distinct indices below ``previous_length``),
-    ``gamma`` a float or ``[B]`` tensor.
+    ``gamma`` a float or ``[B]`` tensor, or ``block_margins``
+    ``[B, ceil(previous_length / block_size)]`` float64 per-block margins used
+    instead of it (e.g. :func:`dsa_amd.certified.certified_margins`).
     """
 
     _lib.load()
@@ -132,6 +135,11 @@ def temporal_step(
     prev_max = previous_block_max.to(device=device, dtype=torch.float32).contiguous()
     seeds = previous_topk.to(device=device, dtype=torch.int64).contiguous()
     gamma_t = gamma_t.contiguous()
+    margins = None
+    if block_margins is not None:
+        if tuple(block_margins.shape) != (batch, prev_blocks):
+            raise ValueError(f"block_margins must be [batch,{prev_blocks}]")
+        margins = block_margins.to(device=device, dtype=torch.float64).contiguous()
     stream = _lib.stream_of(keys)
     blocks = math.ceil(length / block_size)
     scores = torch.empty((batch, length), device=device, dtype=torch.float32)
@@ -141,7 +149,7 @@ def temporal_step(
     ws = _workspace(device, stream, batch, length, k, block_size)
     _lib.call(
         "dsa_temporal_step", _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), key_stride, _lib.ptr(key_scales),
-        _lib.ptr(prev_max), previous_length, _lib.ptr(seeds), _lib.ptr(gamma_t), _lib.ptr(scores),
+        _lib.ptr(prev_max), previous_length, _lib.ptr(seeds), _lib.ptr(gamma_t), _lib.ptr(margins), _lib.ptr(scores),
         _lib.ptr(evaluated), _lib.ptr(topk), _lib.ptr(qk), batch, length, k, block_size,
         SCAN_ORDERS[scan_order], wave, _lib.dtype_code(keys.dtype), _lib.ptr(ws), ws.numel(), stream,
     )

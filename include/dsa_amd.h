@@ -298,6 +298,10 @@ int dsa_score_topk_noalloc(const void* queries, const float* weights, const void
  *               distinct, < prev_length
  *   gamma       [batch] fp32: absolute margin; U_b = prev max + gamma, and
  *               blocks holding keys past prev_length are never pruned
+ *   block_margins [batch, ceil(prev_length / block_size)] float64 or NULL:
+ *               per-block margins used instead of gamma (U_b = prev max +
+ *               margin_b), e.g. the certified ones of dsa_certified_margins
+ *               (gamma may then be NULL)
  *   scan_order  0 address, 1 previous-hot (blocks of the seeds first, then
  *               larger U, then address), 2 larger U then address
  *   wave        0: threshold fixed at the seed minimum (static); W > 0: the
@@ -312,8 +316,9 @@ int dsa_score_topk_noalloc(const void* queries, const float* weights, const void
  *   keys        [batch, key_stride, 128]: the first `length` rows of each
  *               sequence are scored (a KV cache with spare capacity needs no
  *               copy); fp8 key_scales are [batch, ceil(key_stride / 128)]
- *   length <= 32768, block_size in {16, 32, 64, 128}, k <= 4096; keys as in
- *   dsa_full_scores (bf16/fp16, or fp8 with key_scales).
+ *   length <= 131072 and at most 2048 blocks, block_size in {16, 32, 64,
+ *   128}, k <= 4096; keys as in dsa_full_scores (bf16/fp16, or fp8 with
+ *   key_scales).
  * Pruned blocks load no key bytes.  A step costs 3 + 2 * ceil(blocks / W)
  * launches (3 when static).
  * ------------------------------------------------------------------------ */
@@ -321,7 +326,8 @@ int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, int64_t k, i
 int dsa_temporal_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
                       const float* key_scales, const float* prev_block_max, int64_t prev_length,
                       const int64_t* prev_topk,
-                      const float* gamma, float* scores, uint8_t* evaluated_blocks, int64_t* out_topk,
+                      const float* gamma, const double* block_margins, float* scores, uint8_t* evaluated_blocks,
+                      int64_t* out_topk,
                       int32_t* qk_scored, int64_t batch, int64_t length, int64_t k, int32_t block_size,
                       int32_t scan_order, int32_t wave, int32_t key_dtype, void* workspace,
                       int64_t workspace_bytes, void* stream);
@@ -564,6 +570,20 @@ int dsa_block_key_norms(const void* keys, int64_t tokens, int64_t heads, int64_t
 int dsa_temporal_score_radius(const double* q_now, const double* q_prev, const double* w_now,
                               const double* w_prev, const double* block_key_norm, int64_t blocks,
                               int64_t heads, int64_t dim, double* out, void* stream);
+
+/* Certified per-block margins of a temporal step over a shared-key cache
+ * (the reference's radius, certified.py:18-48, with every head's block norm
+ * equal to the block's largest key norm), plus an allowance for the fp32
+ * rounding of both steps' scores, so that with the previous step's dense
+ * block maxima, U_b = prev max + margin_b bounds every current score of
+ * block b as the scoring kernels compute it: a step pruning with these
+ * margins keeps every key of the dense top-k.  q_now, q_prev [batch, 64, 128]
+ * and keys [batch, key_stride, 128] in key_dtype (bf16/fp16), w_now, w_prev
+ * [batch, 64] fp32; margins [batch, ceil(prev_length / block_size)] float64
+ * over the first prev_length keys.  Computed in float64. */
+int dsa_certified_margins(const void* q_now, const void* q_prev, const float* w_now, const float* w_prev,
+                          const void* keys, int64_t key_stride, int64_t batch, int64_t prev_length,
+                          int32_t block_size, int32_t key_dtype, double* margins, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sidecar encoder epilogues (sidecar.py:10-88).  The projections wq / wk /

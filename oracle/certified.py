@@ -40,3 +40,26 @@ def block_key_norms(keys, block_size: int) -> np.ndarray:
     norms = np.sqrt((keys ** 2).sum(axis=2))  # [tokens, heads]
     blocks = (keys.shape[0] + block_size - 1) // block_size
     return np.stack([norms[b * block_size : (b + 1) * block_size].max(axis=0) for b in range(blocks)])
+
+
+SCORE_ROUNDING_ALLOWANCE = 2.0**-15
+
+
+def certified_margins(q_now, q_prev, w_now, w_prev, keys, block_size: int) -> np.ndarray:
+    """Per-block margins of a temporal step over one sequence's shared-key
+    cache: ``temporal_score_radius`` (certified.py:18-48) with every head's
+    block norm equal to the block's largest key norm, plus the fp32 score
+    rounding allowance ``2^-15 * n_b * sum_h (|w_now| ||q_now|| + |w_prev|
+    ||q_prev||)`` of the two steps' kernel scores.  q [heads, dim], w [heads],
+    keys [tokens, dim] (the previous step's keys)."""
+
+    q_now = np.asarray(q_now, dtype=np.float64)
+    q_prev = np.asarray(q_prev, dtype=np.float64)
+    w_now = np.asarray(w_now, dtype=np.float64)
+    w_prev = np.asarray(w_prev, dtype=np.float64)
+    keys = np.asarray(keys, dtype=np.float64)
+    heads = q_now.shape[0]
+    block_norm = block_key_norms(keys[:, None, :], block_size)[:, 0]  # [blocks]
+    radius = temporal_score_radius(q_now, q_prev, w_now, w_prev, np.repeat(block_norm[:, None], heads, axis=1))
+    slack = np.abs(w_now) * np.sqrt((q_now ** 2).sum(axis=1)) + np.abs(w_prev) * np.sqrt((q_prev ** 2).sum(axis=1))
+    return radius + SCORE_ROUNDING_ALLOWANCE * block_norm * slack.sum()

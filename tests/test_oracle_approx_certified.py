@@ -175,3 +175,31 @@ def test_approx_wave_covering_every_block_is_the_static_policy() -> None:
         state = initialize_state(previous, k=32, block_size=16)
         _, m2, _ = replay_step(state, current, policy=dynamic, k=32, block_size=16, step=1, previous_length=600)
         assert m2["qk_scored"] <= m0["qk_scored"], order
+
+
+def test_certified_margins_restate_the_radius_for_shared_keys() -> None:
+    from oracle.certified import SCORE_ROUNDING_ALLOWANCE, certified_margins
+
+    # One head, one key block: radius 3*5 + 2*5 = 25 per unit key norm (the
+    # asymmetric closed form above), the block's largest key norm is 13
+    # ((5, 12)), and the rounding allowance adds 2^-15 * 13 * (2*10 + 1*5).
+    keys = np.array([[3.0, 4.0], [5.0, 12.0], [0.0, 1.0]])
+    m = certified_margins(np.array([[6.0, 8.0]]), np.array([[3.0, 4.0]]), np.array([2.0]), np.array([-1.0]), keys, 4)
+    assert m.tolist() == [25.0 * 13.0 + SCORE_ROUNDING_ALLOWANCE * 13.0 * 25.0]
+
+
+def test_certified_margins_cover_every_key_change() -> None:
+    from oracle.certified import certified_margins
+
+    rng = np.random.default_rng(11)
+    for rho in (0.9, 0.999):
+        q_prev = rng.normal(size=(64, 128)) / np.sqrt(128)
+        q_now = rho * q_prev + np.sqrt(1 - rho * rho) * rng.normal(size=(64, 128)) / np.sqrt(128)
+        w_prev = rng.normal(size=64) / 8
+        w_now = w_prev + 0.01 * rng.normal(size=64)
+        keys = rng.normal(size=(500, 128))
+        before = S.relu_index_score(q_prev, keys, w_prev)
+        after = S.relu_index_score(q_now, keys, w_now)
+        m = certified_margins(q_now, q_prev, w_now, w_prev, keys, 16)
+        for b, start in enumerate(range(0, 500, 16)):
+            assert np.all(np.abs(after[start : start + 16] - before[start : start + 16]) <= m[b])
