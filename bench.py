@@ -389,7 +389,7 @@ def run_c3(args) -> None:
     import numpy as np
     import torch
 
-    from dsa_amd import _lib, approx, decode, temporal
+    from dsa_amd import _lib, approx, certified, decode, temporal
 
     _lib.load()
     device = torch.device("cuda", 0)
@@ -469,6 +469,23 @@ def run_c3(args) -> None:
                 variants.append({"kind": "replay", "block_size": bs, "method": method, "scan_order": order,
                                  "gamma_sigma": gamma_sigma, "wave": wave if method == "dynamic" else 0,
                                  **c3_summary(rows)})
+        # Certified bound (reference certified.py:18-62): U_b = previous block
+        # max + the certified margin of the block (radius + fp32 rounding
+        # allowance, dsa_certified_margins), computed per step from the two
+        # queries and the keys; the margins are part of the timed step.
+        for method, order in (("static", "address"), ("dynamic", "previous_hot")):
+            rows = []
+            for t in range(1, C3_STEPS):
+                def certified_step():
+                    margins = certified.certified_margins(queries[t], queries[t - 1], w, w, keys, lengths[t - 1], bs)
+                    return temporal.temporal_step(
+                        queries[t], w, keys[:, : lengths[t]], prev_max[t - 1], lengths[t - 1], dense_topk[t - 1], 0.0,
+                        block_size=bs, method=method, scan_order=order, wave=wave, block_margins=margins)
+                step, us = timed(certified_step)
+                record(rows, t, bs, step, us)
+            variants.append({"kind": "certified", "block_size": bs, "method": method, "scan_order": order,
+                             "gamma_sigma": "certified", "wave": wave if method == "dynamic" else 0,
+                             **c3_summary(rows)})
         # Own trajectory: the policy state is initialised from the dense step 0
         # and then only sees what its own pruned steps scored.
         own = (
@@ -509,7 +526,7 @@ def run_c3(args) -> None:
         "data": "synthetic",
         "config": {
             "workload": "C3 temporal replay: B=4 x 256 decode steps, keys N(0,1) bf16, AR(1) queries rho=0.95, "
-            "K=2048, blocks 16/32/64/128, gamma_sigma 0/0.25/0.5/1",
+            "K=2048, blocks 16/32/64/128, gamma_sigma 0/0.25/0.5/1 and the certified radius",
             "headline_rule": f"largest median net byte reduction among variants with mean Recall@K >= {C3_HEADLINE_RECALL}",
             "refreshes_per_scan": args.c3_refreshes,
         },
@@ -740,6 +757,7 @@ def run_c5(args) -> None:
     keys_per_step = C5_BATCH * C5_LENGTH
     score_bytes = keys_per_step * (128 + 4) + C5_BATCH * (blocks * 4 + 64 * 128 * 2 + 64 * 4)
     progressive = c5_progressive(q, w, sets, idx, flush, device)
+    temporal_leg = c5_temporal(q, w, sets, flush, device)
     achieved = score_bytes / (sc["median_us"] * 1e-6) / 1e9
     line = {
         "metric": "C5 fp8 long-context decode: G keys scored/s + % HBM roofline, B=4 L=131072 fp8 top-K2048",
@@ -763,11 +781,87 @@ def run_c5(args) -> None:
         "step": st,
         "score": sc,
         "progressive": progressive,
+        "temporal": temporal_leg,
         "timing": f"step: HIP events around the step's launches, 512 MiB {args.flush} flush before each, median over 100; "
                   "score: HIP events recorded by the scoring kernel itself (hipExtLaunchKernel), median over 50",
     }
     write_table(args, line, [])
     print(json.dumps(line), flush=True)
+
+
+C5_TEMPORAL_GAMMA_SIGMA = (-0.25, 0.0, 0.25, 0.5, 1.0)
+C5_TEMPORAL_RHO = 0.95
+
+
+def c5_temporal(q, w, sets, flush, device) -> dict:
+    """C5 with block-64 temporal pruning, which skips key bytes: one decode
+    step of the four sequences from L-1 to L = 131072 fp8 keys (the last key
+    appended), the query drifting as AR(1) with rho 0.95 from the C5 query.
+    Teacher-forced as the reference's replay (replay.py:225-400): seeds = the
+    dense top-2048 of step L-1, U_b = its block maxima + gamma_sigma * sigma
+    (sigma = std of the score drift), static (address) and dynamic
+    (previous-hot, 22 threshold refreshes) scans.  Reports, per variant, the
+    median step time (eager, after a cache flush), the key bytes read
+    (keys scored x 128 + 128-key scales + 8 B of metadata per block) against
+    the dense step's, and Recall@K against the dense top-2048."""
+
+    import numpy as np
+    import torch
+
+    from dsa_amd import decode, temporal
+
+    block = 64
+    keys8, scales = sets[0]
+    gen = torch.Generator().manual_seed(SEED + 5)
+    q_prev = q.float().cpu()
+    q_now = (C5_TEMPORAL_RHO * q_prev + math.sqrt(1 - C5_TEMPORAL_RHO ** 2)
+             * torch.randn(q_prev.shape, generator=gen) / math.sqrt(128)).to(torch.bfloat16).to(device)
+    q_prev = q
+    prev_len = C5_LENGTH - 1
+    prev_top, prev_scores = decode.indexer_topk(q_prev, w, keys8[:, :prev_len], TOPK, key_scales=scales,
+                                                return_scores=True)
+    dense_top, dense = decode.indexer_topk(q_now, w, keys8, TOPK, key_scales=scales, return_scores=True)
+    sigma = (dense[:, :prev_len] - prev_scores).std(dim=1, unbiased=False)
+    prev_max = temporal.block_max(prev_scores, block)
+    nb = C5_LENGTH // block
+    truth = torch.zeros(C5_BATCH, C5_LENGTH, dtype=torch.bool, device=device)
+    truth.scatter_(1, dense_top, True)
+    dense_bytes = C5_LENGTH * 128 + (C5_LENGTH // 128) * 4
+    variants = []
+    stream = torch.cuda.current_stream(device)
+    # the dynamic scan refreshes after the largest wave the step's merge allows
+    # (k + wave * block <= 8192: 96 blocks, 22 refreshes per scan)
+    for method, order, wave in (("static", "address", 0), ("dynamic", "previous_hot", (8192 - TOPK) // block)):
+        for gs in C5_TEMPORAL_GAMMA_SIGMA:
+            gamma = gs * sigma
+
+            def run():
+                return temporal.temporal_step(q_now, w, keys8, prev_max, prev_len, prev_top, gamma, block_size=block,
+                                              method=method, scan_order=order, wave=max(wave, 1), key_scales=scales)
+
+            times = []
+            for it in range(12):
+                flush()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                step = run()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                if it >= 2:
+                    times.append(e0.elapsed_time(e1) * 1e3)
+            qk = step.qk_scored.double().cpu().numpy()
+            hits = truth.gather(1, step.topk).sum(dim=1).cpu().numpy()
+            read = qk * 128 + (C5_LENGTH // 128) * 4 + nb * 8
+            variants.append({
+                "method": method, "scan_order": order, "wave": wave, "gamma_sigma": gs,
+                "us_per_step": float(np.median(times)),
+                "key_bytes_skipped": float(np.mean(1.0 - read / dense_bytes)),
+                "qk_reduction": float(np.mean(1.0 - qk / C5_LENGTH)),
+                "recall": float(np.mean(hits / TOPK)),
+            })
+    eligible = [v for v in variants if v["recall"] >= 0.999]
+    best = max(eligible, key=lambda v: v["key_bytes_skipped"]) if eligible else None
+    return {"block_size": block, "rho": C5_TEMPORAL_RHO, "variants": variants, "best_at_recall_0.999": best}
 
 
 def c5_progressive(q, w, sets, dense_idx, flush, device) -> dict:

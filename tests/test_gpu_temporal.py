@@ -132,3 +132,49 @@ def test_temporal_step_fp8(device) -> None:
         assert int(step.qk_scored[b]) == trace.scored
         ev = trace.evaluated
         np.testing.assert_array_equal(step.scores[b].cpu().numpy()[ev], dense[b][ev])
+
+
+@pytest.mark.parametrize("method,order,wave,gamma_sigma",
+                         [("dynamic", "previous_hot", 64, -0.25), ("static", "address", 0, -3.0)])
+def test_temporal_step_fp8_c5_length(device, method, order, wave, gamma_sigma) -> None:
+    # The C5 length: 131072 fp8 keys (one appended), block 64 (2048 blocks),
+    # K=2048, against the oracle's filter on the dense GPU scores.
+    print(f"temporal fp8 C5 length {method}/{order} wave={wave}", flush=True)
+    batch, prev_length, length, k, block = 2, 131071, 131072, 2048, 64
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=131)
+    raw = keys.float()
+    blocks128 = math.ceil(length / 128)
+    scales = raw.reshape(batch, blocks128, 128 * 128).abs().amax(dim=2) / 448
+    keys8 = (raw / scales.repeat_interleave(128, dim=1)[..., None]).to(torch.float8_e4m3fn)
+    del raw
+    q_prev, q_cur, w, keys8, scales = q_prev.to(device), q_cur.to(device), w.to(device), keys8.to(device), scales.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys8[:, :prev_length].contiguous(), k,
+                                                 key_scales=scales[:, : math.ceil(prev_length / 128)].contiguous(),
+                                                 return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys8, k, key_scales=scales, return_scores=True)[1].cpu().numpy()
+    gamma = gamma_sigma * float(prev_scores.std())  # a negative margin, so that blocks are pruned
+    step = temporal.temporal_step(q_cur, w, keys8, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                  method=method, scan_order=order, wave=max(wave, 1), key_scales=scales)
+    seeds = prev_topk.cpu().numpy()
+    schedule, dynamic, _ = R.method_schedule(method, order)
+    pruned_any = False
+    for b in range(batch):
+        blocks = math.ceil(length / block)
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+        upper = R.upper_bounds(previous_max, float(np.float32(gamma)), prev_length, length, block)
+        hot = np.zeros(blocks, dtype=bool)
+        hot[seeds[b] // block] = True
+        scan = R.block_scan_order(schedule, upper, R.block_maxima(dense[b], block), hot)
+        current = dense[b].astype(np.float64)
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=dynamic,
+                             fixed_threshold=float(current[seeds[b]].min()), wave=wave if dynamic else 1)
+        np.testing.assert_array_equal(step.evaluated_blocks[b].cpu().numpy(), trace.kept)
+        assert int(step.qk_scored[b]) == trace.scored
+        ev = trace.evaluated
+        np.testing.assert_array_equal(step.scores[b].cpu().numpy()[ev], dense[b][ev])
+        masked = np.where(ev, dense[b], -np.inf).astype(np.float32)
+        assert step.topk[b].cpu().numpy().tolist() == T.topk_index_order(masked, k).tolist(), b
+        pruned_any |= not trace.kept.all()
+    assert pruned_any, "the negative margin pruned nothing"
