@@ -54,6 +54,9 @@ _SIGNATURES: dict[str, list] = {
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _p,
     ],
     "dsa_promote_blocks": [_p, _p, _p, _p, _i64, _p],
+    "dsa_progressive_scores_batched": [
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p,
+    ],
     "dsa_topk": [_p, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p, _p],
     "dsa_topk_long": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_topk_exact": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],

@@ -487,6 +487,29 @@ struct BlockArgs {
   int32_t compact;
 };
 
+// Sequence `seq` of a batched launch (grid.y = sequences of one length, all
+// arrays packed per sequence): every pointer moves to that sequence's rows.
+template <class KF>
+__device__ __forceinline__ BlockArgs sequence_args(BlockArgs a, int64_t seq, int block_size) {
+  if (seq == 0) return a;
+  const int64_t L = a.length;
+  const int64_t nb = (L + block_size - 1) / block_size;
+  a.q += seq * kHeads * kHeadDim;
+  a.w += seq * kHeads;
+  a.keys += seq * L * KF::kRowBytes;
+  if (a.scales) a.scales += seq * ((L + 127) / 128);
+  if (a.selected) a.selected += seq * kVerifierHeads;
+  if (a.remaining) a.remaining += seq * (kHeads - kVerifierHeads);
+  a.mask += seq * nb;
+  if (a.threshold) a.threshold += seq;
+  a.out_scores += seq * L;
+  if (a.out_indices) a.out_indices += seq * L;
+  if (a.accepted) a.accepted += seq * nb;
+  if (a.block_max) a.block_max += seq * nb;
+  if (a.counter) a.counter += seq;
+  return a;
+}
+
 template <class KF>
 __device__ __forceinline__ float key_scale(const float* scales, int key) {
   if constexpr (KF::kScaled) return scales[key >> 7];
@@ -494,7 +517,8 @@ __device__ __forceinline__ float key_scale(const float* scales, int key) {
 }
 
 template <class Tag, class KF, int MODE, int T>
-__global__ __launch_bounds__(256) void block_kernel(BlockArgs a) {
+__global__ __launch_bounds__(256) void block_kernel(BlockArgs args) {
+  const BlockArgs a = sequence_args<KF>(args, blockIdx.y, 16 * T);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
@@ -658,9 +682,9 @@ int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
 }
 
 template <class Tag, class KF, int MODE>
-int launch_block(const BlockArgs& a, int block_size, hipStream_t stream) {
+int launch_block(const BlockArgs& a, int block_size, hipStream_t stream, int64_t batch) {
   const int nb = (a.length + block_size - 1) / block_size;
-  dim3 grid((unsigned)((nb + 3) / 4));
+  dim3 grid((unsigned)((nb + 3) / 4), (unsigned)batch);
   switch (block_size) {
     case 16: hipLaunchKernelGGL((block_kernel<Tag, KF, MODE, 1>), grid, dim3(256), 0, stream, a); break;
     case 32: hipLaunchKernelGGL((block_kernel<Tag, KF, MODE, 2>), grid, dim3(256), 0, stream, a); break;
@@ -671,11 +695,11 @@ int launch_block(const BlockArgs& a, int block_size, hipStream_t stream) {
 }
 
 template <int MODE>
-int dispatch_block(BlockArgs& a, int block_size, int dtype, hipStream_t stream) {
+int dispatch_block(BlockArgs& a, int block_size, int dtype, hipStream_t stream, int64_t batch = 1) {
   switch (dtype) {
-    case kBF16: return launch_block<Bf16Tag, KeysB16, MODE>(a, block_size, stream);
-    case kF16: return launch_block<F16Tag, KeysB16, MODE>(a, block_size, stream);
-    case kFP8E4M3: return launch_block<Bf16Tag, KeysFP8, MODE>(a, block_size, stream);
+    case kBF16: return launch_block<Bf16Tag, KeysB16, MODE>(a, block_size, stream, batch);
+    case kF16: return launch_block<F16Tag, KeysB16, MODE>(a, block_size, stream, batch);
+    case kFP8E4M3: return launch_block<Bf16Tag, KeysFP8, MODE>(a, block_size, stream, batch);
     default:
       return fail(DSA_STATUS_INVALID_ARGUMENT, "block kernels take fp16/bf16/fp8 keys, got dtype %d",
                   dtype);
@@ -897,15 +921,14 @@ extern "C" int dsa_masked_full_scores(const void* queries, const float* weights,
   return dispatch_block<kModeMasked>(a, block_size, key_dtype, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int dsa_progressive_scores(const void* queries, const float* weights, const void* keys,
-                                      const float* key_scales, const int32_t* selected_heads,
-                                      const int32_t* remaining_heads,
-                                      const uint8_t* direct_blocks, const float* threshold,
-                                      float* out_scores, int32_t* out_indices, int8_t* accepted,
-                                      float* block_max, int32_t* counter, int64_t length,
-                                      int32_t block_size, int32_t compact, int32_t key_dtype,
-                                      void* stream) {
+static int progressive_scores(const void* queries, const float* weights, const void* keys, const float* key_scales,
+                              const int32_t* selected_heads, const int32_t* remaining_heads,
+                              const uint8_t* direct_blocks, const float* threshold, float* out_scores,
+                              int32_t* out_indices, int8_t* accepted, float* block_max, int32_t* counter,
+                              int64_t batch, int64_t length, int32_t block_size, int32_t compact, int32_t key_dtype,
+                              void* stream) {
   if (int st = check_block_common(queries, weights, keys, length, block_size)) return st;
+  DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(selected_heads && remaining_heads && direct_blocks && threshold && out_scores &&
                   accepted && block_max,
               "null pointer argument");
@@ -927,8 +950,32 @@ extern "C" int dsa_progressive_scores(const void* queries, const float* weights,
   a.counter = counter;
   a.length = (int32_t)length;
   a.compact = compact ? 1 : 0;
-  return dispatch_block<kModeProgressive>(a, block_size, key_dtype,
-                                          static_cast<hipStream_t>(stream));
+  return dispatch_block<kModeProgressive>(a, block_size, key_dtype, static_cast<hipStream_t>(stream), batch);
+}
+
+extern "C" int dsa_progressive_scores(const void* queries, const float* weights, const void* keys,
+                                      const float* key_scales, const int32_t* selected_heads,
+                                      const int32_t* remaining_heads,
+                                      const uint8_t* direct_blocks, const float* threshold,
+                                      float* out_scores, int32_t* out_indices, int8_t* accepted,
+                                      float* block_max, int32_t* counter, int64_t length,
+                                      int32_t block_size, int32_t compact, int32_t key_dtype,
+                                      void* stream) {
+  return progressive_scores(queries, weights, keys, key_scales, selected_heads, remaining_heads, direct_blocks,
+                            threshold, out_scores, out_indices, accepted, block_max, counter, 1, length, block_size,
+                            compact, key_dtype, stream);
+}
+
+extern "C" int dsa_progressive_scores_batched(const void* queries, const float* weights, const void* keys,
+                                              const float* key_scales, const int32_t* selected_heads,
+                                              const int32_t* remaining_heads, const uint8_t* direct_blocks,
+                                              const float* thresholds, float* out_scores, int32_t* out_indices,
+                                              int8_t* accepted, float* block_max, int32_t* counters, int64_t batch,
+                                              int64_t length, int32_t block_size, int32_t compact,
+                                              int32_t key_dtype, void* stream) {
+  return progressive_scores(queries, weights, keys, key_scales, selected_heads, remaining_heads, direct_blocks,
+                            thresholds, out_scores, out_indices, accepted, block_max, counters, batch, length,
+                            block_size, compact, key_dtype, stream);
 }
 
 extern "C" int dsa_promote_blocks(const uint8_t* direct_blocks, const float* block_max,

@@ -336,6 +336,77 @@ def progressive_scores_hip(
     return ProgressiveResult(scores, accepted, block_max, indices, candidate_count)
 
 
+def progressive_scores_batched(
+    queries: torch.Tensor,
+    weights: torch.Tensor,
+    keys: torch.Tensor,
+    selected_heads: torch.Tensor,
+    direct_full_blocks: torch.Tensor,
+    threshold: float | torch.Tensor,
+    *,
+    block_size: int = 64,
+    compact: bool = False,
+    key_scales: torch.Tensor | None = None,
+) -> ProgressiveResult:
+    """:func:`progressive_scores_hip` for ``B`` sequences of one length in
+    one launch (``dsa_progressive_scores_batched``).
+
+    queries ``[B, 64, 128]``, weights ``[B, 64]``, keys ``[B, L, 128]`` (fp8
+    with ``key_scales`` ``[B, ceil(L/128)]``), selected_heads ``[B, 8]`` (the
+    remaining 56 heads of each row are its complement), direct_full_blocks
+    ``[B, blocks]``, threshold a float or ``[B]`` tensor.  The result holds
+    ``[B, ...]`` tensors; in compact mode ``candidate_indices`` and ``scores``
+    are ``[B, L]`` with row b's first ``candidate_count[b]`` entries valid and
+    ``candidate_count`` is a device tensor ``[B]`` (no host synchronisation).
+    Row b equals :func:`progressive_scores_hip` on sequence b.
+    """
+
+    if queries.ndim != 3 or weights.ndim != 2 or keys.ndim != 3:
+        raise ValueError("expected queries [B,64,128], weights [B,64] and keys [B,L,128]")
+    batch = queries.shape[0]
+    if weights.shape[0] != batch or keys.shape[0] != batch:
+        raise ValueError("queries, weights and keys must share the batch size")
+    if key_scales is not None and (key_scales.ndim != 2 or key_scales.shape[0] != batch):
+        raise ValueError("key_scales must be [B, ceil(L/128)]")
+    scales = _check_gpu_inputs(queries[0], weights[0], keys[0],
+                               key_scales=None if key_scales is None else key_scales[0])
+    if scales is not None:
+        scales = key_scales.to(device=keys.device, dtype=torch.float32).contiguous()
+    _check_block_size(block_size)
+    if selected_heads.shape != (batch, VERIFIER_HEADS):
+        raise ValueError(f"selected_heads must be [{batch},{VERIFIER_HEADS}]")
+    pairs = [split_head_ids(selected_heads[b].cpu()) for b in range(batch)]
+    selected = torch.stack([p[0] for p in pairs]).to(device=keys.device, dtype=torch.int32).contiguous()
+    remaining = torch.stack([p[1] for p in pairs]).to(device=keys.device, dtype=torch.int32).contiguous()
+    length = keys.shape[1]
+    block_count = math.ceil(length / block_size)
+    if direct_full_blocks.shape != (batch, block_count):
+        raise ValueError(f"direct_full_blocks must be [{batch},{block_count}]")
+    queries = queries.contiguous()
+    keys = keys.contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    direct = direct_full_blocks.to(device=keys.device, dtype=torch.uint8).contiguous()
+    thresholds = torch.as_tensor(threshold, device=keys.device, dtype=torch.float32).reshape(-1)
+    if thresholds.numel() == 1:
+        thresholds = thresholds.expand(batch)
+    if thresholds.numel() != batch:
+        raise ValueError("threshold must be a float or one value per sequence")
+    thresholds = thresholds.contiguous()
+    accepted = torch.empty((batch, block_count), device=keys.device, dtype=torch.int8)
+    block_max = torch.empty((batch, block_count), device=keys.device, dtype=torch.float32)
+    counters = torch.zeros(batch, device=keys.device, dtype=torch.int32)
+    scores = torch.empty((batch, length), device=keys.device, dtype=torch.float32)
+    indices = torch.empty((batch, length), device=keys.device, dtype=torch.int32) if compact else None
+    _lib.call(
+        "dsa_progressive_scores_batched",
+        _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), _lib.ptr(scales), _lib.ptr(selected),
+        _lib.ptr(remaining), _lib.ptr(direct), _lib.ptr(thresholds), _lib.ptr(scores), _lib.ptr(indices),
+        _lib.ptr(accepted), _lib.ptr(block_max), _lib.ptr(counters), batch, length, block_size, int(compact),
+        _lib.dtype_code(keys.dtype), _lib.stream_of(keys),
+    )
+    return ProgressiveResult(scores, accepted, block_max, indices, counters if compact else None)
+
+
 def two_pass_scores_hip(
     queries: torch.Tensor,
     weights: torch.Tensor,

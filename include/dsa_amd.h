@@ -149,6 +149,23 @@ int dsa_progressive_scores(const void* queries, const float* weights, const void
                            float* block_max, int32_t* counter, int64_t length,
                            int32_t block_size, int32_t compact, int32_t key_dtype, void* stream);
 
+/* dsa_progressive_scores over `batch` sequences of one length in one launch
+ * (the reference's kernel takes one sequence, progressive_kernel.py:277-346):
+ * every array is packed per sequence -- queries [batch, 64, 128], weights
+ * [batch, 64], keys [batch, length, 128] (fp8 key_scales [batch,
+ * ceil(length / 128)]), selected_heads [batch, 8], remaining_heads
+ * [batch, 56], direct_blocks, accepted, block_max [batch, blocks],
+ * thresholds [batch] (device), out_scores and out_indices [batch, length],
+ * counters [batch] (zeroed by the caller for compact output).  Each sequence
+ * gives exactly what dsa_progressive_scores gives for it. */
+int dsa_progressive_scores_batched(const void* queries, const float* weights, const void* keys,
+                                   const float* key_scales, const int32_t* selected_heads,
+                                   const int32_t* remaining_heads, const uint8_t* direct_blocks,
+                                   const float* thresholds, float* out_scores, int32_t* out_indices,
+                                   int8_t* accepted, float* block_max, int32_t* counters, int64_t batch,
+                                   int64_t length, int32_t block_size, int32_t compact, int32_t key_dtype,
+                                   void* stream);
+
 /* accepted[b] = direct[b] || block_max[b] >= *threshold  (bytes 0/1).
  * Replaces the torch logical_or at progressive_kernel.py:493. */
 int dsa_promote_blocks(const uint8_t* direct_blocks, const float* block_max,

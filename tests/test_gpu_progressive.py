@@ -226,3 +226,50 @@ def test_rejects_bad_masks_and_heads(device) -> None:
         masked_full_scores_triton(queries, weights, keys, torch.zeros(1, dtype=torch.bool, device=device))
     with pytest.raises(ValueError):
         full_scores_triton(queries, weights, keys.float())
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("block_size,compact", [(16, False), (64, True), (128, False)])
+def test_batched_progressive_equals_per_sequence(device, fp8, block_size, compact) -> None:
+    # One launch over B sequences gives, row by row, exactly the single-
+    # sequence kernel's result (scores, decisions, block maxima, compact
+    # counts and candidates).
+    from dsa_amd.progressive_kernel import progressive_scores_batched
+
+    print(f"progressive batched fp8={fp8} bs={block_size} compact={compact}", flush=True)
+    batch, length = 3, 1000
+    gen = torch.Generator().manual_seed(block_size + 31 * fp8)
+    q = (torch.randn(batch, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(batch, 64, generator=gen) / 8
+    raw = torch.randn(batch, length, 128, generator=gen)
+    nscale = math.ceil(length / 128)
+    scales = None
+    if fp8:
+        scales = torch.stack([torch.stack([raw[b, j * 128 : (j + 1) * 128].abs().max() / 448 for j in range(nscale)])
+                              for b in range(batch)])
+        keys = (raw / scales.repeat_interleave(128, dim=1)[:, :length, None]).to(torch.float8_e4m3fn)
+    else:
+        keys = raw.to(torch.bfloat16)
+    blocks = math.ceil(length / block_size)
+    direct = torch.rand(batch, blocks, generator=gen) < 0.3
+    heads = torch.stack([dynamic_head_ids(w[b]) for b in range(batch)])
+    thresholds = torch.tensor([0.05, -1.0, 0.2])
+    dq, dw, dk = q.to(device), w.to(device), keys.to(device)
+    ds = scales.to(device) if fp8 else None
+    got = progressive_scores_batched(dq, dw, dk, heads, direct.to(device), thresholds.to(device),
+                                     block_size=block_size, compact=compact, key_scales=ds)
+    for b in range(batch):
+        one = progressive_scores_triton(dq[b], dw[b], dk[b], heads[b], direct[b].to(device), float(thresholds[b]),
+                                        block_size=block_size, compact=compact,
+                                        key_scales=ds[b] if fp8 else None)
+        assert torch.equal(got.accepted_blocks[b], one.accepted_blocks), b
+        assert torch.equal(got.block_max[b], one.block_max), b
+        if compact:
+            n = int(got.candidate_count[b])
+            assert n == one.candidate_count, b
+            order_g = torch.argsort(got.candidate_indices[b, :n])
+            order_o = torch.argsort(one.candidate_indices)
+            assert torch.equal(got.candidate_indices[b, :n][order_g], one.candidate_indices[order_o]), b
+            assert torch.equal(got.scores[b, :n][order_g], one.scores[order_o]), b
+        else:
+            assert torch.equal(got.scores[b], one.scores), b
