@@ -83,34 +83,91 @@ def make_inputs(device):
     return q, w, key_sets
 
 
+def host_cpu() -> dict:
+    """Host facts the CPU baseline is quoted with: online CPUs (nproc), the
+    CPUs this process may run on, and the processor model name."""
+
+    import os
+
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model}
+
+
+def _percentile(sorted_values, frac: float) -> float:
+    pos = frac * (len(sorted_values) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(sorted_values) - 1)
+    return sorted_values[lo] + (sorted_values[hi] - sorted_values[lo]) * (pos - lo)
+
+
 def cpu_baseline(q, w, keys, k: int, budget_s: float) -> tuple[dict, "object"]:
     """Oracle restatement of the reference CPU path: torch fp32 dense score
-    (reference progressive_kernel.py:45-55) + numpy stable_topk (metrics.py:9-22)."""
+    (reference progressive_kernel.py:45-55) + numpy stable_topk (metrics.py:9-22).
+
+    Protocol: one run = one sequence (L keys) scored + its stable top-K.  5
+    warm-up runs, then at least 20 timed runs (more while the budget lasts),
+    at all host threads this process may use and at 1 thread; median, p5 and
+    p95 of each, keys/s = L / median run time."""
 
     import torch
 
     from oracle import scores as S
     from oracle import topk as T
 
-    threads = torch.get_num_threads()
+    host = host_cpu()
+    # The GPU box caps a job's threads through OMP_NUM_THREADS; use that share
+    # (or every CPU this process may run on, when it is unset).
+    all_threads = min(int(os.environ.get("OMP_NUM_THREADS", host["affinity"])), host["affinity"])
     q0, w0, k0 = q[0].cpu(), w[0].cpu(), keys[0].cpu()
-    reps = 0
-    start = time.perf_counter()
+    saved = torch.get_num_threads()
     top = None
-    while True:
-        scores = S.torch_full_scores(q0, w0, k0)
-        top = T.stable_topk(scores.numpy(), k)
-        reps += 1
-        if time.perf_counter() - start >= budget_s and reps >= 3:
-            break
-    elapsed = time.perf_counter() - start
-    value = reps * LENGTH / elapsed / 1e9
+    legs = {}
+    try:
+        for name, threads in (("all", all_threads), ("one", 1)):
+            torch.set_num_threads(threads)
+            for _ in range(5):
+                top = T.stable_topk(S.torch_full_scores(q0, w0, k0).numpy(), k)
+            times = []
+            start = time.perf_counter()
+            while len(times) < 20 or time.perf_counter() - start < budget_s / 2:
+                t0 = time.perf_counter()
+                top = T.stable_topk(S.torch_full_scores(q0, w0, k0).numpy(), k)
+                times.append(time.perf_counter() - t0)
+                if len(times) >= 20 and time.perf_counter() - start >= budget_s / 2:
+                    break
+            times.sort()
+            med = _percentile(times, 0.5)
+            legs[name] = {
+                "threads": threads,
+                "runs": len(times),
+                "median_ms": round(med * 1e3, 3),
+                "p5_ms": round(_percentile(times, 0.05) * 1e3, 3),
+                "p95_ms": round(_percentile(times, 0.95) * 1e3, 3),
+                "g_keys_per_s": round(LENGTH / med / 1e9, 5),
+            }
+    finally:
+        torch.set_num_threads(saved)
     info = {
-        "value": value,
+        "value": legs["all"]["g_keys_per_s"],
         "unit": "G keys/s",
-        "cores": threads,
+        "cores": all_threads,
         "kind": "port",
-        "sample": f"{reps} x (1 sequence, L={LENGTH}, K={k}) scored + stable_topk in {elapsed:.1f} s",
+        "sample": f"1 sequence (L={LENGTH}, K={k}) scored + stable_topk per run; 5 warm-up + "
+                  f"{legs['all']['runs']} timed runs at {all_threads} threads, {legs['one']['runs']} at 1 thread; "
+                  f"value = L / median run",
+        "one_thread": legs["one"],
+        "all_threads": legs["all"],
+        "nproc": host["nproc"],
+        "affinity_cpus": host["affinity"],
+        "cpu_model": host["model"],
     }
     return info, top
 
@@ -674,7 +731,7 @@ def run_c4(args) -> None:
                    "top-512 per query over its visible keys, 8 independent layers", "causal_pairs": pairs},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "dense_scores_kernel<bf16, M=4> (multi-query, causal)",
+                     "kernel": "prefill_scores_kernel<bf16> (multi-query, causal, dsa_score_queries)",
                      "kernel_median_us": sc["median_us"], "flops": flops},
         "layer": {"step": st, "score": sc, "topk": time_stats(select_ms)},
         "timing": f"HIP events around one layer's launches, 512 MiB {args.flush} flush before each, median over 40",
