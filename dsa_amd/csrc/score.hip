@@ -7,6 +7,7 @@
 // accumulators in registers, so only the fp32 score leaves the kernel.
 #include "common.hpp"
 #include "indexer.hpp"
+#include "lists.hpp"
 #include "select.hpp"
 #include "status.hpp"
 #include "waveops.hpp"
@@ -158,30 +159,6 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
   }
 }
 
-// A scoring workgroup's candidate list: thread t takes keys [t * per, t * per
-// + per) of the chunk (per <= P), all read from LDS at once, and writes those
-// in bins >= lbin in index order at offsets from one block scan.
-template <int P, int kWaves>
-__device__ __forceinline__ uint32_t emit_list(const float* chunk_scores, int per, int n_chunk, int chunk_base,
-                                              uint32_t lbin, uint64_t* list, uint32_t* wsum) {
-  const int i0 = (int)threadIdx.x * per;
-  uint32_t key[P];
-  uint32_t takes = 0;  // bit e: key e is listed
-#pragma unroll
-  for (int e = 0; e < P; ++e) {
-    key[e] = float_to_ordered(chunk_scores[e < per ? i0 + e : i0]);
-    if (e < per && i0 + e < n_chunk && (key[e] >> 20) >= lbin) takes |= 1u << e;
-  }
-  uint32_t listed;
-  uint32_t slot = block_excl_scan<kWaves>((uint32_t)__builtin_popcount(takes), wsum, listed);
-  if (takes) {
-#pragma unroll
-    for (int e = 0; e < P; ++e)
-      if (takes & (1u << e)) list[slot++] = select_composite(key[e], (uint32_t)(chunk_base + i0 + e));
-  }
-  return listed;
-}
-
 template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists, int kWaves>
 __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores_kernel(DenseArgs a) {
   constexpr int kThreads = 64 * kWaves;
@@ -254,34 +231,9 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
       // chunk has no more), in index order.
       __shared__ uint32_t s_list_bin;
       __shared__ __align__(16) uint32_t s_list_wsum[kWaves];
-      const int n_chunk = min(chunk_keys, valid - chunk_base);
-      if (wave == 0) {
-        const Locate t = wave_locate<kSelectBins / kWave>(hist, (uint32_t)a.list_quota, true);
-        if (lane == 0) s_list_bin = t.digit == kNoBin ? 0u : t.digit;
-      }
-      __syncthreads();
-      const uint32_t lbin = s_list_bin;
-      uint64_t* list = a.lists + seq * (int64_t)L + chunk_base;
-      uint32_t listed;
-      const int per = chunk_keys / kThreads;  // keys per thread, 1..32
-      switch (per) {
-        case 1: listed = emit_list<1, kWaves>(chunk_scores, 1, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
-        case 2: listed = emit_list<2, kWaves>(chunk_scores, 2, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
-        case 3:
-        case 4: listed = emit_list<4, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
-        case 5: case 6: case 7:
-        case 8: listed = emit_list<8, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum); break;
-        case 9: case 10: case 11: case 12: case 13: case 14: case 15:
-        case 16: listed = emit_list<16, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum);
-          break;
-        default: listed = emit_list<32, kWaves>(chunk_scores, per, n_chunk, chunk_base, lbin, list, s_list_wsum);
-          break;
-      }
-      if (threadIdx.x == 0) {
-        uint32_t* meta = a.list_meta + 2 * (seq * kMaxListChunks + chunk);
-        meta[0] = listed;
-        meta[1] = lbin;
-      }
+      write_chunk_list<kWaves>(hist, chunk_scores, chunk_keys, min(chunk_keys, valid - chunk_base), chunk_base,
+                               (uint32_t)a.list_quota, a.lists + seq * (int64_t)L + chunk_base,
+                               a.list_meta + 2 * (seq * kMaxListChunks + chunk), &s_list_bin, s_list_wsum);
       return;
     }
     // All sixteen LDS reads first, then the atomics for the bins in use: one

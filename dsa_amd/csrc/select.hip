@@ -101,14 +101,6 @@ __device__ __forceinline__ uint64_t radix_cut(uint32_t bin, uint32_t want, uint3
   return prefix;  // all 64 bits fixed
 }
 
-// Same XCD-aware renumbering as the scoring kernel: with a grid that is a
-// multiple of 8, a row's chunks run on one XCD, whose L2 holds its scores.
-__device__ __forceinline__ uint32_t logical_block() {
-  const uint32_t grid = gridDim.x;
-  const uint32_t b = blockIdx.x;
-  return (grid % 8u == 0u) ? (b % 8u) * (grid / 8u) + b / 8u : b;
-}
-
 // ---------------------------------------------------------------------------
 // gather: one workgroup per (row, chunk).
 // ---------------------------------------------------------------------------
@@ -410,6 +402,8 @@ struct ListArgs {
   uint32_t total_wgs;       // rows * chunks (the grid is padded to a multiple of 8)
   int64_t* out_idx;         // [rows, k]
   float* out_val;           // [rows, k] or null
+  const uint32_t* count_parts;  // [rows * chunks] or null: per-chunk counts summed into count_out
+  int32_t* count_out;           // [rows]
 };
 
 struct ListShared {
@@ -440,6 +434,12 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
   const uint32_t kk = (uint32_t)a.k;
   const float* srow = a.scores + (size_t)row * n;
   const uint64_t* lrow = a.lists + (size_t)row * n;
+  if (a.count_parts && c == 0 && wave == 0) {
+    uint32_t sum = 0;
+    for (uint32_t j = lane; j < chunks; j += kWave) sum += a.count_parts[(size_t)row * chunks + j];
+    for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+    if (lane == 0) a.count_out[row] = (int32_t)sum;
+  }
 
   // This thread's list j and its place r among the list's threads.
   const uint32_t tpl = chunks >= (uint32_t)kSelThreads ? 1u : (uint32_t)kSelThreads / chunks;
@@ -732,8 +732,11 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
 
 int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64_t k,
                         const ListPlan& plan, const SelectWorkspace& ws, int64_t* out_idx,
-                        float* out_val, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+                        float* out_val, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                        const uint32_t* count_parts, int32_t* count_out) {
   ListArgs a;
+  a.count_parts = count_parts;
+  a.count_out = count_out;
   a.scores = scores;
   a.lists = ws.cand;
   a.meta = ws.list_meta;

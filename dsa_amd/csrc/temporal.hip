@@ -24,6 +24,9 @@
 // blocks load no key bytes.
 #include "temporal.hpp"
 
+#include <cstdlib>
+#include <cstring>
+
 #include "status.hpp"
 
 namespace dsa {
@@ -657,8 +660,20 @@ int launch_scan(TemporalArgs& a, int32_t wave, hipStream_t stream) {
   return DSA_STATUS_OK;
 }
 
+// DSA_AMD_TEMPORAL_PATH=launch keeps static steps on the multi-launch path
+// (prep, seeds, blocks, histogram select), for comparisons.
+bool fused_static_enabled() {
+  const char* v = std::getenv("DSA_AMD_TEMPORAL_PATH");
+  return !(v && std::strcmp(v, "launch") == 0);
+}
+
 int run_step(TemporalArgs& a, int32_t wave, int32_t key_dtype, int64_t* out_topk, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (wave == 0 && fused_static_enabled()) {
+    bool ran = false;
+    if (int st = temporal_static_fused(a, key_dtype, out_topk, s, ran)) return st;
+    if (ran) return DSA_STATUS_OK;
+  }
   if (int st = temporal_scan(a, wave, key_dtype, s)) return st;
   return temporal_finish(a, out_topk, nullptr, s);
 }

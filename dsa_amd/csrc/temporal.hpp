@@ -19,7 +19,15 @@ constexpr int kMaxMerge = 8192;            // k + one wave's keys, merged in LDS
 constexpr uint32_t kFarKey = 0x00ffffffu;  // a key index whose rows lie past every buffer
 constexpr int kDigitBinsT = 2048;          // 11-bit radix digits of the threshold refresh
 
+// Workgroups of the fused static step (temporal_fused.hip): one exchange slot
+// and one scored-key count each, at fixed offsets at the start of the
+// workspace so that they do not move with the step's shape.
+constexpr int kMaxFusedWgs = 4096;
+
 struct TemporalWorkspace {
+  uint64_t* slots;      // [kMaxFusedWgs] (generation << 32) | least seed key of each fused workgroup; zero
+                        // before the workspace's first use
+  uint32_t* qk_parts;   // [kMaxFusedWgs] keys each fused workgroup scored
   uint32_t* tau;        // [rows] ordered key of the threshold in force
   uint32_t* run;        // [rows][k] ordered keys of the k largest evaluated scores
   uint32_t* order;      // [rows][blocks] block ids in scan order
@@ -32,7 +40,9 @@ struct TemporalWorkspace {
 inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t length, int64_t k, int32_t block_size) {
   const int64_t blocks = (length + block_size - 1) / block_size;
   auto round = [](int64_t bytes) { return (bytes + 255) / 256 * 256; };
-  const int64_t tau_off = 0;
+  const int64_t slots_off = 0;
+  const int64_t parts_off = slots_off + kMaxFusedWgs * 8;
+  const int64_t tau_off = parts_off + kMaxFusedWgs * 4;
   const int64_t run_off = tau_off + round(rows * 4);
   const int64_t order_off = run_off + round(rows * k * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
@@ -42,6 +52,8 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   const uintptr_t p = reinterpret_cast<uintptr_t>(base);
   ws.select = select_workspace_layout(base ? reinterpret_cast<void*>(p + select_off) : nullptr, rows, length);
   ws.bytes = select_off + round(ws.select.bytes);
+  ws.slots = base ? reinterpret_cast<uint64_t*>(p + slots_off) : nullptr;
+  ws.qk_parts = base ? reinterpret_cast<uint32_t*>(p + parts_off) : nullptr;
   ws.tau = base ? reinterpret_cast<uint32_t*>(p + tau_off) : nullptr;
   ws.run = base ? reinterpret_cast<uint32_t*>(p + run_off) : nullptr;
   ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
@@ -227,6 +239,13 @@ int temporal_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t 
 // top-k of the scores row into out_topk, and (policy mode) the state update
 // of every block refreshed by the scan or flagged in `rescued` (may be null).
 int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, hipStream_t stream);
+
+// The static replay-filter step (wave 0, no policy, live keys) as one
+// scoring launch plus the candidate-list select.  Returns
+// DSA_STATUS_OK with `ran` false, launching nothing, when the step's shape
+// does not fit that path (the caller then runs temporal_scan and
+// temporal_finish).
+int temporal_static_fused(TemporalArgs& a, int32_t key_dtype, int64_t* out_topk, hipStream_t stream, bool& ran);
 
 // Shared argument checks of the step entry points.
 int check_step(const void* queries, const void* keys, int64_t key_stride, const float* key_scales,

@@ -1,0 +1,374 @@
+// The static replay-filter step in one scoring launch.
+//
+// With a fixed threshold (wave 0: the reference's static filter,
+// replay.py:172-222 with the threshold never refreshed) a block's fate does
+// not depend on the scan order: block b is kept iff !(U_b < tau), tau being
+// the least score of the previous step's top-k (the seeds).  The step is then
+// a dense decode step whose workgroups skip the keys of pruned blocks:
+//
+//  1. each workgroup owns one chunk of a row's keys (the candidate-list plan
+//     of the decode step) and scores the seeds that fall inside it, loading
+//     only those key rows;
+//  2. it publishes the least of them in its own exchange slot, stamped with
+//     the call's generation, and waits until every workgroup of the row has
+//     published; tau is the least over the row's slots;
+//  3. it decides its blocks against tau and streams its units with the key
+//     rows of pruned blocks replaced by an out-of-range offset (no memory
+//     access), writing kept keys' scores, seeds' scores and -inf elsewhere;
+//  4. its candidate list goes to the decode step's list select, which also
+//     totals the keys scored.
+//
+// The only data that crosses workgroups inside the launch is the slots, each
+// a 64-bit atomic written once per call; nothing else needs ordering.  The
+// grid is launched only when all of it fits on the device at once (at most
+// the occupancy limit times the CU count), so every workgroup a row waits for
+// becomes resident once the work ahead of it on the stream drains.  The wait
+// is also bounded: a workgroup that gives up keeps every block of its chunk
+// (a superset, visible in qk_scored) and the kernel still ends.  (A
+// cooperative launch would promise residency outright, but costs ~20 us of
+// host-side setup per call here.)
+//
+// Scores use the dense kernel's tile code (indexer.hpp), so an evaluated key
+// gets the dense score bit for bit.
+#include <atomic>
+#include <mutex>
+
+#include "lists.hpp"
+#include "status.hpp"
+#include "temporal.hpp"
+
+namespace dsa {
+namespace {
+
+constexpr int kFusedWaves = kDecodeWaves;
+constexpr int kFusedThreads = 64 * kFusedWaves;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every unit resource
+constexpr uint32_t kSpinLimit = 1u << 22;      // polls (each ~1 us) before a workgroup stops waiting
+
+struct FusedPlan {
+  int32_t chunk_keys;
+  int32_t chunks;  // per row
+  uint32_t quota;
+  uint32_t total_wgs;
+  uint32_t gen;
+};
+
+template <class Tag, class KF>
+__global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(TemporalArgs a, FusedPlan p) {
+  __shared__ uint32_t hist[kSelectBins];
+  __shared__ uint32_t seed_bits[kListChunkMax / 32];   // seeds of the chunk
+  __shared__ uint16_t seed_list[kListChunkMax];         // the same, as chunk-local positions
+  __shared__ uint32_t s_nseeds;
+  __shared__ uint32_t tile_bits[kListChunkMax / 512];  // 16-key tiles of the chunk's kept blocks
+  __shared__ uint32_t s_least, s_tau, s_count, s_list_bin;
+  __shared__ __align__(16) uint32_t s_wsum[kFusedWaves];
+  extern __shared__ float chunk_scores[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const uint32_t logical = logical_block();
+  if (logical >= p.total_wgs) return;
+  const int row = (int)(logical / (uint32_t)p.chunks);
+  const int c = (int)(logical % (uint32_t)p.chunks);
+  const int L = a.length;
+  const int base = c * p.chunk_keys;
+  const int n_chunk = min(p.chunk_keys, L - base);
+  const int units = (n_chunk + 63) >> 6;
+  const int bs = a.block_size;
+
+  for (int i = tid; i < kSelectBins; i += kFusedThreads) hist[i] = 0;
+  for (int i = tid; i < kListChunkMax / 32; i += kFusedThreads) seed_bits[i] = 0;
+  if (tid < kListChunkMax / 512) tile_bits[tid] = 0;
+  if (tid == 0) {
+    s_least = 0xffffffffu;
+    s_count = 0;
+    s_nseeds = 0;
+  }
+  uint4 qa[4][4];
+  float wr[4][4];
+  load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads, r, g,
+                                          qa, wr);
+  // The bounds of the chunk's blocks (at most 512: two per thread), loaded
+  // now so that the decisions after the exchange need no memory round trip.
+  const int first_new = a.prev_length / bs;
+  const bool grown = a.prev_length < L;
+  const int b_first = base / bs;
+  const int b_end = (base + n_chunk + bs - 1) / bs;
+  double upper[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = b_first + tid + kFusedThreads * j;
+    upper[j] = HUGE_VAL;
+    if (b < b_end && !(grown && b >= first_new)) {
+      const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
+      const double margin = a.margins ? a.margins[(size_t)row * a.prev_blocks + min(b, a.prev_blocks - 1)]
+                                      : (a.gamma_d ? a.gamma_d[row] : (double)a.gamma[row]);
+      upper[j] = (double)pm + margin;
+    }
+  }
+
+  __syncthreads();
+  const int64_t* seeds = a.seeds + (size_t)row * a.k;
+  for (int i0 = 0; i0 < a.k; i0 += 8 * kFusedThreads) {  // eight loads in flight per thread
+    int64_t key[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + tid + kFusedThreads * j;
+      key[j] = i < a.k ? seeds[i] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (key[j] >= base && key[j] < base + n_chunk) {
+        const uint32_t bit = 1u << (key[j] & 31);
+        const uint32_t was = __hip_atomic_fetch_or(&seed_bits[(key[j] - base) >> 5], bit, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (!(was & bit))  // listed once, even if the caller repeats a seed
+          seed_list[__hip_atomic_fetch_add(&s_nseeds, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] =
+              (uint16_t)(key[j] - base);
+      }
+  }
+  __syncthreads();
+
+  const uint8_t* row_keys = a.keys + (size_t)row * a.key_stride * KF::kRowBytes;
+  const int valid_bytes = L * KF::kRowBytes;  // below 2^31 (L <= 131072)
+  const float* row_scales = KF::kScaled ? a.scales + (size_t)row * ((a.key_stride + 127) / 128) : nullptr;
+  uint32_t loff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) loff[t] = KF::lane_offset(t, r, g);
+  // Unit ul of the chunk through its own resource, tile t loaded iff bit t of
+  // `tiles` (else an offset past the resource: zeros, no memory access).
+  auto load_unit = [&](int ul, uint32_t tiles, uint4 (&buf)[4][KF::kRaw]) {
+    const int ub = (base + 64 * ul) * KF::kRowBytes;
+    const BufferRsrc unit = make_buffer(row_keys + ub, (uint32_t)max(valid_bytes - ub, 0));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) KF::load_at(unit, ((tiles >> t) & 1u) ? loff[t] : kOutOfRange, buf[t]);
+  };
+  // Lane l's score of key l of the unit.
+  auto score_of = [&](int ul, const uint4 (&buf)[4][KF::kRaw]) {
+    float s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[t]);
+    float v = unit_reduce(s, g);
+    if constexpr (KF::kScaled) v *= row_scales[(base + 64 * ul + lane) >> 7];
+    return v;
+  };
+
+  // 1. The chunk's seeds, gathered 64 per wave-tile so that every wave's
+  // loads are in flight together: only their key rows are loaded.
+  uint32_t least = 0xffffffffu;
+  {
+    const uint32_t n_seeds = s_nseeds;
+    const BufferRsrc row_rsrc = make_buffer(row_keys, (uint32_t)valid_bytes);
+    constexpr int kPerWave = 2;  // gathered tiles a wave loads before scoring them
+    for (uint32_t e0 = 64u * kPerWave * wave; e0 < n_seeds; e0 += 64u * kPerWave * kFusedWaves) {
+      uint4 buf[kPerWave][4][KF::kRaw];
+#pragma unroll
+      for (int q = 0; q < kPerWave; ++q)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t e = e0 + 64u * q + 16u * t + (uint32_t)r;
+          const int key = e < n_seeds ? base + (int)seed_list[e] : (int)kFarKey;
+          KF::load_buf(row_rsrc, key, g, buf[q][t]);
+        }
+#pragma unroll
+      for (int q = 0; q < kPerWave; ++q) {
+        const uint32_t e = e0 + 64u * q + (uint32_t)lane;  // lane l holds entry e0 + 64q + l
+        float sc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[q][t]);
+        float v = unit_reduce(sc, g);
+        if (e < n_seeds) {
+          const int local = seed_list[e];
+          if constexpr (KF::kScaled) v *= row_scales[(base + local) >> 7];
+          chunk_scores[local] = v;
+          least = min(least, float_to_ordered(v));
+        }
+      }
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) least = min(least, (uint32_t)__shfl_xor((int)least, off, kWave));
+  if (lane == 0 && least != 0xffffffffu)
+    __hip_atomic_fetch_min(&s_least, least, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+
+  // 2. Exchange: publish this chunk's least seed key, then wait for the row's.
+  uint64_t* slots = a.ws.slots;
+  if (tid == 0)
+    __hip_atomic_store(&slots[logical], ((uint64_t)p.gen << 32) | s_least, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  if (wave == 0) {
+    const uint32_t first = (uint32_t)row * (uint32_t)p.chunks;
+    uint32_t tau = float_to_ordered(-__builtin_inff());  // if the wait gives up: keep every block
+    for (uint32_t it = 0; it < kSpinLimit; ++it) {
+      bool ready = true;
+      uint32_t mn = 0xffffffffu;
+      for (int j = lane; j < p.chunks; j += kWave) {
+        const uint64_t v = __hip_atomic_load(&slots[first + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ready = ready && (uint32_t)(v >> 32) == p.gen;
+        mn = min(mn, (uint32_t)v);
+      }
+      if (__ballot(!ready) == 0) {
+        for (int off = 32; off > 0; off >>= 1) mn = min(mn, (uint32_t)__shfl_xor((int)mn, off, kWave));
+        tau = mn;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (lane == 0) s_tau = tau;
+  }
+  __syncthreads();
+
+  // 3. Decisions for the chunk's blocks (whole blocks: chunks are multiples
+  // of 256 keys), their flags, and the keys scored.
+  const double bound = (double)ordered_to_float(s_tau);
+  uint32_t count = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = b_first + tid + kFusedThreads * j;
+    if (b >= b_end) continue;
+    const bool keep = !(upper[j] < bound);
+    a.evaluated[(size_t)row * a.blocks + b] = keep ? 1 : 0;
+    const int k0 = b * bs;
+    const int k1 = min(L, k0 + bs);
+    for (int key = k0; key < k1; key += 16) {  // 16-key tiles
+      const int t = (key - base) >> 4;
+      if (keep) {
+        __hip_atomic_fetch_or(&tile_bits[t >> 5], 1u << (t & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        count += (uint32_t)min(16, k1 - key);
+      } else {
+        uint32_t bits = (seed_bits[t >> 1] >> (16 * (t & 1))) & 0xffffu;
+        if (k1 - key < 16) bits &= (1u << (k1 - key)) - 1u;
+        count += (uint32_t)__builtin_popcount(bits);
+      }
+    }
+  }
+  if (count) __hip_atomic_fetch_add(&s_count, count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+  if (tid == 0) a.ws.qk_parts[logical] = s_count;
+
+  // 4. The chunk's scores: kept tiles scored, the rest -inf but for seeds.
+  // Units stream through a ring of KF::kBuffers register buffers as in the
+  // dense kernel (the unit kBuffers - 1 ahead is always in flight; past the
+  // wave's last unit the prefetch repeats that unit).
+  const BufferRsrc out = make_buffer(a.scores + (size_t)row * L, (uint32_t)L * 4u);
+  const int count_units = units > wave ? (units - wave + kFusedWaves - 1) / kFusedWaves : 0;
+  auto tiles_of = [&](int ul) {
+    return __builtin_amdgcn_readfirstlane((tile_bits[ul >> 3] >> (4 * (ul & 7))) & 0xfu);
+  };
+  auto finish_unit = [&](int ul, const uint4 (&buf)[4][KF::kRaw]) {
+    const uint32_t tiles = tiles_of(ul);
+    float v = 0.f;
+    if (tiles) v = score_of(ul, buf);
+    const uint32_t word = seed_bits[2 * ul + (lane >> 5)];
+    const bool seed = (word >> (lane & 31)) & 1u;
+    const bool kept = (tiles >> (lane >> 4)) & 1u;
+    const int local = 64 * ul + lane;
+    const float s = kept ? v : (seed ? chunk_scores[local] : -__builtin_inff());
+    buffer_store_f32(out, (uint32_t)(base + local) * 4u, s);  // stores past L are dropped
+    chunk_scores[local] = s;
+    if (base + local < L)
+      __hip_atomic_fetch_add(&hist[float_to_ordered(s) >> 20], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  if (count_units > 0) {
+    constexpr int NB = KF::kBuffers;
+    const int last = wave + kFusedWaves * (count_units - 1);
+    uint4 buf[NB][4][KF::kRaw];
+#pragma unroll
+    for (int s = 0; s < NB - 1; ++s) {
+      const int ul = min(wave + kFusedWaves * s, last);
+      load_unit(ul, tiles_of(ul), buf[s]);
+    }
+    for (int i = 0; i < count_units; i += NB) {
+#pragma unroll
+      for (int s = 0; s < NB; ++s) {
+        if (i + s >= count_units) break;
+        const int ahead = min(wave + kFusedWaves * (i + s + NB - 1), last);
+        load_unit(ahead, tiles_of(ahead), buf[(s + NB - 1) % NB]);
+        __builtin_amdgcn_sched_barrier(0);
+        finish_unit(wave + kFusedWaves * (i + s), buf[s]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // 5. The chunk's candidate list for the list select.
+  write_chunk_list<kFusedWaves>(hist, chunk_scores, p.chunk_keys, n_chunk, base, p.quota,
+                                a.ws.select.cand + (size_t)row * L + base,
+                                a.ws.select.list_meta + 2 * ((size_t)row * kMaxListChunks + c), &s_list_bin, s_wsum);
+}
+
+std::atomic<uint32_t> g_generation{0};
+
+// Workgroups of one temporal_static_kernel instance resident at once on the
+// current device (cached per device and instance).
+template <class Tag, class KF>
+int resident_capacity(size_t lds, int64_t& capacity) {
+  static std::mutex mutex;
+  static int64_t cached[64] = {};
+  static size_t cached_lds[64] = {};
+  int device = 0;
+  if (int st = check_hip(hipGetDevice(&device), "hipGetDevice")) return st;
+  if (device < 0 || device >= 64) return fail(DSA_STATUS_INVALID_ARGUMENT, "device %d out of range", device);
+  std::lock_guard<std::mutex> lock(mutex);
+  if (cached[device] == 0 || cached_lds[device] != lds) {
+    int per_cu = 0;
+    int cus = 0;
+    if (int st = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                               &per_cu, reinterpret_cast<const void*>(&temporal_static_kernel<Tag, KF>),
+                               kFusedThreads, lds),
+                           "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
+      return st;
+    if (int st = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                           "hipDeviceGetAttribute"))
+      return st;
+    cached[device] = (int64_t)per_cu * cus;
+    cached_lds[device] = lds;
+  }
+  capacity = cached[device];
+  return DSA_STATUS_OK;
+}
+
+template <class Tag, class KF>
+int launch_static(TemporalArgs& a, const ListPlan& plan, hipStream_t stream, bool& ran) {
+  const int64_t total = (int64_t)a.rows * plan.chunks;
+  const int64_t grid = (total + kXcds - 1) / kXcds * kXcds;
+  const size_t lds = (size_t)plan.chunk_keys * sizeof(float);
+  int64_t capacity = 0;
+  if (int st = resident_capacity<Tag, KF>(lds, capacity)) return st;
+  if (total > kMaxFusedWgs || grid > capacity) return DSA_STATUS_OK;  // not resident at once: the launch path
+  FusedPlan p;
+  p.chunk_keys = plan.chunk_keys;
+  p.chunks = plan.chunks;
+  p.quota = (uint32_t)plan.quota;
+  p.total_wgs = (uint32_t)total;
+  uint32_t gen = 0;
+  while (gen == 0) gen = ++g_generation;  // 0 never names a call (a zeroed slot)
+  p.gen = gen;
+  hipLaunchKernelGGL((temporal_static_kernel<Tag, KF>), dim3((unsigned)grid), dim3(kFusedThreads), (uint32_t)lds,
+                     stream, a, p);
+  if (int st = check_launch("temporal_static_kernel")) return st;
+  ran = true;
+  return DSA_STATUS_OK;
+}
+
+}  // namespace
+
+int temporal_static_fused(TemporalArgs& a, int32_t key_dtype, int64_t* out_topk, hipStream_t stream, bool& ran) {
+  ran = false;
+  if (a.policy_mode != 0 || a.source) return DSA_STATUS_OK;
+  const ListPlan plan = list_plan(a.rows, a.length, a.k);
+  if (!plan.on) return DSA_STATUS_OK;
+  int st;
+  switch (key_dtype) {
+    case DSA_DTYPE_BF16: st = launch_static<Bf16Tag, KeysB16>(a, plan, stream, ran); break;
+    case DSA_DTYPE_F16: st = launch_static<F16Tag, KeysB16>(a, plan, stream, ran); break;
+    default: st = launch_static<Bf16Tag, KeysFP8>(a, plan, stream, ran); break;
+  }
+  if (st || !ran) return st;
+  return launch_select_lists(a.scores, a.rows, a.length, a.k, plan, a.ws.select, out_topk, nullptr, stream, nullptr,
+                             nullptr, a.ws.qk_parts, a.qk_scored);
+}
+
+}  // namespace dsa

@@ -11,6 +11,14 @@ constexpr uint32_t kNoBin = 0xffffffffu;
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (kWave - 1); }
 
+// Same XCD-aware renumbering as the scoring kernel: with a grid that is a
+// multiple of 8, a row's chunks run on one XCD, whose L2 holds its scores.
+__device__ __forceinline__ uint32_t logical_block() {
+  const uint32_t grid = gridDim.x;
+  const uint32_t b = blockIdx.x;
+  return (grid % 8u == 0u) ? (b % 8u) * (grid / 8u) + b / 8u : b;
+}
+
 // Inclusive scan over the 64 lanes: DPP row shifts within 16-lane rows, then
 // the row totals read off lanes 15, 31 and 47.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {

@@ -45,10 +45,12 @@ class TemporalStep:
 
 def _workspace(device, stream, batch, length, k, block_size) -> torch.Tensor:
     """Workspace shared by the temporal, own-trajectory and verifier steps on
-    one stream (no zero-fill needed: the steps clear what they use)."""
+    one stream.  Zero-filled when allocated: the fused static step's exchange
+    slots (a fixed region at its start, the same for every shape) must not
+    hold a stamp of a later call; the steps clear everything else they use."""
 
     need = int(_lib.query("dsa_temporal_workspace_bytes", batch, length, k, block_size))
-    return _lib.workspace("temporal", device, stream, need, zeroed=False)
+    return _lib.workspace("temporal", device, stream, need, zeroed=True, rows=0)
 
 
 def temporal_step(
@@ -125,7 +127,10 @@ def temporal_step(
     elif queries.dtype not in (torch.float16, torch.bfloat16) or keys.dtype != queries.dtype:
         raise ValueError("queries and keys must share FP16/BF16 dtype")
     device = keys.device
-    gamma_t = torch.as_tensor(gamma, dtype=torch.float32, device=device).reshape(-1)
+    if isinstance(gamma, torch.Tensor):
+        gamma_t = gamma.to(device=device, dtype=torch.float32).reshape(-1)
+    else:  # a number: filled on the device (a host tensor would be copied with a synchronising transfer)
+        gamma_t = torch.full((batch,), float(gamma), dtype=torch.float32, device=device)
     if gamma_t.numel() == 1:
         gamma_t = gamma_t.expand(batch)
     if gamma_t.numel() != batch:

@@ -178,3 +178,72 @@ def test_temporal_step_fp8_c5_length(device, method, order, wave, gamma_sigma) -
         assert step.topk[b].cpu().numpy().tolist() == T.topk_index_order(masked, k).tolist(), b
         pruned_any |= not trace.kept.all()
     assert pruned_any, "the negative margin pruned nothing"
+
+
+STATIC_CASES = [
+    # block, gamma_sigma (negative: blocks are pruned), prev length, length, k, dtype
+    (16, -1.0, 16384, 16385, 2048, torch.bfloat16),
+    (16, -4.0, 16384, 16385, 2048, torch.bfloat16),
+    (32, -3.0, 16384, 16385, 2048, torch.float16),
+    (64, -3.0, 5000, 5003, 300, torch.bfloat16),
+    (128, -5.0, 16384, 16400, 2048, torch.bfloat16),
+    (64, 0.25, 16384, 16385, 2048, torch.bfloat16),
+    (16, -3.0, 100, 100, 40, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("block,gamma_sigma,prev_length,length,k,dtype", STATIC_CASES)
+def test_static_step_paths_agree(device, monkeypatch, block, gamma_sigma, prev_length, length, k, dtype) -> None:
+    # The static filter (fixed seed threshold) runs as one cooperative scoring
+    # launch + the list select; DSA_AMD_TEMPORAL_PATH=launch runs it on the
+    # prep / seed / block / histogram-select launches.  Both must equal the
+    # oracle's filter, and each other bit for bit, also when pruned blocks
+    # hold seeds.
+    print(f"static paths bs={block} gs={gamma_sigma} L={prev_length}->{length} k={k} {dtype}", flush=True)
+    batch = 3
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=block + length)
+    q_prev, q_cur, keys = q_prev.to(dtype), q_cur.to(dtype), keys.to(dtype)
+    q_prev, q_cur, w, keys = q_prev.to(device), q_cur.to(device), w.to(device), keys.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys[:, :prev_length].contiguous(), k, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys, k, return_scores=True)[1].cpu().numpy()
+    gamma = torch.full((batch,), gamma_sigma * float(prev_scores.std()), device=device)
+
+    def run():
+        s = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                   method="static")
+        return (s.scores.cpu().numpy(), s.evaluated_blocks.cpu().numpy(), s.qk_scored.cpu().numpy(),
+                s.topk.cpu().numpy())
+
+    fused = run()
+    monkeypatch.setenv("DSA_AMD_TEMPORAL_PATH", "launch")
+    launch = run()
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_PATH")
+    again = run()  # the fused path a second time on the same workspace (a new generation)
+    for name, a, b, c in zip(("scores", "kept", "qk", "topk"), fused, launch, again):
+        np.testing.assert_array_equal(a, b, err_msg=f"fused vs launch path: {name}")
+        np.testing.assert_array_equal(a, c, err_msg=f"fused, second call: {name}")
+    scores, kept, qk, topk = fused
+    seeds = prev_topk.cpu().numpy()
+    blocks = math.ceil(length / block)
+    seeds_in_pruned = 0
+    for b in range(batch):
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+        upper = R.upper_bounds(previous_max, float(gamma[b]), prev_length, length, block)
+        scan = R.block_scan_order("address", upper, R.block_maxima(dense[b], block), np.zeros(blocks, dtype=bool))
+        current = dense[b].astype(np.float64)
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=False,
+                             fixed_threshold=float(current[seeds[b]].min()), wave=1)
+        np.testing.assert_array_equal(kept[b], trace.kept, err_msg=f"row {b}: kept blocks")
+        assert int(qk[b]) == trace.scored, (b, int(qk[b]), trace.scored)
+        ev = trace.evaluated
+        np.testing.assert_array_equal(scores[b][ev], dense[b][ev])
+        assert np.isneginf(scores[b][~ev]).all()
+        masked = np.where(ev, dense[b], -np.inf).astype(np.float32)
+        assert topk[b].tolist() == T.topk_index_order(masked, k).tolist(), b
+        seeds_in_pruned += int((~trace.kept[seeds[b] // block]).sum())
+    if gamma_sigma <= -3.0:
+        assert not kept.all(), "the negative margin pruned nothing"
+    if gamma_sigma <= -4.0:  # below the seeds' own drift: blocks holding seeds are pruned too
+        assert seeds_in_pruned > 0, "no pruned block holds a seed"
