@@ -183,3 +183,38 @@ def test_integer_and_bool_inputs(device) -> None:
     assert metrics.stable_topk(ints, 4).tolist() == T.stable_topk(ints, 4).tolist()
     with pytest.raises(ValueError, match="2\\^53"):
         metrics.stable_topk(torch.tensor([2**60, 1], dtype=torch.int64, device=device), 1)
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties", "neginf"])
+@pytest.mark.parametrize("rows,length,k", [(512, 1000, 100), (300, 4096, 512), (2048, 64, 64)])
+def test_candidate_lists_many_rows(device, kind, rows, length, k) -> None:
+    # dsa_topk over candidate lists (values + their indices; a negative index
+    # drops the slot) for many rows: the one-wave-per-row kernel.  Ties go to
+    # the earlier slot; the result lists the chosen indices in slot order.
+    import ctypes
+
+    from dsa_amd import _lib
+
+    print(f"topk candidate lists kind={kind} rows={rows} L={length} k={k}", flush=True)
+    host = rows_for(kind, rows, length, seed=rows + length)
+    rng = np.random.default_rng(k)
+    ids = rng.integers(0, 1 << 40, size=(rows, length)).astype(np.int64)
+    ids[rng.random(size=ids.shape) < 0.2] = -1
+    x = torch.from_numpy(host).to(device)
+    ids_d = torch.from_numpy(ids).to(device)
+    out_idx = torch.empty(rows, k, dtype=torch.int64, device=device)
+    out_val = torch.empty(rows, k, dtype=torch.float32, device=device)
+    _lib.load()
+    _lib.call("dsa_topk", x.data_ptr(), ids_d.data_ptr(), rows, length, length, None, k, 0, out_idx.data_ptr(),
+              out_val.data_ptr(), torch.cuda.current_stream(device).cuda_stream)
+    got_idx = out_idx.cpu().numpy()
+    got_val = out_val.cpu().numpy()
+    for r in range(rows):
+        valid = np.flatnonzero(ids[r] >= 0)
+        sel = T.topk_index_order(host[r][valid], min(k, valid.size))
+        slots = valid[sel]
+        want = np.full(k, -1, dtype=np.int64)
+        want[: slots.size] = ids[r][slots]
+        assert got_idx[r].tolist() == want.tolist(), r
+        np.testing.assert_array_equal(got_val[r][: slots.size].view(np.uint32), host[r][slots].view(np.uint32))
+        assert np.isneginf(got_val[r][slots.size :]).all()
