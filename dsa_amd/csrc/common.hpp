@@ -157,4 +157,23 @@ __device__ __forceinline__ float reduce_lane_groups(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Phase timestamps, compiled in only with -DDSA_PHASE_TRACE (the trace build
+// of the library): thread 0 of workgroup `wg` stores the 100 MHz wall clock
+// at mark i of a per-file log of kTraceWgs x kTraceMarks entries.
+// ---------------------------------------------------------------------------
+constexpr int kTraceWgs = 4096;
+constexpr int kTraceMarks = 8;
+#ifdef DSA_PHASE_TRACE
+#define DSA_TRACE_MARK(log, wg, i)                                                         \
+  do {                                                                                     \
+    if (threadIdx.x == 0 && (uint32_t)(wg) < (uint32_t)kTraceWgs)                          \
+      (log)[(size_t)(wg) * kTraceMarks + (i)] = wall_clock64();                            \
+  } while (0)
+#else
+#define DSA_TRACE_MARK(log, wg, i) \
+  do {                             \
+  } while (0)
+#endif
+
 }  // namespace dsa

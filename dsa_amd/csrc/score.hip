@@ -30,6 +30,12 @@ namespace {
 // groups so that lane l ends with the score of key 64u + l and the store is one
 // coalesced 256-byte row.
 // ---------------------------------------------------------------------------
+#ifdef DSA_PHASE_TRACE
+// Decode scoring (candidate-list variant), per workgroup (by blockIdx.x):
+// 0 start, 1 first unit scored, 2 last unit scored, 3 list written.
+__device__ uint64_t g_trace_dense[kTraceWgs * kTraceMarks];
+#endif
+
 struct DenseArgs {
   const uint16_t* q;
   int64_t q_stride;  // elements between sequences' query blocks
@@ -155,8 +161,11 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
       __builtin_amdgcn_sched_barrier(0);
       dense_compute_unit<Tag, KF, M, kHist, kLists>(qa, wr, buf[s], u + u_stride * s, valid, L, lane, g,
                                                     scale[s], out, hist, chunk_scores, chunk_base);
+      if constexpr (kLists)
+        if (i == 0 && s == 0) DSA_TRACE_MARK(g_trace_dense, blockIdx.x, 1);
     }
   }
+  if constexpr (kLists) DSA_TRACE_MARK(g_trace_dense, blockIdx.x, 2);
 }
 
 template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists, int kWaves>
@@ -188,6 +197,7 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
   // the grid below 2^31 workgroups.)
   const uint32_t logical = (blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
   if (logical >= (uint64_t)a.total_wgs) return;
+  if constexpr (kLists) DSA_TRACE_MARK(g_trace_dense, blockIdx.x, 0);
   const int64_t seq = logical / (uint32_t)a.wgs_per_seq;
   const int chunk = (int)(logical % (uint32_t)a.wgs_per_seq);
   const int L = a.length;
@@ -234,6 +244,7 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
       write_chunk_list<kWaves>(hist, chunk_scores, chunk_keys, min(chunk_keys, valid - chunk_base), chunk_base,
                                (uint32_t)a.list_quota, a.lists + seq * (int64_t)L + chunk_base,
                                a.list_meta + 2 * (seq * kMaxListChunks + chunk), &s_list_bin, s_list_wsum);
+      DSA_TRACE_MARK(g_trace_dense, blockIdx.x, 3);
       return;
     }
     // All sixteen LDS reads first, then the atomics for the bins in use: one
@@ -941,3 +952,18 @@ extern "C" int dsa_promote_blocks(const uint8_t* direct_blocks, const float* blo
                      accepted, blocks);
   return check_launch("promote_blocks_kernel");
 }
+
+#ifdef DSA_PHASE_TRACE
+// The decode scoring kernel's phase log (trace builds only): copies n
+// entries to host memory, then zeroes the log if `clear`.
+extern "C" int dsa_trace_dense_scores(uint64_t* host, int64_t n, int32_t clear) {
+  DSA_REQUIRE(host && n >= 0 && n <= int64_t(kTraceWgs) * kTraceMarks, "bad trace read");
+  if (int st = check_hip(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace_dense), (size_t)n * 8), "trace read"))
+    return st;
+  if (clear) {
+    static const uint64_t zeros[kTraceWgs * kTraceMarks] = {};
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_dense), zeros, sizeof(zeros)), "trace clear");
+  }
+  return DSA_STATUS_OK;
+}
+#endif

@@ -45,6 +45,12 @@ constexpr int kFusedThreads = 64 * kFusedWaves;
 constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every unit resource
 constexpr uint32_t kSpinLimit = 1u << 22;      // polls (each ~1 us) before a workgroup stops waiting
 
+#ifdef DSA_PHASE_TRACE
+// Per workgroup (by blockIdx.x): 0 start, 1 seeds listed, 2 seeds scored,
+// 3 threshold exchanged, 4 blocks decided, 5 units scored, 6 list written.
+__device__ uint64_t g_trace_static[kTraceWgs * kTraceMarks];
+#endif
+
 struct FusedPlan {
   int32_t chunk_keys;
   int32_t chunks;  // per row
@@ -70,6 +76,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   const int g = lane >> 4;
   const uint32_t logical = logical_block();
   if (logical >= p.total_wgs) return;
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 0);
   const int row = (int)(logical / (uint32_t)p.chunks);
   const int c = (int)(logical % (uint32_t)p.chunks);
   const int L = a.length;
@@ -130,6 +137,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
       }
   }
   __syncthreads();
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 1);
 
   const uint8_t* row_keys = a.keys + (size_t)row * a.key_stride * KF::kRowBytes;
   const int valid_bytes = L * KF::kRowBytes;  // below 2^31 (L <= 131072)
@@ -193,6 +201,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
     __hip_atomic_fetch_min(&s_least, least, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   __syncthreads();
 
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 2);
   // 2. Exchange: publish this chunk's least seed key, then wait for the row's.
   uint64_t* slots = a.ws.slots;
   if (tid == 0)
@@ -220,6 +229,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   }
   __syncthreads();
 
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 3);
   // 3. Decisions for the chunk's blocks (whole blocks: chunks are multiples
   // of 256 keys), their flags, and the keys scored.
   const double bound = (double)ordered_to_float(s_tau);
@@ -248,6 +258,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   __syncthreads();
   if (tid == 0) a.ws.qk_parts[logical] = s_count;
 
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 4);
   // 4. The chunk's scores: kept tiles scored, the rest -inf but for seeds.
   // Units stream through a ring of KF::kBuffers register buffers as in the
   // dense kernel (the unit kBuffers - 1 ahead is always in flight; past the
@@ -293,10 +304,12 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   }
   __syncthreads();
 
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 5);
   // 5. The chunk's candidate list for the list select.
   write_chunk_list<kFusedWaves>(hist, chunk_scores, p.chunk_keys, n_chunk, base, p.quota,
                                 a.ws.select.cand + (size_t)row * L + base,
                                 a.ws.select.list_meta + 2 * ((size_t)row * kMaxListChunks + c), &s_list_bin, s_wsum);
+  DSA_TRACE_MARK(g_trace_static, blockIdx.x, 6);
 }
 
 std::atomic<uint32_t> g_generation{0};
@@ -372,3 +385,18 @@ int temporal_static_fused(TemporalArgs& a, int32_t key_dtype, int64_t* out_topk,
 }
 
 }  // namespace dsa
+
+#ifdef DSA_PHASE_TRACE
+// The fused static temporal kernel's phase log (trace builds only).
+extern "C" int dsa_trace_temporal_static(uint64_t* host, int64_t n, int32_t clear) {
+  using namespace dsa;
+  DSA_REQUIRE(host && n >= 0 && n <= int64_t(kTraceWgs) * kTraceMarks, "bad trace read");
+  if (int st = check_hip(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace_static), (size_t)n * 8), "trace read"))
+    return st;
+  if (clear) {
+    static const uint64_t zeros[kTraceWgs * kTraceMarks] = {};
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_static), zeros, sizeof(zeros)), "trace clear");
+  }
+  return DSA_STATUS_OK;
+}
+#endif

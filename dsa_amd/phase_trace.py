@@ -1,0 +1,139 @@
+"""Per-workgroup phase timelines of the decode scoring kernel and of the fused
+static temporal step, from the trace build of the library.
+
+    python -m dsa_amd.build --trace
+    python -m dsa_amd.phase_trace --config c2 [--out timeline.json]
+
+The trace build (``-DDSA_PHASE_TRACE``) has thread 0 of every workgroup store
+the GPU's 100 MHz wall clock at named points of the kernel.  Each run here is
+queued behind a 512 MiB read, as the benchmark's cold-cache runs are; the log
+of the last run is read back and every mark is reported relative to the
+earliest workgroup start, as percentiles over workgroups and per XCD
+(workgroups are dispatched to the 8 XCDs round-robin by blockIdx.x).
+
+Configurations: ``c2`` (B=16, L=32768 bf16, K=2048 decode step), ``c5``
+(B=4, L=131072 fp8, K=2048) and ``c3-static`` (B=4, 16384 -> 16385 keys,
+K=2048, block 64 static temporal step).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _lib
+from .build import TRACE_LIBRARY
+
+WALL_CLOCK_MHZ = 100.0
+MARKS = {
+    "dense": ["start", "first unit scored", "last unit scored", "list written"],
+    "static": ["start", "seeds listed", "seeds scored", "threshold exchanged", "blocks decided", "units scored",
+               "list written"],
+}
+KERNEL_SYMBOL = {"dense": "dsa_trace_dense_scores", "static": "dsa_trace_temporal_static"}
+
+
+def _c2(device):
+    from . import decode
+
+    gen = torch.Generator().manual_seed(1582)
+    q = (torch.randn(16, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16).to(device)
+    w = (torch.randn(16, 64, generator=gen) / 8).to(device)
+    keys = torch.randn(16, 32768, 128, generator=gen).to(torch.bfloat16).to(device)
+    return "dense", lambda: decode.indexer_topk(q, w, keys, 2048)
+
+
+def _c5(device):
+    from . import decode
+
+    gen = torch.Generator().manual_seed(1582)
+    q = (torch.randn(4, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16).to(device)
+    w = (torch.randn(4, 64, generator=gen) / 8).to(device)
+    raw = torch.randn(4, 131072, 128, generator=gen)
+    scales = raw.reshape(4, 1024, 128 * 128).abs().amax(dim=2) / 448
+    keys = (raw / scales.repeat_interleave(128, dim=1)[..., None]).to(torch.float8_e4m3fn).to(device)
+    scales = scales.to(device)
+    return "dense", lambda: decode.indexer_topk(q, w, keys, 2048, key_scales=scales)
+
+
+def _c3_static(device):
+    from . import decode, temporal
+
+    gen = torch.Generator().manual_seed(1582)
+    keys = torch.randn(4, 16385, 128, generator=gen).to(torch.bfloat16).to(device)
+    q0 = torch.randn(4, 64, 128, generator=gen)
+    q1 = 0.95 * q0 + math.sqrt(1 - 0.95**2) * torch.randn(4, 64, 128, generator=gen)
+    q0, q1 = q0.to(torch.bfloat16).to(device), q1.to(torch.bfloat16).to(device)
+    w = (torch.randn(4, 64, generator=gen) / 8).to(device)
+    prev_top, prev_scores = decode.indexer_topk(q0, w, keys[:, :16384].contiguous(), 2048, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, 64)
+    gamma = torch.full((4,), 0.25 * float(prev_scores.std()), device=device)
+    return "static", lambda: temporal.temporal_step(q1, w, keys, prev_max, 16384, prev_top, gamma, block_size=64,
+                                                    method="static")
+
+
+CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static}
+
+
+def timeline(config: str, runs: int = 8) -> dict:
+    if not TRACE_LIBRARY.exists():
+        raise RuntimeError(f"{TRACE_LIBRARY} is missing: run `python -m dsa_amd.build --trace` first")
+    _lib.LIBRARY_PATH = TRACE_LIBRARY
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    kernel, step = CONFIGS[config](device)
+    reader = getattr(lib, KERNEL_SYMBOL[kernel])
+    reader.restype = ctypes.c_int
+    reader.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32]
+    n = 4096 * 8
+    host = (ctypes.c_uint64 * n)()
+    flush = torch.ones(512 * 1024 * 1024 // 4, device=device)
+    for i in range(runs):
+        torch.cuda.synchronize()
+        if reader(host, n, 1) != 0:
+            raise RuntimeError(lib.dsa_last_error().decode(errors="replace"))
+        flush.amax()
+        step()
+        torch.cuda.synchronize()
+    if reader(host, n, 0) != 0:
+        raise RuntimeError(lib.dsa_last_error().decode(errors="replace"))
+    log = np.frombuffer(host, dtype=np.uint64).reshape(4096, 8).astype(np.int64)
+    wgs = np.flatnonzero(log[:, 0] > 0)
+    names = MARKS[kernel]
+    t = (log[wgs][:, : len(names)] - log[wgs, 0].min()) / WALL_CLOCK_MHZ  # microseconds
+    out = {"config": config, "kernel": kernel, "workgroups": int(wgs.size), "unit": "us from the earliest start",
+           "marks": {}}
+    for i, name in enumerate(names):
+        col = t[:, i]
+        out["marks"][name] = {q: round(float(np.percentile(col, p)), 2)
+                              for q, p in (("min", 0), ("p10", 10), ("median", 50), ("p90", 90), ("max", 100))}
+    last = len(names) - 1
+    xcd = wgs % 8
+    out["per_xcd_end"] = {int(x): {"median": round(float(np.median(t[xcd == x, last])), 2),
+                                   "max": round(float(t[xcd == x, last].max()), 2)} for x in range(8)}
+    return out
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    parser.add_argument("--runs", type=int, default=8)
+    parser.add_argument("--out", default=None)
+    args = parser.parse_args()
+    result = timeline(args.config, args.runs)
+    text = json.dumps(result, indent=1)
+    if args.out:
+        Path(args.out).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.out).write_text(text)
+    print(text, flush=True)
+
+
+if __name__ == "__main__":
+    sys.exit(main())
