@@ -21,6 +21,12 @@ constexpr int kMaxK = 4096;
 constexpr int kSmallCap = 1024;  // candidate buffer of the short-row kernel
 constexpr int kBins = 2048;
 
+#ifdef DSA_PHASE_TRACE
+// Per workgroup (by blockIdx.x): 0 start, 1 row loaded, 2 range known,
+// 3 cut located, 4 cut resolved, 5 output slots scanned, 6 written.
+__device__ uint64_t g_trace_topk[kTraceWgs * kTraceMarks];
+#endif
+
 struct TopkArgs {
   const float* scores;
   const int64_t* in_idx;
@@ -174,6 +180,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
   const int64_t base = row * a.row_stride + start;
   const int k = a.k;
   const int64_t out_base = v * (int64_t)k;
+  DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 0);
 
   // Load this thread's slice as ordered keys; 0 marks an invalid slot.  The
   // buffer bounds check turns reads past n into zeros, which are masked.
@@ -212,6 +219,15 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
   uint32_t n_valid = 0;
   float lo = __builtin_inff();
   float hi = -__builtin_inff();
+#ifdef DSA_PHASE_TRACE
+  {  // wait for the row (trace builds only) so that the mark times its arrival
+    uint32_t dep = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) dep ^= key[e];
+    asm volatile("" ::"v"(dep));
+  }
+#endif
+  DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 1);
   if (n > k) {
     // Valid count and finite range of the row in one pass and one barrier;
     // the histogram is cleared in the same phase.
@@ -245,6 +261,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
       hi = fmaxf(hi, sh.wave_hi[i]);
     }
   }
+  DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 2);
   if (n_valid > (uint32_t)k) {
     bool resolved = false;
     const float scale = (float)kBins / (hi - lo);
@@ -256,6 +273,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
       }
       __syncthreads();
       locate_bin(sh, (uint32_t)k);
+      DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 3);
       const int bucket = (int)sh.digit;
       const uint32_t need = sh.krem;
       const uint32_t crowd = sh.hist[bucket];
@@ -346,6 +364,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
     __syncthreads();
   }
 
+  DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 4);
   // Chosen elements (composite >= cstar) in index order: thread slices are
   // contiguous, so the exclusive scan of the per-thread counts is each
   // element's output slot.
@@ -357,6 +376,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
   }
   uint32_t sel_total;
   uint32_t p = block_exclusive_scan<kWaves>(n_sel, sh.wave_sums, sel_total);
+  DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 5);
   // Exactly min(valid, k) elements are chosen; the clamp only guards buffers.
   sel_total = min(sel_total, (uint32_t)k);
   if (a.sorted) {
@@ -398,6 +418,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
     if (a.out_idx) a.out_idx[out_base + i] = -1;
     if (a.out_val) a.out_val[out_base + i] = -__builtin_inff();
   }
+  DSA_TRACE_MARK(g_trace_topk, blockIdx.x, 6);
 }
 
 int launch_topk(const TopkArgs& a, int64_t virtual_rows, hipStream_t stream) {
@@ -497,3 +518,17 @@ extern "C" int dsa_topk_long(const float* scores, int64_t rows, int64_t length, 
   return dsa_topk(cand_val, cand_idx, rows, chunks * k, chunks * k, nullptr, k, sorted,
                   out_indices, out_values, stream);
 }
+
+#ifdef DSA_PHASE_TRACE
+// The per-row top-k kernel's phase log (trace builds only).
+extern "C" int dsa_trace_topk(uint64_t* host, int64_t n, int32_t clear) {
+  DSA_REQUIRE(host && n >= 0 && n <= int64_t(kTraceWgs) * kTraceMarks, "bad trace read");
+  if (int st = check_hip(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace_topk), (size_t)n * 8), "trace read"))
+    return st;
+  if (clear) {
+    static const uint64_t zeros[kTraceWgs * kTraceMarks] = {};
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_topk), zeros, sizeof(zeros)), "trace clear");
+  }
+  return DSA_STATUS_OK;
+}
+#endif

@@ -12,8 +12,10 @@ earliest workgroup start, as percentiles over workgroups and per XCD
 (workgroups are dispatched to the 8 XCDs round-robin by blockIdx.x).
 
 Configurations: ``c2`` (B=16, L=32768 bf16, K=2048 decode step), ``c5``
-(B=4, L=131072 fp8, K=2048) and ``c3-static`` (B=4, 16384 -> 16385 keys,
-K=2048, block 64 static temporal step).
+(B=4, L=131072 fp8, K=2048), ``c3-static`` (B=4, 16384 -> 16385 keys,
+K=2048, block 64 static temporal step) and ``c4-topk`` (the prefill top-512
+of 4096 causal rows of 1..4096 scores; in this one the row-loaded mark waits
+for the row, so the trace build's timing of that kernel differs slightly).
 """
 
 from __future__ import annotations
@@ -36,8 +38,9 @@ MARKS = {
     "dense": ["start", "first unit scored", "last unit scored", "list written"],
     "static": ["start", "seeds listed", "seeds scored", "threshold exchanged", "blocks decided", "units scored",
                "list written"],
+    "topk": ["start", "row loaded", "range known", "cut located", "cut resolved", "slots scanned", "written"],
 }
-KERNEL_SYMBOL = {"dense": "dsa_trace_dense_scores", "static": "dsa_trace_temporal_static"}
+KERNEL_SYMBOL = {"dense": "dsa_trace_dense_scores", "static": "dsa_trace_temporal_static", "topk": "dsa_trace_topk"}
 
 
 def _c2(device):
@@ -79,7 +82,22 @@ def _c3_static(device):
                                                     method="static")
 
 
-CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static}
+def _c4_topk(device):
+    from . import _lib as lib
+
+    gen = torch.Generator().manual_seed(1582)
+    t = 4096
+    scores = torch.randn(t, t, generator=gen).mul_(0.1)
+    scores = torch.where(torch.arange(t)[None, :] <= torch.arange(t)[:, None], scores,
+                         torch.full_like(scores, -float("inf"))).to(device)
+    visible = torch.arange(1, t + 1, dtype=torch.int32, device=device)
+    idx = torch.empty(t, 512, dtype=torch.int64, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    return "topk", lambda: lib.call("dsa_topk", scores.data_ptr(), None, t, t, t, visible.data_ptr(), 512, 0,
+                                    idx.data_ptr(), None, stream)
+
+
+CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static, "c4-topk": _c4_topk}
 
 
 def timeline(config: str, runs: int = 8) -> dict:
