@@ -117,68 +117,107 @@ __global__ __launch_bounds__(256) void temporal_radius_kernel(const double* q_no
 // sum_h |w_h| ||q_h|| ||k|| of its exact value, so
 //   margin_b = n_b * (C + 2^-15 * sum_h (|w_now|_h ||q_now,h|| + |w_prev|_h ||q_prev,h||))
 // bounds |score_now - score_prev| of every key of the block as computed here.
-// Everything is float64 and the result is scaled by kRadiusRoundUp.  One wave
-// per block; each workgroup derives its row's two head sums first.
+// Everything is float64 and the result is scaled by kRadiusRoundUp.  A
+// workgroup takes a run of whole blocks (256 keys, or one block when blocks
+// are longer): each thread the float64 norm of one key row at a time (its 256
+// contiguous bytes), the workgroup's head sums from 16-byte query loads (four
+// threads per head), then one thread per block the maximum over its keys.
 constexpr double kScoreRoundingAllowance = 0x1p-15;
+constexpr int kMarginThreads = 256;
+constexpr int kMaxMarginBlock = 4096;  // keys per block (the norms of one workgroup's keys sit in LDS)
 
-__global__ __launch_bounds__(256) void certified_margins_kernel(const uint16_t* q_now, const uint16_t* q_prev,
-                                                                const float* w_now, const float* w_prev,
-                                                                const uint16_t* keys, int64_t key_stride,
-                                                                int prev_length, int block_size, int blocks_per_row,
-                                                                int q_dtype, double* margins) {
+__device__ __forceinline__ double half_to_double(uint32_t bits16, int dtype) {
+  return dtype == kBF16 ? (double)__uint_as_float(bits16 << 16)
+                        : (double)(float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// Sum of squares of the 8 halves of v, added to acc in order.
+__device__ __forceinline__ double sum_squares8(uint4 v, int dtype, double acc) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const double lo = half_to_double(w[i] & 0xffffu, dtype);
+    const double hi = half_to_double(w[i] >> 16, dtype);
+    acc = fma(lo, lo, acc);
+    acc = fma(hi, hi, acc);
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(kMarginThreads) void certified_margins_kernel(const uint16_t* q_now, const uint16_t* q_prev,
+                                                                           const float* w_now, const float* w_prev,
+                                                                           const uint16_t* keys, int64_t key_stride,
+                                                                           int prev_length, int block_size,
+                                                                           int blocks_per_row, int blocks_per_wg,
+                                                                           int q_dtype, double* margins) {
   __shared__ double s_radius[kHeads];
   __shared__ double s_slack[kHeads];
+  __shared__ double s_norm[kMaxMarginBlock];
   const int row = blockIdx.y;
   const int tid = threadIdx.x;
-  auto q_at = [&](const uint16_t* q, int i) -> double {
-    const uint16_t bits = q[(size_t)row * kHeads * kHeadDim + i];
-    return q_dtype == kBF16 ? (double)__uint_as_float(uint32_t(bits) << 16)
-                            : (double)(float)__builtin_bit_cast(_Float16, bits);
-  };
-  if (tid < kHeads) {
+  {
+    // Head sums: thread t takes head t / 4, dims [32 (t % 4), 32 (t % 4) + 32).
+    const int h = tid >> 2;
+    const int part = tid & 3;
+    const size_t at = ((size_t)row * kHeads + h) * kHeadDim + 32 * part;
+    const uint4* pp = reinterpret_cast<const uint4*>(q_prev + at);
+    const uint4* pn = reinterpret_cast<const uint4*>(q_now + at);
     double prev_sq = 0.0, now_sq = 0.0, diff_sq = 0.0;
-    for (int d = 0; d < kHeadDim; ++d) {
-      const double p = q_at(q_prev, tid * kHeadDim + d);
-      const double c = q_at(q_now, tid * kHeadDim + d);
-      prev_sq = fma(p, p, prev_sq);
-      now_sq = fma(c, c, now_sq);
-      diff_sq = fma(c - p, c - p, diff_sq);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 a = pp[v];
+      const uint4 c = pn[v];
+      const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
+      const uint32_t wc[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const double p = half_to_double((wa[i >> 1] >> (16 * (i & 1))) & 0xffffu, q_dtype);
+        const double n = half_to_double((wc[i >> 1] >> (16 * (i & 1))) & 0xffffu, q_dtype);
+        prev_sq = fma(p, p, prev_sq);
+        now_sq = fma(n, n, now_sq);
+        diff_sq = fma(n - p, n - p, diff_sq);
+      }
     }
-    const double wn = (double)w_now[(size_t)row * kHeads + tid];
-    const double wp = (double)w_prev[(size_t)row * kHeads + tid];
-    s_radius[tid] = fabs(wn - wp) * sqrt(prev_sq) + fabs(wn) * sqrt(diff_sq);
-    s_slack[tid] = fabs(wn) * sqrt(now_sq) + fabs(wp) * sqrt(prev_sq);
+#pragma unroll
+    for (int off = 1; off < 4; off <<= 1) {
+      prev_sq += __shfl_xor(prev_sq, off, kWave);
+      now_sq += __shfl_xor(now_sq, off, kWave);
+      diff_sq += __shfl_xor(diff_sq, off, kWave);
+    }
+    if (part == 0) {
+      const double wn = (double)w_now[(size_t)row * kHeads + h];
+      const double wp = (double)w_prev[(size_t)row * kHeads + h];
+      s_radius[h] = fabs(wn - wp) * sqrt(prev_sq) + fabs(wn) * sqrt(diff_sq);
+      s_slack[h] = fabs(wn) * sqrt(now_sq) + fabs(wp) * sqrt(prev_sq);
+    }
+  }
+  // Key norms of the workgroup's blocks (0 past prev_length).
+  const int first = blockIdx.x * blocks_per_wg * block_size;
+  const int count = blocks_per_wg * block_size;
+  for (int i = tid; i < count; i += kMarginThreads) {
+    const int key = first + i;
+    double acc = 0.0;
+    if (key < prev_length) {
+      const uint4* kp = reinterpret_cast<const uint4*>(keys + ((size_t)row * key_stride + key) * kHeadDim);
+#pragma unroll
+      for (int v = 0; v < kHeadDim / 8; ++v) acc = sum_squares8(kp[v], q_dtype, acc);
+    }
+    s_norm[i] = sqrt(acc);
   }
   __syncthreads();
-  double radius = 0.0, slack = 0.0;
-  for (int h = 0; h < kHeads; ++h) {
-    radius += s_radius[h];
-    slack += s_slack[h];
-  }
-  const double coef = radius + kScoreRoundingAllowance * slack;
-  const int lane = tid & 63;
-  const int b = blockIdx.x * 4 + (tid >> 6);
-  if (b >= blocks_per_row) return;
-  const int start = b * block_size;
-  const int stop = min(prev_length, start + block_size);
-  double best = 0.0;
-  for (int t = start; t < stop; ++t) {
-    // lane l holds dims 2l, 2l + 1 of the key row
-    const uint32_t two = reinterpret_cast<const uint32_t*>(keys + ((size_t)row * key_stride + t) * kHeadDim)[lane];
-    double x0, x1;
-    if (q_dtype == kBF16) {
-      x0 = (double)__uint_as_float(two << 16);
-      x1 = (double)__uint_as_float(two & 0xffff0000u);
-    } else {
-      x0 = (double)(float)__builtin_bit_cast(_Float16, (uint16_t)(two & 0xffffu));
-      x1 = (double)(float)__builtin_bit_cast(_Float16, (uint16_t)(two >> 16));
+  if (tid < blocks_per_wg) {
+    const int b = blockIdx.x * blocks_per_wg + tid;
+    if (b < blocks_per_row) {
+      double radius = 0.0, slack = 0.0;
+      for (int h = 0; h < kHeads; ++h) {
+        radius += s_radius[h];
+        slack += s_slack[h];
+      }
+      double best = 0.0;
+      for (int j = 0; j < block_size; ++j) best = fmax(best, s_norm[tid * block_size + j]);
+      margins[(size_t)row * blocks_per_row + b] = best * (radius + kScoreRoundingAllowance * slack) * kRadiusRoundUp;
     }
-    double acc = fma(x0, x0, x1 * x1);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-    best = fmax(best, sqrt(acc));
   }
-  if (lane == 0) margins[(size_t)row * blocks_per_row + b] = best * coef * kRadiusRoundUp;
 }
 
 }  // namespace
@@ -195,12 +234,16 @@ extern "C" int dsa_certified_margins(const void* q_now, const void* q_prev, cons
               "prev_length %lld invalid", (long long)prev_length);
   DSA_REQUIRE(block_size > 0, "block_size must be positive");
   DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16, "certified margins take bf16/fp16 queries and keys");
-  DSA_REQUIRE(reinterpret_cast<uintptr_t>(keys) % 4 == 0, "keys must be 4-byte aligned");
+  DSA_REQUIRE(block_size <= kMaxMarginBlock, "block_size %d above %d", block_size, kMaxMarginBlock);
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(keys) % 16 == 0 && reinterpret_cast<uintptr_t>(q_now) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(q_prev) % 16 == 0,
+              "queries and keys must be 16-byte aligned");
   const int64_t blocks = (prev_length + block_size - 1) / block_size;
-  hipLaunchKernelGGL(certified_margins_kernel, dim3((unsigned)((blocks + 3) / 4), (unsigned)batch), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q_now),
+  const int per_wg = block_size < kMarginThreads ? kMarginThreads / block_size : 1;
+  hipLaunchKernelGGL(certified_margins_kernel, dim3((unsigned)((blocks + per_wg - 1) / per_wg), (unsigned)batch),
+                     dim3(kMarginThreads), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q_now),
                      static_cast<const uint16_t*>(q_prev), w_now, w_prev, static_cast<const uint16_t*>(keys),
-                     key_stride, (int)prev_length, (int)block_size, (int)blocks, (int)key_dtype, margins);
+                     key_stride, (int)prev_length, (int)block_size, (int)blocks, per_wg, (int)key_dtype, margins);
   return check_launch("certified_margins_kernel");
 }
 

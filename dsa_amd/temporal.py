@@ -53,6 +53,27 @@ def _workspace(device, stream, batch, length, k, block_size) -> torch.Tensor:
     return _lib.workspace("temporal", device, stream, need, zeroed=True, rows=0)
 
 
+def _outputs(device, batch: int, length: int, blocks: int, k: int):
+    """The step's four outputs as views of one allocation (one allocator
+    call per step instead of four): scores fp32 [B, L], top-k int64 [B, k],
+    keys scored int32 [B] and kept-block flags uint8 [B, blocks]."""
+
+    def up(n: int) -> int:
+        return (n + 255) // 256 * 256
+
+    sizes = (batch * length * 4, batch * k * 8, batch * 4, batch * blocks)
+    offsets, total = [], 0
+    for size in sizes:
+        offsets.append(total)
+        total += up(size)
+    buf = torch.empty(total, device=device, dtype=torch.uint8)
+    scores = buf[offsets[0] : offsets[0] + sizes[0]].view(torch.float32).view(batch, length)
+    topk = buf[offsets[1] : offsets[1] + sizes[1]].view(torch.int64).view(batch, k)
+    qk = buf[offsets[2] : offsets[2] + sizes[2]].view(torch.int32)
+    evaluated = buf[offsets[3] : offsets[3] + sizes[3]].view(batch, blocks)
+    return scores, evaluated, topk, qk
+
+
 def temporal_step(
     queries: torch.Tensor,
     weights: torch.Tensor,
@@ -147,10 +168,7 @@ def temporal_step(
         margins = block_margins.to(device=device, dtype=torch.float64).contiguous()
     stream = _lib.stream_of(keys)
     blocks = math.ceil(length / block_size)
-    scores = torch.empty((batch, length), device=device, dtype=torch.float32)
-    evaluated = torch.empty((batch, blocks), device=device, dtype=torch.uint8)
-    topk = torch.empty((batch, k), device=device, dtype=torch.int64)
-    qk = torch.empty(batch, device=device, dtype=torch.int32)
+    scores, evaluated, topk, qk = _outputs(device, batch, length, blocks, k)
     ws = _workspace(device, stream, batch, length, k, block_size)
     _lib.call(
         "dsa_temporal_step", _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), key_stride, _lib.ptr(key_scales),

@@ -336,8 +336,18 @@ int dsa_score_topk_noalloc(const void* queries, const float* weights, const void
  *   length <= 131072 and at most 2048 blocks, block_size in {16, 32, 64,
  *   128}, k <= 4096; keys as in dsa_full_scores (bf16/fp16, or fp8 with
  *   key_scales).
- * Pruned blocks load no key bytes.  A step costs 3 + 2 * ceil(blocks / W)
- * launches (3 when static).
+ *   workspace   dsa_temporal_workspace_bytes(batch, length, k, block_size)
+ *               bytes, 256-byte aligned, shared by the temporal, approximate
+ *               and verifier steps; its first 32 KiB must be zero before its
+ *               first use (the static step's generation-stamped exchange
+ *               slots, which no later call misreads); calls that share it
+ *               must be ordered (one stream).
+ * Pruned blocks load no key bytes.  A static step (wave 0) whose shape fits
+ * the decode step's candidate-list plan and whose workgroups fit on the
+ * device at once is one scoring launch plus the list select; other steps
+ * cost 4 + 2 * ceil(blocks / W) launches, or 6 with the persistent per-row
+ * scan (more than 16 waves of W blocks).  DSA_AMD_TEMPORAL_PATH=launch in the
+ * environment keeps static steps on the launch path.
  * ------------------------------------------------------------------------ */
 int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, int64_t k, int32_t block_size);
 int dsa_temporal_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
@@ -597,7 +607,8 @@ int dsa_temporal_score_radius(const double* q_now, const double* q_prev, const d
  * margins keeps every key of the dense top-k.  q_now, q_prev [batch, 64, 128]
  * and keys [batch, key_stride, 128] in key_dtype (bf16/fp16), w_now, w_prev
  * [batch, 64] fp32; margins [batch, ceil(prev_length / block_size)] float64
- * over the first prev_length keys.  Computed in float64. */
+ * over the first prev_length keys, block_size <= 4096; queries and keys
+ * 16-byte aligned.  Computed in float64. */
 int dsa_certified_margins(const void* q_now, const void* q_prev, const float* w_now, const float* w_prev,
                           const void* keys, int64_t key_stride, int64_t batch, int64_t prev_length,
                           int32_t block_size, int32_t key_dtype, double* margins, void* stream);
