@@ -247,3 +247,52 @@ def test_static_step_paths_agree(device, monkeypatch, block, gamma_sigma, prev_l
         assert not kept.all(), "the negative margin pruned nothing"
     if gamma_sigma <= -4.0:  # below the seeds' own drift: blocks holding seeds are pruned too
         assert seeds_in_pruned > 0, "no pruned block holds a seed"
+
+
+@pytest.mark.parametrize("batch,prev_length,length,k,block,capacity", [
+    (2, 5000, 5003, 300, 64, 8192),   # a view of a larger KV cache (key stride 8192 rows)
+    (24, 700, 705, 700, 16, 705),     # many short rows; every previous key is a seed
+    (1, 100, 100, 100, 32, 100),      # one row, one chunk, k = length
+])
+def test_static_step_cache_views_and_shapes(device, monkeypatch, batch, prev_length, length, k, block, capacity) -> None:
+    print(f"static shapes B={batch} L={prev_length}->{length} k={k} bs={block} cap={capacity}", flush=True)
+    q_prev, q_cur, w, cache = transition(batch, prev_length, capacity, seed=batch * 31 + length)
+    q_prev, q_cur, w, cache = q_prev.to(device), q_cur.to(device), w.to(device), cache.to(device)
+    view = cache[:, :length]
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, cache[:, :prev_length].contiguous(), k,
+                                                 return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, view.contiguous(), k, return_scores=True)[1].cpu().numpy()
+    gamma = torch.full((batch,), -1.0 * float(prev_scores.std()), device=device)
+
+    def run(keys):
+        s = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                   method="static")
+        return [x.cpu().numpy() for x in (s.scores, s.evaluated_blocks, s.qk_scored, s.topk)]
+
+    fused_view = run(view)
+    fused_copy = run(view.contiguous())
+    monkeypatch.setenv("DSA_AMD_TEMPORAL_PATH", "launch")
+    launch_view = run(view)
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_PATH")
+    for a, b, c in zip(fused_view, fused_copy, launch_view):
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(a, c)
+    scores, kept, qk, topk = fused_view
+    seeds = prev_topk.cpu().numpy()
+    blocks = math.ceil(length / block)
+    for b in range(batch):
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+        upper = R.upper_bounds(previous_max, float(gamma[b]), prev_length, length, block)
+        scan = R.block_scan_order("address", upper, R.block_maxima(dense[b], block), np.zeros(blocks, dtype=bool))
+        current = dense[b].astype(np.float64)
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=False,
+                             fixed_threshold=float(current[seeds[b]].min()), wave=1)
+        np.testing.assert_array_equal(kept[b], trace.kept, err_msg=f"row {b}: kept blocks")
+        assert int(qk[b]) == trace.scored, (b, int(qk[b]), trace.scored)
+        ev = trace.evaluated
+        np.testing.assert_array_equal(scores[b][ev], dense[b][ev])
+        assert np.isneginf(scores[b][~ev]).all()
+        masked = np.where(ev, dense[b], -np.inf).astype(np.float32)
+        assert topk[b].tolist() == T.topk_index_order(masked, k).tolist(), b
