@@ -324,8 +324,12 @@ constexpr int kMaxTemporalLength = 131072;
 // Above this many waves of scan positions a step runs the persistent
 // per-row scan: one launch per wave costs a launch, a grid drain and a refresh
 // launch (~11 us at C3), against ~4.4 us per wave in LDS but with one CU per
-// row scoring (~130 us for a C3 row's kept keys).
+// row scoring (~185 us for a C3 row's 4 MB of keys).  Rows of more key bytes
+// than kPersistentRowBytes stay on the launch path, whose block launches
+// spread the scoring over the whole GPU (C5, 16 MB of fp8 keys per row, 22
+// waves: 435 us per step against 717 us in the persistent scan).
 constexpr int kPersistentScanWaves = 16;
+constexpr int64_t kPersistentRowBytes = int64_t(8) << 20;
 
 template <class Tag, class KF>
 __global__ __launch_bounds__(kScanThreads) void temporal_scan_kernel(TemporalArgs a, int32_t wave_blocks) {
@@ -639,7 +643,8 @@ int launch_scan(TemporalArgs& a, int32_t wave, hipStream_t stream) {
   if (int st = check_launch("temporal_seed_kernel")) return st;
   const int step = wave > 0 ? wave : a.blocks;
   const int waves = (a.blocks + step - 1) / step;
-  if (wave > 0 && waves > kPersistentScanWaves) {
+  const bool light_rows = a.source || int64_t(a.length) * KF::kRowBytes <= kPersistentRowBytes;
+  if (wave > 0 && waves > kPersistentScanWaves && light_rows) {
     // many refreshes: the whole scan of a row in one workgroup, no relaunch per wave
     hipLaunchKernelGGL((temporal_scan_kernel<Tag, KF>), dim3(a.rows), dim3(kScanThreads), 0, stream, a, wave);
     return check_launch("temporal_scan_kernel");
