@@ -41,6 +41,9 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   __shared__ uint64_t xh[kSortN];
   __shared__ uint32_t xl[kSortN];
   __shared__ uint8_t hot[kMaxTemporalBlocks];
+  __shared__ double s_upper[kMaxTemporalBlocks];
+  __shared__ double s_rank[kMaxTemporalBlocks];
+  __shared__ uint32_t s_exact;
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const int L = a.length;
@@ -51,10 +54,13 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   const int words = (L + 31) / 32;
   for (int i = tid; i < words; i += 1024) a.ws.seed_mask[(size_t)row * words + i] = 0;
   for (int i = tid; i < nb; i += 1024) a.evaluated[(size_t)row * nb + i] = 0;
+  if (tid < kMaxRounds) a.ws.list_total[(size_t)row * kMaxRounds + tid] = 0;
   for (int i = tid; i < kSelectBins; i += 1024) a.ws.select.hist[(size_t)row * kSelectBins + i] = 0;
   if (tid == 0) {
     a.ws.tau[row] = 0xffffffffu;
+    a.ws.floor[row] = 0xffffffffu;
     a.qk_scored[row] = 0;
+    s_exact = 0;
   }
   const int first_new = a.prev_length / bs;
   const bool grown = a.prev_length < L;
@@ -107,6 +113,8 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
       group = hot_first && !hot[b] ? 0x80000000u : 0u;
     }
     a.ws.upper[(size_t)row * nb + b] = upper;
+    s_upper[b] = upper;
+    s_rank[b] = rank_value;
     h[j] = ~double_to_ordered(rank_value);
     l[j] = group | (uint32_t)b;
   }
@@ -115,11 +123,47 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
       a.ws.order[(size_t)row * nb + b] = b;
       if (a.order_out) a.order_out[(size_t)row * nb + b] = b;
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (2 * tid + j < nb) a.ws.upper_pos[(size_t)row * nb + 2 * tid + j] = s_upper[2 * tid + j];
     return;
   }
   int n = 2;
   while (n < nb) n <<= 1;
-  block_sort(h, l, xh, xl, n);
+  // Fast sort of (group, rank value rounded to float, larger first, block)
+  // packed in 64 bits.  The rounding is monotone, so only blocks whose rank
+  // values round to one float can come out of the float64 order; when two
+  // such values differ the exact sort (float64 key, then group | block) runs.
+  uint64_t v[2] = {~0ull, ~0ull};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int b = 2 * tid + j;
+    if (b >= nb) continue;
+    const double d = __builtin_isnan(s_rank[b]) ? -HUGE_VAL : s_rank[b];
+    const uint32_t fkey = float_to_ordered((float)d);
+    v[j] = ((uint64_t)(l[j] >> 31) << 63) | ((uint64_t)~fkey << 12) | (uint64_t)b;
+  }
+  uint64_t* xk = xh;
+  block_sort64(v, xk, n);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) xk[2 * tid + j] = v[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int pos = 2 * tid + j;
+    if (pos == 0 || pos >= nb) continue;
+    const uint64_t prev = xk[pos - 1];
+    if ((prev >> 12) == (v[j] >> 12) &&
+        double_to_ordered(s_rank[prev & 0xfffu]) != double_to_ordered(s_rank[v[j] & 0xfffu]))
+      s_exact = 1;
+  }
+  __syncthreads();
+  if (s_exact) {  // uniform
+    block_sort(h, l, xh, xl, n);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (2 * tid + j < nb) v[j] = l[j] & 0x7fffffffu;
+  }
   if (policy && a.ap.p.order == DSA_ORDER_BUCKET) {
     // Rank r in the risk order -> bucket min(N - 1, r * N / nb); then address
     // order within each bucket.
@@ -127,18 +171,19 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = 2 * tid + j;
-      if (r < nb) {
-        h[j] = (uint64_t)min<int64_t>(buckets - 1, (int64_t)r * buckets / nb);
-        l[j] &= 0x7fffffffu;
-      }
+      if (r < nb) v[j] = ((uint64_t)min<int64_t>(buckets - 1, (int64_t)r * buckets / nb) << 12) | (v[j] & 0xfffu);
     }
-    block_sort(h, l, xh, xl, n);
+    __syncthreads();  // xk is reused
+    block_sort64(v, xk, n);
   }
+  __syncthreads();  // s_upper of every block, for the bound at each position
 #pragma unroll
   for (int j = 0; j < 2; ++j)
     if (2 * tid + j < nb) {
-      a.ws.order[(size_t)row * nb + 2 * tid + j] = l[j] & 0x7fffffffu;
-      if (a.order_out) a.order_out[(size_t)row * nb + 2 * tid + j] = (int32_t)(l[j] & 0x7fffffffu);
+      const uint32_t blk = (uint32_t)(v[j] & 0xfffu);
+      a.ws.order[(size_t)row * nb + 2 * tid + j] = blk;
+      a.ws.upper_pos[(size_t)row * nb + 2 * tid + j] = s_upper[blk];
+      if (a.order_out) a.order_out[(size_t)row * nb + 2 * tid + j] = (int32_t)blk;
     }
 }
 
@@ -171,10 +216,12 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
     v = score_unit<Tag, KF>(a, row, tile_key, r, g);
   }
   uint32_t least = 0xffffffffu;  // this lane's seed key (none: neutral for the min)
+  uint32_t lowest = 0xffffffffu;  // this lane's entry of run (the floor of the running k largest)
   if (i < a.k) {
     const int64_t key = seeds[i];
     if (key < 0 || key >= a.length) {
       a.ws.run[(size_t)row * a.k + i] = 0;  // below every score
+      lowest = 0;
     } else {
       if constexpr (KF::kScaled)
         if (!a.source) v *= a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key >> 7)];
@@ -183,13 +230,19 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
       __hip_atomic_fetch_or(a.ws.seed_mask + (size_t)row * words + (key >> 5), 1u << (key & 31),
                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       least = float_to_ordered(v);
+      lowest = least;
       a.ws.run[(size_t)row * a.k + i] = least;
     }
   }
-  // One atomic per wave: the minimum of its 64 seeds.
-  for (int off = 32; off > 0; off >>= 1) least = min(least, (uint32_t)__shfl_xor((int)least, off, kWave));
+  // One atomic per wave and value: the minimum of its 64 seeds.
+  for (int off = 32; off > 0; off >>= 1) {
+    least = min(least, (uint32_t)__shfl_xor((int)least, off, kWave));
+    lowest = min(lowest, (uint32_t)__shfl_xor((int)lowest, off, kWave));
+  }
   if (lane == 0 && least != 0xffffffffu)
     __hip_atomic_fetch_min(a.ws.tau + row, least, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0 && lowest != 0xffffffffu)
+    __hip_atomic_fetch_min(a.ws.floor + row, lowest, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One block per wave: scan positions [wave_start, wave_start + wave_len) of
@@ -636,11 +689,12 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
 }
 
 template <class Tag, class KF>
-int launch_scan(TemporalArgs& a, int32_t wave, hipStream_t stream) {
+int launch_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(temporal_prep_kernel, dim3(a.rows), dim3(1024), 0, stream, a);
   if (int st = check_launch("temporal_prep_kernel")) return st;
   hipLaunchKernelGGL((temporal_seed_kernel<Tag, KF>), dim3(a.rows * ((a.k + 255) / 256)), dim3(256), 0, stream, a);
   if (int st = check_launch("temporal_seed_kernel")) return st;
+  if (wave > 0 && !legacy_paths_forced()) return temporal_rounds(a, wave, key_dtype, stream);
   const int step = wave > 0 ? wave : a.blocks;
   const int waves = (a.blocks + step - 1) / step;
   const bool light_rows = a.source || int64_t(a.length) * KF::kRowBytes <= kPersistentRowBytes;
@@ -665,16 +719,9 @@ int launch_scan(TemporalArgs& a, int32_t wave, hipStream_t stream) {
   return DSA_STATUS_OK;
 }
 
-// DSA_AMD_TEMPORAL_PATH=launch keeps static steps on the multi-launch path
-// (prep, seeds, blocks, histogram select), for comparisons.
-bool fused_static_enabled() {
-  const char* v = std::getenv("DSA_AMD_TEMPORAL_PATH");
-  return !(v && std::strcmp(v, "launch") == 0);
-}
-
 int run_step(TemporalArgs& a, int32_t wave, int32_t key_dtype, int64_t* out_topk, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (wave == 0 && fused_static_enabled()) {
+  if (wave == 0 && !legacy_paths_forced()) {
     bool ran = false;
     if (int st = temporal_static_fused(a, key_dtype, out_topk, s, ran)) return st;
     if (ran) return DSA_STATUS_OK;
@@ -685,11 +732,16 @@ int run_step(TemporalArgs& a, int32_t wave, int32_t key_dtype, int64_t* out_topk
 
 }  // namespace
 
+bool legacy_paths_forced() {
+  const char* v = std::getenv("DSA_AMD_TEMPORAL_PATH");
+  return v && std::strcmp(v, "launch") == 0;
+}
+
 int temporal_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream) {
   switch (key_dtype) {
-    case DSA_DTYPE_BF16: return launch_scan<Bf16Tag, KeysB16>(a, wave, stream);
-    case DSA_DTYPE_F16: return launch_scan<F16Tag, KeysB16>(a, wave, stream);
-    default: return launch_scan<Bf16Tag, KeysFP8>(a, wave, stream);
+    case DSA_DTYPE_BF16: return launch_scan<Bf16Tag, KeysB16>(a, wave, key_dtype, stream);
+    case DSA_DTYPE_F16: return launch_scan<F16Tag, KeysB16>(a, wave, key_dtype, stream);
+    default: return launch_scan<Bf16Tag, KeysFP8>(a, wave, key_dtype, stream);
   }
 }
 

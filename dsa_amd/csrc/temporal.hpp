@@ -29,36 +29,74 @@ struct TemporalWorkspace {
                         // before the workspace's first use
   uint32_t* qk_parts;   // [kMaxFusedWgs] keys each fused workgroup scored
   uint32_t* tau;        // [rows] ordered key of the threshold in force
+  uint32_t* floor;      // [rows] least of run (the k-th largest evaluated score), dynamic rounds
   uint32_t* run;        // [rows][k] ordered keys of the k largest evaluated scores
   uint32_t* order;      // [rows][blocks] block ids in scan order
   double* upper;        // [rows][blocks] U_b, in double like the float64 reference
+  double* upper_pos;    // [rows][blocks] the same, by scan position
   uint32_t* seed_mask;  // [rows][ceil(L / 32)] keys evaluated as seeds
+  // Dynamic rounds: the keys each round's scoring lists (a row's list is
+  // entries [0, list_total[round])), and the replay's sorted keys when they
+  // outgrow its LDS.
+  uint32_t* list_total;  // [rows][kMaxRounds]
+  uint64_t* entries;     // [rows][list_capacity] (group << 49) | (key << 32) | ordered score
+  uint32_t* spill_val;   // [rows][spill_capacity]
+  uint32_t* spill_item;  // [rows][spill_capacity]
+  uint8_t* spill_join;   // [rows][spill_capacity]
+  int64_t list_capacity;
+  int64_t spill_capacity;
   SelectWorkspace select;  // final top-k over the evaluated keys
   int64_t bytes;
 };
 
+// Keys one scoring wave of a dynamic round covers at most (two 64-key units),
+// keys per scoring workgroup (four waves), and rounds per scan.
+constexpr int kRoundWaveKeys = 128;
+constexpr int kRoundKeys = 4 * kRoundWaveKeys;
+constexpr int kMaxRounds = 8;
+
 inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t length, int64_t k, int32_t block_size) {
   const int64_t blocks = (length + block_size - 1) / block_size;
   auto round = [](int64_t bytes) { return (bytes + 255) / 256 * 256; };
+  // A round's scoring workgroups cover at most blocks * block_size + kRoundKeys
+  // keys of region space; the replay sorts k of them more.
+  const int64_t list_capacity = blocks * block_size + kRoundKeys;
+  const int64_t spill_capacity = list_capacity + k;
   const int64_t slots_off = 0;
   const int64_t parts_off = slots_off + kMaxFusedWgs * 8;
   const int64_t tau_off = parts_off + kMaxFusedWgs * 4;
-  const int64_t run_off = tau_off + round(rows * 4);
+  const int64_t floor_off = tau_off + round(rows * 4);
+  const int64_t run_off = floor_off + round(rows * 4);
   const int64_t order_off = run_off + round(rows * k * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
-  const int64_t mask_off = upper_off + round(rows * blocks * 8);
-  const int64_t select_off = mask_off + round(rows * ((length + 31) / 32) * 4);
+  const int64_t upos_off = upper_off + round(rows * blocks * 8);
+  const int64_t mask_off = upos_off + round(rows * blocks * 8);
+  const int64_t count_off = mask_off + round(rows * ((length + 31) / 32) * 4);
+  const int64_t entries_off = count_off + round(rows * kMaxRounds * 4);
+  const int64_t sval_off = entries_off + round(rows * list_capacity * 8);
+  const int64_t sitem_off = sval_off + round(rows * spill_capacity * 4);
+  const int64_t sjoin_off = sitem_off + round(rows * spill_capacity * 4);
+  const int64_t select_off = sjoin_off + round(rows * spill_capacity);
   TemporalWorkspace ws;
   const uintptr_t p = reinterpret_cast<uintptr_t>(base);
   ws.select = select_workspace_layout(base ? reinterpret_cast<void*>(p + select_off) : nullptr, rows, length);
   ws.bytes = select_off + round(ws.select.bytes);
+  ws.list_capacity = list_capacity;
+  ws.spill_capacity = spill_capacity;
   ws.slots = base ? reinterpret_cast<uint64_t*>(p + slots_off) : nullptr;
   ws.qk_parts = base ? reinterpret_cast<uint32_t*>(p + parts_off) : nullptr;
   ws.tau = base ? reinterpret_cast<uint32_t*>(p + tau_off) : nullptr;
+  ws.floor = base ? reinterpret_cast<uint32_t*>(p + floor_off) : nullptr;
   ws.run = base ? reinterpret_cast<uint32_t*>(p + run_off) : nullptr;
   ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
   ws.upper = base ? reinterpret_cast<double*>(p + upper_off) : nullptr;
+  ws.upper_pos = base ? reinterpret_cast<double*>(p + upos_off) : nullptr;
   ws.seed_mask = base ? reinterpret_cast<uint32_t*>(p + mask_off) : nullptr;
+  ws.list_total = base ? reinterpret_cast<uint32_t*>(p + count_off) : nullptr;
+  ws.entries = base ? reinterpret_cast<uint64_t*>(p + entries_off) : nullptr;
+  ws.spill_val = base ? reinterpret_cast<uint32_t*>(p + sval_off) : nullptr;
+  ws.spill_item = base ? reinterpret_cast<uint32_t*>(p + sitem_off) : nullptr;
+  ws.spill_join = base ? reinterpret_cast<uint8_t*>(p + sjoin_off) : nullptr;
   return ws;
 }
 
@@ -208,6 +246,50 @@ __device__ inline void block_sort(uint64_t (&h)[2], uint32_t (&l)[2], uint64_t* 
   }
 }
 
+// The same network over single 64-bit keys, ascending (padding: ~0).  One
+// 64-bit compare and two selects per compare-exchange, against the three
+// compares of the (hi, lo) entries above: the scan-order sort packs its keys
+// into 64 bits where it can.
+__device__ inline void block_sort64(uint64_t (&v)[2], uint64_t* x, int n) {
+  const int t = threadIdx.x;
+  const bool active = 2 * t < n;
+  for (int size = 2; size <= n; size <<= 1) {
+    const bool up = ((2 * t) & size) == 0;
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride == 1) {
+        const bool swap = up ? v[1] < v[0] : v[0] < v[1];
+        const uint64_t a0 = swap ? v[1] : v[0];
+        const uint64_t a1 = swap ? v[0] : v[1];
+        v[0] = a0;
+        v[1] = a1;
+        continue;
+      }
+      const int mask = stride >> 1;  // partner thread t ^ mask
+      const bool lower = (t & mask) == 0;
+      uint64_t o[2];
+      if (stride <= 64) {
+        if (!active) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) o[j] = __shfl_xor(v[j], mask, kWave);
+      } else {
+        if (active) {
+          x[2 * t] = v[0];
+          x[2 * t + 1] = v[1];
+        }
+        __syncthreads();
+        if (active) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) o[j] = x[(2 * t + j) ^ stride];
+        }
+        __syncthreads();
+        if (!active) continue;
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) v[j] = (up == lower) ? min(v[j], o[j]) : max(v[j], o[j]);
+    }
+  }
+}
+
 // Scores 64 keys of one row with the dense kernel's unit code: lane (r, g)
 // loads, for each tile t, its slice of key tile_key[t] (kFarKey: nothing is
 // loaded and the result is not a key's score).  Lane l returns the score of
@@ -246,6 +328,18 @@ int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, 
 // does not fit that path (the caller then runs temporal_scan and
 // temporal_finish).
 int temporal_static_fused(TemporalArgs& a, int32_t key_dtype, int64_t* out_topk, hipStream_t stream, bool& ran);
+
+// The dynamic scan (wave > 0) in rounds (temporal_rounds.hip), after the prep
+// and seed kernels: each round scores every block of its scan positions whose
+// bound clears the threshold in force at the round's start, then one
+// workgroup per row replays the scan's decisions over those positions
+// exactly.
+int temporal_rounds(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream);
+
+// Scan paths: DSA_AMD_TEMPORAL_PATH=launch keeps every step on the
+// multi-launch paths (static: prep, seeds, blocks, histogram select; dynamic:
+// per-wave launches or the persistent per-row scan), for comparisons.
+bool legacy_paths_forced();
 
 // Shared argument checks of the step entry points.
 int check_step(const void* queries, const void* keys, int64_t key_stride, const float* key_scales,

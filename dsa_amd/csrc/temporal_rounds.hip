@@ -1,0 +1,690 @@
+// The dynamic temporal scan in rounds.
+//
+// The dynamic filter (replay.py:172-222, the threshold refreshed after every
+// group of W scan positions to the k-th largest score evaluated so far) is
+// sequential: whether the block at a position is kept depends on every
+// decision before its group.  But the threshold never falls inside a scan:
+// it is the k-th largest of a set that only grows (the running k largest
+// starts as the seeds' scores), so the k-th largest at the start of a range
+// of positions bounds every threshold inside that range from below.  A round
+// over a range of positions therefore
+//
+//  1. scores, over the whole GPU, every block of the range whose bound clears
+//     that floor -- a superset of the blocks the scan keeps there -- writing
+//     their scores and listing each non-seed key above the floor under its
+//     threshold group (temporal_round_kernel);
+//  2. replays the scan over the range in one workgroup per row, group by
+//     group: the group's decisions against the exact threshold, then the
+//     listed keys of its kept blocks join the running k largest; scored
+//     blocks that the replay prunes get -inf back, seeds excepted
+//     (temporal_resolve_kernel).
+//
+// The decisions, the evaluated keys and their scores are those of the
+// sequential scan (the persistent and per-wave paths of temporal.hip) bit for
+// bit.  The blocks scored and then pruned are the price of the parallel
+// scoring: the rounds split the scan at group boundaries so that later rounds
+// start from a higher floor.
+//
+// The running k largest in the replay (one wave, no barriers): a count per
+// 12-bit bin of the ordered key (E), the bin of the k-th largest (the cut
+// bin), the number of keys above that bin, the keys at or above it (V) and the
+// keys in it (B).  A bound outside the cut bin is decided by the bins alone;
+// one inside it needs the exact k-th largest, a select among B's keys, which
+// stays valid until keys join.  When the count above the cut bin reaches k the
+// cut moves up and V and B are rebuilt from V.
+#include <cstdlib>
+#include <mutex>
+#include <vector>
+
+#include "status.hpp"
+#include "temporal.hpp"
+
+namespace dsa {
+namespace {
+
+constexpr int kRoundThreads = 256;
+constexpr int kRoundWaves = kRoundThreads / kWave;
+constexpr int kRoundTiles = kRoundKeys / 16;
+static_assert(kRoundWaves * kRoundWaveKeys == kRoundKeys, "two 64-key units per scoring wave");
+
+#ifdef DSA_PHASE_TRACE
+// Per row (trace builds only): wall-clock ticks of the replay's phases and
+// event counts: 0 total, 1 decisions, 2 exact selects, 3 select count,
+// 4 joins, 5 cut moves, 6 move count, 7 compactions.
+__device__ uint64_t g_trace_resolve[kTraceWgs * kTraceMarks];
+#define RESOLVE_T0(v) uint64_t v = wall_clock64()
+#define RESOLVE_ADD(i, t0) \
+  do {                     \
+    if (lane == 0 && row < kTraceWgs) g_trace_resolve[(size_t)row * kTraceMarks + (i)] += wall_clock64() - (t0); \
+  } while (0)
+#define RESOLVE_COUNT(i) \
+  do {                   \
+    if (lane == 0 && row < kTraceWgs) g_trace_resolve[(size_t)row * kTraceMarks + (i)] += 1; \
+  } while (0)
+#else
+#define RESOLVE_T0(v) \
+  do {                \
+  } while (0)
+#define RESOLVE_ADD(i, t0) \
+  do {                     \
+  } while (0)
+#define RESOLVE_COUNT(i) \
+  do {                   \
+  } while (0)
+#endif
+
+struct RoundPlan {
+  int32_t pos_begin, pos_end;  // scan positions of the round (whole groups)
+  int32_t per_wg;              // scan positions per scoring workgroup
+  int32_t wgs_per_row;
+  int32_t group;         // scan positions per threshold group (the wave W)
+  int32_t first_round;   // the round's first group is the scan's first (seed threshold)
+  int32_t last_round;    // no round follows: the running k largest is not written back
+  int32_t round;         // index of the round (its list count)
+};
+
+// The key of the largest float at or below a float64 bound: for every float
+// t that is not NaN, (bound < t) == (upper_key(bound) < key(t)).  A NaN bound
+// (never pruned) maps to the largest key.
+__device__ __forceinline__ uint32_t upper_key(double bound) {
+  if (__builtin_isnan(bound)) return 0xffffffffu;
+  return float_to_ordered(__double2float_rd(bound));
+}
+
+// Ordered keys of NaN floats (a threshold that prunes nothing: `U < NaN` is
+// false), and the pruning test `U < t` on keys.
+__device__ __forceinline__ bool nan_key(uint32_t t) { return t > 0xff800000u || t < 0x007fffffu; }
+__device__ __forceinline__ bool prunes(uint32_t bound_key, uint32_t t) { return !nan_key(t) && bound_key < t; }
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// 1. Scoring.  Workgroup (row, part) covers scan positions
+// [pos_begin + part * per_wg, + per_wg) of the round (kRoundKeys keys): the
+// blocks there whose bound clears the row's floor are cut into 16-key tiles,
+// which the four waves score four at a time (one MFMA unit, two units per
+// wave) with the dense kernel's tile code.  Every scored key's score goes to
+// the scores row; a non-seed key above the floor is listed, with its group,
+// in the wave's own region of the row's list (no atomics).
+// ---------------------------------------------------------------------------
+template <class Tag, class KF>
+__global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalArgs a, RoundPlan rp) {
+  __shared__ uint32_t s_tile_key[kRoundTiles];
+  __shared__ uint16_t s_tile_group[kRoundTiles];
+  __shared__ __align__(16) uint32_t s_wsum[kRoundWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int row = blockIdx.x / rp.wgs_per_row;
+  const int part = blockIdx.x % rp.wgs_per_row;
+  const int p0 = rp.pos_begin + part * rp.per_wg;
+  const int p1 = min(p0 + rp.per_wg, rp.pos_end);
+  const int nb = a.blocks;
+  const int bs = a.block_size;
+  const int L = a.length;
+
+  // The query tiles, then the position's block and bound (one position per
+  // thread): their loads are in flight together.
+  uint4 qa[4][4] = {};
+  float wr[4][4] = {};
+  if (!a.source)
+    load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads, r, g,
+                                            qa, wr);
+  const uint32_t floor_key = a.ws.floor[row];
+  int blk = 0;
+  uint32_t my_tiles = 0;
+  const int p = p0 + tid;
+  if (p < p1) {
+    blk = (int)a.ws.order[(size_t)row * nb + p];
+    const double up = a.ws.upper_pos[(size_t)row * nb + p];
+    if (!prunes(upper_key(up), floor_key)) my_tiles = (uint32_t)((min(L, (blk + 1) * bs) - blk * bs + 15) >> 4);
+  }
+  uint32_t total = 0;
+  const uint32_t first = block_excl_scan<kRoundWaves>(my_tiles, s_wsum, total);
+  for (uint32_t j = 0; j < my_tiles; ++j) {
+    s_tile_key[first + j] = (uint32_t)(blk * bs) + 16u * j;
+    s_tile_group[first + j] = (uint16_t)(p / rp.group);
+  }
+  __syncthreads();
+
+  // recorded scores: an empty key buffer (every load reads 0 without touching memory)
+  const BufferRsrc keys = make_buffer(a.source ? nullptr : a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
+                                      a.source ? 0u : (uint32_t)L * KF::kRowBytes);
+  const BufferRsrc out = make_buffer(a.scores + (size_t)row * L, (uint32_t)L * 4u);
+  const uint32_t* mask = a.ws.seed_mask + (size_t)row * ((L + 31) / 32);
+  const int units = (int)(total + 3) >> 2;
+  const int t_res = lane >> 4;  // the tile of this lane's result
+  // Two units per wave, all loads first.
+  uint4 buf[2][4][KF::kRaw];
+  uint32_t word[2] = {0u, 0u};
+  float scale[2] = {1.f, 1.f};
+  int key_res[2];
+  bool valid[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int u = wave + kRoundWaves * h;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int ti = 4 * u + t;
+      const int key = ti < (int)total ? (int)s_tile_key[ti] + r : (int)kFarKey;
+      KF::load_buf(keys, key < L ? key : (int)kFarKey, g, buf[h][t]);
+    }
+    const int ti = 4 * u + t_res;
+    valid[h] = ti < (int)total;
+    key_res[h] = valid[h] ? (int)s_tile_key[ti] + r : 0;
+    valid[h] = valid[h] && key_res[h] < L;
+    if (valid[h]) {
+      word[h] = mask[key_res[h] >> 5];
+      if constexpr (KF::kScaled)
+        if (!a.source) scale[h] = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key_res[h] >> 7)];
+    }
+  }
+  uint32_t listed = 0;
+  uint64_t entry[2] = {0ull, 0ull};
+  uint32_t at[2] = {0u, 0u};
+  bool take[2] = {false, false};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int u = wave + kRoundWaves * h;
+    if (u >= units) break;  // uniform over the wave
+    float v;
+    if (a.source) {
+      v = valid[h] ? a.source[(size_t)row * a.source_stride + key_res[h]] : 0.f;
+    } else {
+      float sc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[h][t]);
+      v = unit_reduce(sc, g) * scale[h];
+    }
+    const int key = key_res[h];
+    if (valid[h]) buffer_store_f32(out, (uint32_t)key * 4u, v);
+    const uint32_t o = float_to_ordered(v);
+    const bool seed = (word[h] >> (key & 31)) & 1u;
+    take[h] = valid[h] && !seed && o > floor_key;
+    const uint64_t m = __ballot(take[h]);
+    if (take[h]) entry[h] = ((uint64_t)s_tile_group[4 * u + t_res] << 49) | ((uint64_t)key << 32) | o;
+    at[h] = listed + lanes_below(m);
+    listed += (uint32_t)__builtin_popcountll(m);
+  }
+  // One reservation per wave in the row's list of this round.
+  uint32_t base = 0;
+  if (lane == 0 && listed)
+    base = __hip_atomic_fetch_add(&a.ws.list_total[(size_t)row * kMaxRounds + rp.round], listed, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+  uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity + base;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    if (take[h]) list[at[h]] = entry[h];
+}
+
+// ---------------------------------------------------------------------------
+// 2. The replay of one row over the round's positions (one workgroup).
+//
+// Setup, by every thread: the running k largest (run, joined from the start)
+// and every listed key of the round are sorted by bin of their ordered key,
+// counting from the row's floor (every such key is at or above it) with bins
+// as fine as the span of the keys allows, 4096 in all: bin b holds slots
+// [end(b - 1), end(b)).  The listed keys are also sorted by threshold group
+// (items: slot | block << 18).
+//
+// Then wave 0 walks the groups: decisions against the threshold in force
+// (the seed threshold for the scan's first group; after it the k-th largest
+// joined key), then the listed keys of kept blocks join.  The threshold is
+// tracked by the bin holding it (the cut bin), the count of joined keys above
+// that bin and E, the joined keys per bin: a bound outside the cut bin is
+// decided by bins alone, one inside it needs the exact k-th largest, a select
+// among the cut bin's joined keys.
+// ---------------------------------------------------------------------------
+constexpr int kResolveThreads = 512;
+constexpr int kResolveWaves = kResolveThreads / kWave;
+constexpr int kSortCap = 8192;  // keys the replay sorts in LDS (more: in the workspace)
+constexpr int kBins = 4096;
+constexpr int kCutDigits = 1024;  // 10-bit digits of the select inside the cut bin
+
+struct ResolveShared {
+  uint32_t val[kSortCap];   // ordered keys, by bin
+  uint32_t item[kSortCap];  // listed keys by group: slot | block << 18
+  uint8_t join[kSortCap];   // joined (evaluated) flag of each slot
+  uint32_t end[kBins];      // past-the-end slot of each bin (after the scatter)
+  uint32_t E[kBins];        // joined keys per bin
+  uint32_t gend[kMaxTemporalBlocks];  // past-the-end item of each group (after the scatter)
+  uint32_t uk[kMaxTemporalBlocks];    // bound key at each of the round's positions
+  uint16_t blk[kMaxTemporalBlocks];   // block at each
+  uint8_t kept[kMaxTemporalBlocks];   // by block id
+  uint16_t resets[kMaxTemporalBlocks];
+  uint32_t digits[kCutDigits];
+  uint32_t wsum[kResolveWaves];
+  uint32_t above, max_key, nreset, tau, cut_bin, n_out;
+};
+
+// The j-th largest (1-based) of the joined keys in slots [s0, s1) of bin `bin`
+// (keys base .. base + 2^shift - 1), by one wave: a bitonic sort across the
+// lanes for at most 64 slots, else radix digits of the key's offset from the
+// bin's base (10 bits, then the rest).
+template <class P8, class P32>
+__device__ __forceinline__ uint32_t cut_select(P32 val, P8 join, uint32_t s0, uint32_t s1, uint32_t j, uint32_t base, uint32_t shift,
+                               uint32_t* digits) {
+  const uint32_t lane = lane_id();
+  const uint32_t n = s1 - s0;
+  if (n <= (uint32_t)kWave) {
+    uint32_t v = 0u;  // 0 sorts last
+    if (lane < n && join[s0 + lane]) v = val[s0 + lane];
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, stride, kWave);
+        const bool lower = (lane & (uint32_t)stride) == 0;
+        const bool descending = (lane & (uint32_t)size) == 0;
+        v = (lower == descending) ? max(v, o) : min(v, o);
+      }
+    }
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)(j - 1));
+  }
+  const uint32_t lo_bits = shift > 10 ? shift - 10 : 0;  // bits below the first digit
+  uint32_t want = j;
+  uint32_t hi = 0;
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1 && lo_bits == 0) break;
+    for (int i = (int)lane; i < kCutDigits; i += kWave) digits[i] = 0;
+    wave_sync();
+    for (uint32_t i = s0 + lane; i < s1; i += kWave) {
+      if (!join[i]) continue;
+      const uint32_t d = val[i] - base;
+      if (pass == 0)
+        __hip_atomic_fetch_add(&digits[d >> lo_bits], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      else if ((d >> lo_bits) == hi)
+        __hip_atomic_fetch_add(&digits[d & ((1u << lo_bits) - 1u)], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    wave_sync();
+    const Locate loc = wave_locate<kCutDigits / kWave>(digits, want, false);
+    wave_sync();
+    if (pass == 0) {
+      hi = loc.digit;
+      want = loc.rem;
+      if (lo_bits == 0) return base + hi;
+    } else {
+      return base + (hi << lo_bits) + loc.digit;
+    }
+  }
+  return base + (hi << lo_bits);
+}
+
+template <bool kSpill>
+__device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPlan& rp, ResolveShared& sh,
+                                            uint32_t n_listed) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = blockIdx.x;
+  const int nb = a.blocks;
+  const int k = a.k;
+  const int W = rp.group;
+  const int g_begin = rp.pos_begin / W;
+  const int n_groups = (rp.pos_end + W - 1) / W - g_begin;
+  const int n_pos = rp.pos_end - rp.pos_begin;
+  const uint32_t floor_key = a.ws.floor[row];
+  const uint32_t max_key = sh.max_key;
+  const uint32_t span = max_key - floor_key;
+  const uint32_t shift = span < (uint32_t)kBins ? 0u : 32u - (uint32_t)__builtin_clz(span) - 12u;
+  const size_t spill_at = (size_t)row * a.ws.spill_capacity;
+  uint32_t* val = kSpill ? a.ws.spill_val + spill_at : sh.val;
+  uint32_t* item = kSpill ? a.ws.spill_item + spill_at : sh.item;
+  uint8_t* join = kSpill ? a.ws.spill_join + spill_at : sh.join;
+  const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
+
+  // Bin and group counts (E counts the joined keys: run's).
+  for (int i = tid; i < kBins; i += kResolveThreads) {
+    sh.end[i] = 0;
+    sh.E[i] = 0;
+  }
+  for (int i = tid; i < n_groups; i += kResolveThreads) sh.gend[i] = 0;
+  if (tid == 0) sh.above = 0;
+  __syncthreads();
+  uint32_t above = 0;
+  for (int i = tid; i < k; i += kResolveThreads) {
+    const uint32_t b = (a.ws.run[(size_t)row * k + i] - floor_key) >> shift;
+    __hip_atomic_fetch_add(&sh.end[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_add(&sh.E[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    above += b > 0 ? 1u : 0u;
+  }
+  for (int off = 32; off > 0; off >>= 1) above += (uint32_t)__shfl_xor((int)above, off, kWave);
+  if (lane == 0 && above) __hip_atomic_fetch_add(&sh.above, above, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
+    const uint64_t x = list[e];
+    const uint32_t b = ((uint32_t)x - floor_key) >> shift;
+    __hip_atomic_fetch_add(&sh.end[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_add(&sh.gend[(int)(x >> 49) - g_begin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  // Exclusive scans: end[b] <- first slot of bin b, gend[g] <- first item of
+  // group g (the scatter's cursors; past it they hold each one's end).
+  {
+    constexpr int kPer = kBins / kResolveThreads;
+    uint32_t c[kPer];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      c[j] = sh.end[tid * kPer + j];
+      sum += c[j];
+    }
+    uint32_t total;
+    uint32_t before = block_excl_scan<kResolveWaves>(sum, sh.wsum, total);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      sh.end[tid * kPer + j] = before;
+      before += c[j];
+    }
+    __syncthreads();
+    constexpr int kGPer = kMaxTemporalBlocks / kResolveThreads;
+    uint32_t gc[kGPer];
+    uint32_t gsum = 0;
+#pragma unroll
+    for (int j = 0; j < kGPer; ++j) {
+      const int gi = tid * kGPer + j;
+      gc[j] = gi < n_groups ? sh.gend[gi] : 0u;
+      gsum += gc[j];
+    }
+    uint32_t gbefore = block_excl_scan<kResolveWaves>(gsum, sh.wsum, total);
+#pragma unroll
+    for (int j = 0; j < kGPer; ++j) {
+      const int gi = tid * kGPer + j;
+      if (gi < n_groups) sh.gend[gi] = gbefore;
+      gbefore += gc[j];
+    }
+  }
+  __syncthreads();
+  // Scatter: run's keys joined, listed keys not yet; listed keys' items by group.
+  for (int i = tid; i < k; i += kResolveThreads) {
+    const uint32_t v = a.ws.run[(size_t)row * k + i];
+    const uint32_t slot = __hip_atomic_fetch_add(&sh.end[(v - floor_key) >> shift], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    val[slot] = v;
+    join[slot] = 1;
+  }
+  for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
+    const uint64_t x = list[e];
+    const uint32_t v = (uint32_t)x;
+    const uint32_t slot = __hip_atomic_fetch_add(&sh.end[(v - floor_key) >> shift], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    val[slot] = v;
+    join[slot] = 0;
+    const uint32_t blk = (uint32_t)((x >> 32) & 0x1ffffu) / (uint32_t)a.block_size;
+    const uint32_t at = __hip_atomic_fetch_add(&sh.gend[(int)(x >> 49) - g_begin], 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    item[at] = slot | (blk << 18);
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    uint32_t bin = 0;  // the cut bin: the floor (the k-th largest) is in bin 0
+    uint32_t cut_above = sh.above;
+    uint32_t tau = floor_key;
+    bool tau_ok = true;
+    uint32_t nreset = 0;
+    const uint32_t seed_tau = a.ws.tau[row];
+    RESOLVE_T0(t_all);
+    auto bin_start = [&](uint32_t b) { return b ? sh.end[b - 1] : 0u; };
+    auto exact_tau = [&]() {
+      if (!tau_ok) {
+        RESOLVE_T0(t_sel);
+        tau = cut_select(val, join, bin_start(bin), sh.end[bin], (uint32_t)k - cut_above, floor_key + (bin << shift),
+                         shift, sh.digits);
+        tau_ok = true;
+        RESOLVE_ADD(2, t_sel);
+        RESOLVE_COUNT(3);
+      }
+      return tau;
+    };
+    for (int gi = 0; gi < n_groups; ++gi) {
+      const int q0 = gi * W;
+      const int q1 = min(q0 + W, n_pos);
+      const bool seed_group = rp.first_round && gi == 0;
+      // The cut bin's keys, and whether NaN keys can fall in it (then every
+      // decision takes the exact threshold).
+      const uint64_t lo = (uint64_t)floor_key + ((uint64_t)bin << shift);
+      const uint64_t hi = lo + (1ull << shift) - 1ull;
+      const bool finite_bin = lo >= 0x007fffffull && hi <= 0xff800000ull;
+      RESOLVE_T0(t_dec);
+      for (int c0 = q0; c0 < q1; c0 += kWave) {
+        const int q = c0 + lane;
+        const bool active = q < q1;
+        const uint32_t uk = active ? sh.uk[q] : 0u;
+        const int blk = active ? (int)sh.blk[q] : 0;
+        int verdict = 2;  // 0 pruned, 1 kept, 2 needs the exact threshold
+        if (seed_group) {
+          verdict = prunes(uk, seed_tau) ? 0 : 1;
+        } else if (finite_bin) {
+          verdict = uk < lo ? 0 : (uk > hi ? 1 : 2);
+        }
+        if (__ballot(active && verdict == 2)) {
+          const uint32_t t = exact_tau();
+          if (verdict == 2) verdict = prunes(uk, t) ? 0 : 1;
+        }
+        if (active) {
+          a.evaluated[(size_t)row * nb + blk] = (uint8_t)verdict;
+          sh.kept[blk] = (uint8_t)verdict;
+        }
+        const bool reset = active && verdict == 0 && !prunes(uk, floor_key);
+        const uint64_t m = __ballot(reset);
+        if (reset) sh.resets[nreset + lanes_below(m)] = (uint16_t)blk;
+        nreset += (uint32_t)__builtin_popcountll(m);
+      }
+      wave_sync();
+      RESOLVE_ADD(1, t_dec);
+      // The kept blocks' listed keys join.
+      RESOLVE_T0(t_join);
+      const uint32_t i0 = gi ? sh.gend[gi - 1] : 0u;
+      const uint32_t i1 = sh.gend[gi];
+      for (uint32_t c0 = i0; c0 < i1; c0 += kWave) {
+        const uint32_t i = c0 + (uint32_t)lane;
+        const uint32_t it = i < i1 ? item[i] : 0u;
+        const bool in = i < i1 && sh.kept[it >> 18];
+        uint32_t b = 0;
+        if (in) {
+          const uint32_t slot = it & 0x3ffffu;
+          join[slot] = 1;
+          b = (val[slot] - floor_key) >> shift;
+          __hip_atomic_fetch_add(&sh.E[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        cut_above += (uint32_t)__builtin_popcountll(__ballot(in && b > bin));
+        if (__ballot(in && b >= bin)) tau_ok = false;
+      }
+      wave_sync();
+      RESOLVE_ADD(4, t_join);
+      if (cut_above >= (uint32_t)k) {
+        // The cut moves up to the highest bin b with at least k joined keys at
+        // or above it.  (c counts the keys of the bins at or above s, so the
+        // bin is found below kBins; the bound only guards the loop.)
+        RESOLVE_T0(t_move);
+        RESOLVE_COUNT(6);
+        uint32_t s = bin + 1;
+        uint32_t c = cut_above;
+        for (int guard = 0; guard < kBins / kWave; ++guard) {
+          const uint32_t eb = s + (uint32_t)lane < (uint32_t)kBins ? sh.E[s + lane] : 0u;
+          const uint32_t incl = wave_incl_scan(eb);
+          const uint64_t m = __ballot(c - incl < (uint32_t)k);
+          if (m) {
+            const uint32_t l = (uint32_t)__builtin_ctzll(m);
+            bin = s + l;
+            cut_above = c - (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)l);
+            break;
+          }
+          c -= (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+          s += kWave;
+        }
+        tau_ok = false;
+        RESOLVE_ADD(5, t_move);
+      }
+    }
+    RESOLVE_ADD(0, t_all);
+    if (lane == 0) {
+      sh.nreset = nreset;
+      sh.cut_bin = bin;
+      sh.n_out = 0;
+    }
+    if (!rp.last_round) {
+      const uint32_t t = exact_tau();
+      if (lane == 0) sh.tau = t;
+    }
+  }
+  __syncthreads();
+  if (!rp.last_round) {
+    // The next round starts from the exact k largest: the joined keys above
+    // the threshold, then copies of it.
+    const uint32_t t = sh.tau;
+    const uint32_t s0 = sh.cut_bin ? sh.end[sh.cut_bin - 1] : 0u;
+    const uint32_t s1 = sh.end[kBins - 1];
+    for (uint32_t i = s0 + (uint32_t)tid; i < s1; i += kResolveThreads) {
+      const uint32_t v = val[i];
+      if (join[i] && v > t)
+        a.ws.run[(size_t)row * k +
+                 __hip_atomic_fetch_add(&sh.n_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] = v;
+    }
+    __syncthreads();
+    for (uint32_t c = sh.n_out + (uint32_t)tid; c < (uint32_t)k; c += kResolveThreads)
+      a.ws.run[(size_t)row * k + c] = t;
+    if (tid == 0) {
+      a.ws.tau[row] = t;
+      a.ws.floor[row] = t;
+    }
+  }
+  // Scored blocks the replay pruned: their keys back to -inf, seeds excepted.
+  const int bs = a.block_size;
+  const int L = a.length;
+  int bs_shift = 4;
+  while ((1 << bs_shift) < bs) ++bs_shift;
+  const uint32_t nreset = sh.nreset;
+  const uint32_t* mask = a.ws.seed_mask + (size_t)row * ((L + 31) / 32);
+  float* srow = a.scores + (size_t)row * L;
+  for (uint32_t i = (uint32_t)tid; i < nreset * (uint32_t)bs; i += kResolveThreads) {
+    const int key = (int)sh.resets[i >> bs_shift] * bs + (int)(i & (uint32_t)(bs - 1));
+    if (key < L && !((mask[key >> 5] >> (key & 31)) & 1u)) srow[key] = -__builtin_inff();
+  }
+}
+
+__global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(TemporalArgs a, RoundPlan rp) {
+  __shared__ ResolveShared sh;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int row = blockIdx.x;
+  const int nb = a.blocks;
+  const int k = a.k;
+  const int n_pos = rp.pos_end - rp.pos_begin;
+  for (int i = tid; i < n_pos; i += kResolveThreads) {
+    sh.blk[i] = (uint16_t)a.ws.order[(size_t)row * nb + rp.pos_begin + i];
+    sh.uk[i] = upper_key(a.ws.upper_pos[(size_t)row * nb + rp.pos_begin + i]);
+  }
+  if (tid == 0) sh.max_key = 0;
+  __syncthreads();
+  // Keys to sort and their largest (the span of the bins).
+  uint32_t mx = 0;
+  for (int i = tid; i < k; i += kResolveThreads) mx = max(mx, a.ws.run[(size_t)row * k + i]);
+  const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
+  const uint32_t n_listed = a.ws.list_total[(size_t)row * kMaxRounds + rp.round];
+  for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) mx = max(mx, (uint32_t)list[e]);
+  for (int off = 32; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, kWave));
+  if (lane == 0) __hip_atomic_fetch_max(&sh.max_key, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+  if ((uint32_t)k + n_listed <= (uint32_t)kSortCap)
+    resolve_row<false>(a, rp, sh, n_listed);
+  else
+    resolve_row<true>(a, rp, sh, n_listed);
+}
+
+// Round splits, as fractions of the scan's groups: DSA_AMD_TEMPORAL_ROUNDS, a
+// comma-separated increasing list in (0, 1), or "1" for a single round (read
+// at every step).  By default one split at a quarter of the scan, and two
+// (a tenth, three tenths) for rows of 64K keys or more, whose later rounds
+// gain more from a floor raised early (C3 at 16K keys: 124-148 us per step
+// with one split, 139-162 with two; C5 at 128K: 296-342 us with one,
+// 196-246 with two).
+std::vector<double> round_splits(int length) {
+  std::vector<double> splits;
+  const char* v = std::getenv("DSA_AMD_TEMPORAL_ROUNDS");
+  const char* s = v ? v : (length >= 65536 ? "0.1,0.3" : "0.25");
+  double last = 0.0;
+  while (*s) {
+    char* end = nullptr;
+    const double f = std::strtod(s, &end);
+    if (end == s) break;
+    if (f > last && f < 1.0) {
+      splits.push_back(f);
+      last = f;
+    }
+    if (*end != ',') break;
+    s = end + 1;
+  }
+  return splits;
+}
+
+template <class Tag, class KF>
+int launch_rounds(TemporalArgs& a, int32_t wave, hipStream_t stream) {
+  // Item and list packing: slots below 2^18, blocks below 2^14, keys below
+  // 2^17, groups below 2^15.
+  DSA_REQUIRE(wave > 0 && a.blocks <= kMaxTemporalBlocks && a.length <= (1 << 17) &&
+                  a.ws.spill_capacity < (1 << 18) && kRoundKeys % a.block_size == 0,
+              "step shape outside the dynamic rounds (blocks %d, length %d)", a.blocks, a.length);
+  const int W = wave;
+  const int nb = a.blocks;
+  const int groups = (nb + W - 1) / W;
+  std::vector<int> cuts = {0};
+  for (double f : round_splits(a.length)) {
+    const int c = (int)(f * groups + 0.5);
+    if (c > cuts.back() && c < groups && (int)cuts.size() < kMaxRounds) cuts.push_back(c);
+  }
+  cuts.push_back(groups);
+  const int per_wg = kRoundKeys / a.block_size;
+  for (size_t r = 0; r + 1 < cuts.size(); ++r) {
+    RoundPlan rp;
+    rp.pos_begin = cuts[r] * W;
+    rp.pos_end = min(cuts[r + 1] * W, nb);
+    rp.per_wg = per_wg;
+    rp.wgs_per_row = (rp.pos_end - rp.pos_begin + per_wg - 1) / per_wg;
+    rp.group = W;
+    rp.first_round = r == 0;
+    rp.last_round = r + 2 == cuts.size();
+    rp.round = (int32_t)r;
+    hipLaunchKernelGGL((temporal_round_kernel<Tag, KF>), dim3((unsigned)(a.rows * rp.wgs_per_row)),
+                       dim3(kRoundThreads), 0, stream, a, rp);
+    if (int st = check_launch("temporal_round_kernel")) return st;
+    hipLaunchKernelGGL(temporal_resolve_kernel, dim3((unsigned)a.rows), dim3(kResolveThreads), 0, stream, a, rp);
+    if (int st = check_launch("temporal_resolve_kernel")) return st;
+  }
+  return DSA_STATUS_OK;
+}
+
+}  // namespace
+
+int temporal_rounds(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream) {
+  switch (key_dtype) {
+    case DSA_DTYPE_BF16: return launch_rounds<Bf16Tag, KeysB16>(a, wave, stream);
+    case DSA_DTYPE_F16: return launch_rounds<F16Tag, KeysB16>(a, wave, stream);
+    default: return launch_rounds<Bf16Tag, KeysFP8>(a, wave, stream);
+  }
+}
+
+}  // namespace dsa
+
+#ifdef DSA_PHASE_TRACE
+// The replay's per-row phase totals (trace builds only).
+extern "C" int dsa_trace_temporal_resolve(uint64_t* host, int64_t n, int32_t clear) {
+  using namespace dsa;
+  DSA_REQUIRE(host && n >= 0 && n <= int64_t(kTraceWgs) * kTraceMarks, "bad trace read");
+  if (int st = check_hip(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace_resolve), (size_t)n * 8), "trace read"))
+    return st;
+  if (clear) {
+    static const uint64_t zeros[kTraceWgs * kTraceMarks] = {};
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_resolve), zeros, sizeof(zeros)), "trace clear");
+  }
+  return DSA_STATUS_OK;
+}
+#endif

@@ -120,3 +120,35 @@ def test_collect_trace_rows_are_the_dense_scores(device) -> None:
         assert row.size == n
         np.testing.assert_allclose(row, want, rtol=2e-3, atol=2e-3 * np.abs(want).max())
         assert np.all(np.isneginf(trace.scores[t, n:]))
+
+
+@pytest.mark.parametrize("order", ["previous_hot", "upper_hot", "oracle_current"])
+@pytest.mark.parametrize("gamma", [0.05, 1.0e8])
+def test_scan_order_matches_oracle(device, order, gamma) -> None:
+    # The scan order of the prep kernel against the oracle's sort (replay.py:
+    # 153-169).  A margin of 1e8 makes the float64 bounds of distinct block
+    # maxima round to one float, so the packed (float-keyed) sort must fall
+    # back to the exact float64 order.
+    rng = np.random.default_rng(7)
+    length, k, bs = 3000, 64, 16
+    previous = rng.standard_normal(length - 3).astype(np.float32)
+    current = np.concatenate([0.9 * previous + 0.1 * rng.standard_normal(previous.size), rng.standard_normal(3)])
+    current = current.astype(np.float32)
+    seed = torch.from_numpy(np.argsort(-previous.astype(np.float64), kind="stable")[:k].copy()).to(device)
+    truth = torch.from_numpy(np.argsort(-current.astype(np.float64), kind="stable")[:k].copy()).to(device)
+    t = replay._Transition(torch.from_numpy(previous).to(device), torch.from_numpy(current).to(device), k, bs,
+                           seed, truth)
+    oracle = order == "oracle_current"
+    _, _, _, got = t.run([gamma], order, True, oracle, 4)
+    blocks = -(-length // bs)
+    prev_max = np.full(blocks, -np.inf)
+    prev_max[: t.prev_max.shape[1]] = t.prev_max.cpu().double().numpy()[0]
+    upper = R.upper_bounds(prev_max, gamma, previous.size, length, bs)
+    hot = np.zeros(blocks, dtype=bool)
+    hot[np.minimum(t.seed_h // bs, blocks - 1)] = True
+    cur_max = t.cur_max.cpu().double().numpy()[0]
+    want = R.block_scan_order(order, cur_max if oracle else upper, cur_max, hot)
+    np.testing.assert_array_equal(got[0], want)
+    if gamma > 1e6 and not oracle:  # the case the packed sort cannot order alone
+        kept_upper = upper[np.isfinite(upper)]
+        assert np.unique(kept_upper.astype(np.float32)).size < np.unique(kept_upper).size

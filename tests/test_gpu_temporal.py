@@ -296,3 +296,76 @@ def test_static_step_cache_views_and_shapes(device, monkeypatch, batch, prev_len
         assert np.isneginf(scores[b][~ev]).all()
         masked = np.where(ev, dense[b], -np.inf).astype(np.float32)
         assert topk[b].tolist() == T.topk_index_order(masked, k).tolist(), b
+
+
+DYNAMIC_CASES = [
+    # block, scan order, wave, gamma_sigma, prev length, length, k, dtype, distinct keys (0: all distinct)
+    (16, "previous_hot", 33, 0.25, 16384, 16385, 2048, torch.bfloat16, 0),
+    (16, "address", 33, -0.5, 16384, 16385, 2048, torch.bfloat16, 0),
+    (32, "upper_hot", 17, -1.0, 16384, 16385, 2048, torch.float16, 0),
+    (64, "previous_hot", 1, -0.5, 4096, 4100, 256, torch.bfloat16, 0),
+    (128, "address", 5, -1.0, 16384, 16400, 2048, torch.bfloat16, 0),
+    (16, "address", 64, -1.0, 8000, 8003, 512, torch.bfloat16, 37),   # 37 distinct keys: scores tie in crowds
+    (64, "previous_hot", 8, -2.0, 3000, 3000, 1000, torch.bfloat16, 5),
+]
+
+
+@pytest.mark.parametrize("block,order,wave,gamma_sigma,prev_length,length,k,dtype,distinct", DYNAMIC_CASES)
+def test_dynamic_step_paths_agree(device, monkeypatch, block, order, wave, gamma_sigma, prev_length, length, k,
+                                  dtype, distinct) -> None:
+    # The dynamic filter runs in rounds (wide scoring of the blocks above the
+    # round's floor, then an exact replay per row); DSA_AMD_TEMPORAL_PATH=launch
+    # runs the sequential scan (persistent per-row scan or per-wave launches).
+    # Every round split must equal that path and the oracle's filter bit for
+    # bit, also when scores tie in crowds around the threshold.
+    print(f"dynamic paths bs={block} {order} W={wave} gs={gamma_sigma} L={length} k={k} {dtype} d={distinct}",
+          flush=True)
+    batch = 3
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=block * 3 + length + distinct)
+    if distinct:
+        keys = keys[:, torch.arange(length) % distinct]
+    q_prev, q_cur, keys = q_prev.to(dtype), q_cur.to(dtype), keys.to(dtype)
+    q_prev, q_cur, w, keys = q_prev.to(device), q_cur.to(device), w.to(device), keys.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys[:, :prev_length].contiguous(), k, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys, k, return_scores=True)[1].cpu().numpy()
+    gamma = torch.full((batch,), gamma_sigma * float(prev_scores.std()), device=device)
+
+    def run():
+        s = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                   method="dynamic", scan_order=order, wave=wave)
+        return [x.cpu().numpy() for x in (s.scores, s.evaluated_blocks, s.qk_scored, s.topk)]
+
+    results = {}
+    for splits in ("1", "0.25", "0.1,0.3,0.6"):
+        monkeypatch.setenv("DSA_AMD_TEMPORAL_ROUNDS", splits)
+        results[splits] = run()
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_ROUNDS")
+    monkeypatch.setenv("DSA_AMD_TEMPORAL_PATH", "launch")
+    sequential = run()
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_PATH")
+    for splits, got in results.items():
+        for name, a, b in zip(("scores", "kept", "qk", "topk"), got, sequential):
+            np.testing.assert_array_equal(a, b, err_msg=f"rounds {splits} vs the sequential scan: {name}")
+    scores, kept, qk, topk = sequential
+    seeds = prev_topk.cpu().numpy()
+    blocks = math.ceil(length / block)
+    for b in range(batch):
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+        upper = R.upper_bounds(previous_max, float(gamma[b]), prev_length, length, block)
+        hot = np.zeros(blocks, dtype=bool)
+        hot[seeds[b] // block] = True
+        scan = R.block_scan_order(order, upper, R.block_maxima(dense[b], block), hot)
+        current = dense[b].astype(np.float64)
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=True,
+                             fixed_threshold=float(current[seeds[b]].min()), wave=wave)
+        np.testing.assert_array_equal(kept[b], trace.kept, err_msg=f"row {b}: kept blocks")
+        assert int(qk[b]) == trace.scored, (b, int(qk[b]), trace.scored)
+        ev = trace.evaluated
+        np.testing.assert_array_equal(scores[b][ev], dense[b][ev])
+        assert np.isneginf(scores[b][~ev]).all()
+        masked = np.where(ev, dense[b], -np.inf).astype(np.float32)
+        assert topk[b].tolist() == T.topk_index_order(masked, k).tolist(), b
+    if not distinct:
+        assert not kept.all(), "the margin pruned nothing: the case does not exercise the replay"
