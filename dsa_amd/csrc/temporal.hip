@@ -32,6 +32,14 @@
 namespace dsa {
 namespace {
 
+// Scan orders ranked by temporal_rank_kernel (every sorted order but the
+// policy's buckets, which the prep kernel sorts itself).
+__host__ __device__ inline bool ranked_order(const TemporalArgs& a) {
+  const bool policy = a.policy_mode != 0;
+  const bool sorted = policy ? a.ap.p.order != DSA_ORDER_ADDRESS : a.scan_order != 0;
+  return sorted && !(policy && a.ap.p.order == DSA_ORDER_BUCKET);
+}
+
 // Bounds, scan order and a clean slate for one row (one workgroup per row).
 // Replay filter: U_b = prev max + gamma, +inf for blocks with new keys, order
 // (previous-hot first,) larger U, lower address.  Policy: U_b = risk, or +inf
@@ -117,7 +125,12 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     s_rank[b] = rank_value;
     h[j] = ~double_to_ordered(rank_value);
     l[j] = group | (uint32_t)b;
+    if (ranked_order(a)) {
+      a.ws.sort_hi[(size_t)row * nb + b] = h[j];
+      a.ws.sort_lo[(size_t)row * nb + b] = l[j];
+    }
   }
+  if (ranked_order(a)) return;  // temporal_rank_kernel orders the blocks
   if (!sorted) {
     for (int b = tid; b < nb; b += 1024) {
       a.ws.order[(size_t)row * nb + b] = b;
@@ -187,6 +200,47 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     }
 }
 
+
+// The scan order by ranks: block t's position is the number of blocks whose
+// (group, sort key, block) entry sorts before its own.  One workgroup per 16
+// blocks of a row, 16 threads per block each counting over a sixteenth of
+// the row's entries (in LDS), so the ranking of a row spreads over
+// ceil(blocks / 16) CUs instead of one CU sorting.
+constexpr int kRankTargets = 16;
+constexpr int kRankParts = 16;
+
+__global__ __launch_bounds__(kRankTargets * kRankParts) void temporal_rank_kernel(TemporalArgs a) {
+  __shared__ uint64_t s_hi[kMaxTemporalBlocks];
+  __shared__ uint32_t s_lo[kMaxTemporalBlocks];
+  __shared__ uint32_t s_part[kRankParts][kRankTargets];
+  const int tid = threadIdx.x;
+  const int nb = a.blocks;
+  const int per_row = (nb + kRankTargets - 1) / kRankTargets;
+  const int row = blockIdx.x / per_row;
+  const int target = (blockIdx.x % per_row) * kRankTargets + tid % kRankTargets;
+  const int part = tid / kRankTargets;
+  for (int i = tid; i < nb; i += kRankTargets * kRankParts) {
+    s_hi[i] = a.ws.sort_hi[(size_t)row * nb + i];
+    s_lo[i] = a.ws.sort_lo[(size_t)row * nb + i];
+  }
+  __syncthreads();
+  uint32_t count = 0;
+  if (target < nb) {
+    const uint64_t th = s_hi[target];
+    const uint32_t tl = s_lo[target];
+    for (int b = part; b < nb; b += kRankParts) count += sorts_before(s_hi[b], s_lo[b], th, tl) ? 1u : 0u;
+  }
+  s_part[part][tid % kRankTargets] = count;
+  __syncthreads();
+  if (tid < kRankTargets && target < nb) {
+    uint32_t rank = 0;
+#pragma unroll
+    for (int p = 0; p < kRankParts; ++p) rank += s_part[p][tid];
+    a.ws.order[(size_t)row * nb + rank] = (uint32_t)target;
+    a.ws.upper_pos[(size_t)row * nb + rank] = a.ws.upper[(size_t)row * nb + target];
+    if (a.order_out) a.order_out[(size_t)row * nb + rank] = target;
+  }
+}
 
 // The seeds: 64 per wave, gathered by index.
 template <class Tag, class KF>
@@ -692,6 +746,12 @@ template <class Tag, class KF>
 int launch_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(temporal_prep_kernel, dim3(a.rows), dim3(1024), 0, stream, a);
   if (int st = check_launch("temporal_prep_kernel")) return st;
+  if (ranked_order(a)) {
+    const int per_row = (a.blocks + kRankTargets - 1) / kRankTargets;
+    hipLaunchKernelGGL(temporal_rank_kernel, dim3((unsigned)(a.rows * per_row)), dim3(kRankTargets * kRankParts), 0,
+                       stream, a);
+    if (int st = check_launch("temporal_rank_kernel")) return st;
+  }
   hipLaunchKernelGGL((temporal_seed_kernel<Tag, KF>), dim3(a.rows * ((a.k + 255) / 256)), dim3(256), 0, stream, a);
   if (int st = check_launch("temporal_seed_kernel")) return st;
   if (wave > 0 && !legacy_paths_forced()) return temporal_rounds(a, wave, key_dtype, stream);

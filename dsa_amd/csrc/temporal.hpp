@@ -34,6 +34,8 @@ struct TemporalWorkspace {
   uint32_t* order;      // [rows][blocks] block ids in scan order
   double* upper;        // [rows][blocks] U_b, in double like the float64 reference
   double* upper_pos;    // [rows][blocks] the same, by scan position
+  uint64_t* sort_hi;    // [rows][blocks] scan-order sort key of each block (~ordered float64 rank value)
+  uint32_t* sort_lo;    // [rows][blocks] group << 31 | block
   uint32_t* seed_mask;  // [rows][ceil(L / 32)] keys evaluated as seeds
   // Dynamic rounds: the keys each round's scoring lists (a row's list is
   // entries [0, list_total[round])), and the replay's sorted keys when they
@@ -70,7 +72,9 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   const int64_t order_off = run_off + round(rows * k * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
   const int64_t upos_off = upper_off + round(rows * blocks * 8);
-  const int64_t mask_off = upos_off + round(rows * blocks * 8);
+  const int64_t shi_off = upos_off + round(rows * blocks * 8);
+  const int64_t slo_off = shi_off + round(rows * blocks * 8);
+  const int64_t mask_off = slo_off + round(rows * blocks * 4);
   const int64_t count_off = mask_off + round(rows * ((length + 31) / 32) * 4);
   const int64_t entries_off = count_off + round(rows * kMaxRounds * 4);
   const int64_t sval_off = entries_off + round(rows * list_capacity * 8);
@@ -91,6 +95,8 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
   ws.upper = base ? reinterpret_cast<double*>(p + upper_off) : nullptr;
   ws.upper_pos = base ? reinterpret_cast<double*>(p + upos_off) : nullptr;
+  ws.sort_hi = base ? reinterpret_cast<uint64_t*>(p + shi_off) : nullptr;
+  ws.sort_lo = base ? reinterpret_cast<uint32_t*>(p + slo_off) : nullptr;
   ws.seed_mask = base ? reinterpret_cast<uint32_t*>(p + mask_off) : nullptr;
   ws.list_total = base ? reinterpret_cast<uint32_t*>(p + count_off) : nullptr;
   ws.entries = base ? reinterpret_cast<uint64_t*>(p + entries_off) : nullptr;
