@@ -72,6 +72,7 @@ _SIGNATURES: dict[str, list] = {
         _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
         _p, _i64, _p,
     ],
+    "dsa_temporal_keys_loaded": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "dsa_certified_margins": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p],
     "dsa_approx_step": [
         _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64,

@@ -67,6 +67,7 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   if (tid == 0) {
     a.ws.tau[row] = 0xffffffffu;
     a.ws.floor[row] = 0xffffffffu;
+    a.ws.loaded[row] = 0;
     a.qk_scored[row] = 0;
     s_exact = 0;
   }
@@ -271,6 +272,10 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
   }
   uint32_t least = 0xffffffffu;  // this lane's seed key (none: neutral for the min)
   uint32_t lowest = 0xffffffffu;  // this lane's entry of run (the floor of the running k largest)
+  const uint64_t loads = __ballot(i < a.k && !a.source && seeds[i] >= 0 && seeds[i] < a.length);
+  if (lane == 0 && loads)
+    __hip_atomic_fetch_add(a.ws.loaded + row, (uint32_t)__builtin_popcountll(loads), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
   if (i < a.k) {
     const int64_t key = seeds[i];
     if (key < 0 || key >= a.length) {
@@ -868,6 +873,17 @@ using namespace dsa;
 extern "C" int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, int64_t k, int32_t block_size) {
   if (batch <= 0 || length <= 0 || k <= 0 || block_size <= 0) return 0;
   return temporal_layout(nullptr, batch, length, k, block_size).bytes;
+}
+
+extern "C" int dsa_temporal_keys_loaded(const void* workspace, int64_t batch, int64_t length, int64_t k,
+                                        int32_t block_size, int32_t* out, void* stream) {
+  using namespace dsa;
+  DSA_REQUIRE(workspace && out, "null pointer");
+  DSA_REQUIRE(batch > 0 && length > 0 && k > 0 && block_size > 0, "bad shape");
+  const TemporalWorkspace ws = temporal_layout(const_cast<void*>(workspace), batch, length, k, block_size);
+  return check_hip(hipMemcpyAsync(out, ws.loaded, (size_t)batch * 4, hipMemcpyDeviceToDevice,
+                                  static_cast<hipStream_t>(stream)),
+                   "keys loaded copy");
 }
 
 extern "C" int dsa_temporal_step(const void* queries, const float* weights, const void* keys,

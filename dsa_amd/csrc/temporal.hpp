@@ -30,6 +30,7 @@ struct TemporalWorkspace {
   uint32_t* qk_parts;   // [kMaxFusedWgs] keys each fused workgroup scored
   uint32_t* tau;        // [rows] ordered key of the threshold in force
   uint32_t* floor;      // [rows] least of run (the k-th largest evaluated score), dynamic rounds
+  uint32_t* loaded;     // [rows] key rows a dynamic step loaded (seeds + every key of its rounds' scored blocks)
   uint32_t* run;        // [rows][k] ordered keys of the k largest evaluated scores
   uint32_t* order;      // [rows][blocks] block ids in scan order
   double* upper;        // [rows][blocks] U_b, in double like the float64 reference
@@ -68,7 +69,8 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   const int64_t parts_off = slots_off + kMaxFusedWgs * 8;
   const int64_t tau_off = parts_off + kMaxFusedWgs * 4;
   const int64_t floor_off = tau_off + round(rows * 4);
-  const int64_t run_off = floor_off + round(rows * 4);
+  const int64_t loaded_off = floor_off + round(rows * 4);
+  const int64_t run_off = loaded_off + round(rows * 4);
   const int64_t order_off = run_off + round(rows * k * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
   const int64_t upos_off = upper_off + round(rows * blocks * 8);
@@ -91,6 +93,7 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   ws.qk_parts = base ? reinterpret_cast<uint32_t*>(p + parts_off) : nullptr;
   ws.tau = base ? reinterpret_cast<uint32_t*>(p + tau_off) : nullptr;
   ws.floor = base ? reinterpret_cast<uint32_t*>(p + floor_off) : nullptr;
+  ws.loaded = base ? reinterpret_cast<uint32_t*>(p + loaded_off) : nullptr;
   ws.run = base ? reinterpret_cast<uint32_t*>(p + run_off) : nullptr;
   ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
   ws.upper = base ? reinterpret_cast<double*>(p + upper_off) : nullptr;

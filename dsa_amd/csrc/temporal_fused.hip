@@ -147,11 +147,16 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   for (int t = 0; t < 4; ++t) loff[t] = KF::lane_offset(t, r, g);
   // Unit ul of the chunk through its own resource, tile t loaded iff bit t of
   // `tiles` (else an offset past the resource: zeros, no memory access).
+  // A seed's row is not loaded again: its score is the seed phase's.
   auto load_unit = [&](int ul, uint32_t tiles, uint4 (&buf)[4][KF::kRaw]) {
     const int ub = (base + 64 * ul) * KF::kRowBytes;
     const BufferRsrc unit = make_buffer(row_keys + ub, (uint32_t)max(valid_bytes - ub, 0));
+    const uint32_t sw[2] = {seed_bits[2 * ul], seed_bits[2 * ul + 1]};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) KF::load_at(unit, ((tiles >> t) & 1u) ? loff[t] : kOutOfRange, buf[t]);
+    for (int t = 0; t < 4; ++t) {
+      const bool seed = (sw[t >> 1] >> (16 * (t & 1) + r)) & 1u;
+      KF::load_at(unit, ((tiles >> t) & 1u) && !seed ? loff[t] : kOutOfRange, buf[t]);
+    }
   };
   // Lane l's score of key l of the unit.
   auto score_of = [&](int ul, const uint4 (&buf)[4][KF::kRaw]) {
@@ -276,7 +281,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
     const bool seed = (word >> (lane & 31)) & 1u;
     const bool kept = (tiles >> (lane >> 4)) & 1u;
     const int local = 64 * ul + lane;
-    const float s = kept ? v : (seed ? chunk_scores[local] : -__builtin_inff());
+    const float s = seed ? chunk_scores[local] : (kept ? v : -__builtin_inff());
     buffer_store_f32(out, (uint32_t)(base + local) * 4u, s);  // stores past L are dropped
     chunk_scores[local] = s;
     if (base + local < L)

@@ -114,6 +114,7 @@ template <class Tag, class KF>
 __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalArgs a, RoundPlan rp) {
   __shared__ uint32_t s_tile_key[kRoundTiles];
   __shared__ uint16_t s_tile_group[kRoundTiles];
+  __shared__ uint16_t s_tile_seeds[kRoundTiles];  // the tile's seeds (scored by the seed pass: not loaded again)
   __shared__ __align__(16) uint32_t s_wsum[kRoundWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -144,11 +145,14 @@ __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalA
     const double up = a.ws.upper_pos[(size_t)row * nb + p];
     if (!prunes(upper_key(up), floor_key)) my_tiles = (uint32_t)((min(L, (blk + 1) * bs) - blk * bs + 15) >> 4);
   }
+  const uint32_t* mask = a.ws.seed_mask + (size_t)row * ((L + 31) / 32);
   uint32_t total = 0;
   const uint32_t first = block_excl_scan<kRoundWaves>(my_tiles, s_wsum, total);
   for (uint32_t j = 0; j < my_tiles; ++j) {
-    s_tile_key[first + j] = (uint32_t)(blk * bs) + 16u * j;
+    const uint32_t key0 = (uint32_t)(blk * bs) + 16u * j;  // tiles are 16-key aligned
+    s_tile_key[first + j] = key0;
     s_tile_group[first + j] = (uint16_t)(p / rp.group);
+    s_tile_seeds[first + j] = (uint16_t)(mask[key0 >> 5] >> (key0 & 16u));
   }
   __syncthreads();
 
@@ -156,12 +160,11 @@ __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalA
   const BufferRsrc keys = make_buffer(a.source ? nullptr : a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
                                       a.source ? 0u : (uint32_t)L * KF::kRowBytes);
   const BufferRsrc out = make_buffer(a.scores + (size_t)row * L, (uint32_t)L * 4u);
-  const uint32_t* mask = a.ws.seed_mask + (size_t)row * ((L + 31) / 32);
   const int units = (int)(total + 3) >> 2;
   const int t_res = lane >> 4;  // the tile of this lane's result
-  // Two units per wave, all loads first.
+  // Two units per wave, all loads first.  A seed's row is not loaded (its
+  // score is the seed pass's, already in the scores row).
   uint4 buf[2][4][KF::kRaw];
-  uint32_t word[2] = {0u, 0u};
   float scale[2] = {1.f, 1.f};
   int key_res[2];
   bool valid[2];
@@ -171,18 +174,16 @@ __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalA
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int ti = 4 * u + t;
-      const int key = ti < (int)total ? (int)s_tile_key[ti] + r : (int)kFarKey;
+      int key = (int)kFarKey;
+      if (ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u)) key = (int)s_tile_key[ti] + r;
       KF::load_buf(keys, key < L ? key : (int)kFarKey, g, buf[h][t]);
     }
     const int ti = 4 * u + t_res;
-    valid[h] = ti < (int)total;
+    valid[h] = ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u);
     key_res[h] = valid[h] ? (int)s_tile_key[ti] + r : 0;
     valid[h] = valid[h] && key_res[h] < L;
-    if (valid[h]) {
-      word[h] = mask[key_res[h] >> 5];
-      if constexpr (KF::kScaled)
-        if (!a.source) scale[h] = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key_res[h] >> 7)];
-    }
+    if constexpr (KF::kScaled)
+      if (valid[h] && !a.source) scale[h] = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key_res[h] >> 7)];
   }
   uint32_t listed = 0;
   uint64_t entry[2] = {0ull, 0ull};
@@ -204,18 +205,22 @@ __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalA
     const int key = key_res[h];
     if (valid[h]) buffer_store_f32(out, (uint32_t)key * 4u, v);
     const uint32_t o = float_to_ordered(v);
-    const bool seed = (word[h] >> (key & 31)) & 1u;
-    take[h] = valid[h] && !seed && o > floor_key;
+    take[h] = valid[h] && o > floor_key;
     const uint64_t m = __ballot(take[h]);
     if (take[h]) entry[h] = ((uint64_t)s_tile_group[4 * u + t_res] << 49) | ((uint64_t)key << 32) | o;
     at[h] = listed + lanes_below(m);
     listed += (uint32_t)__builtin_popcountll(m);
   }
-  // One reservation per wave in the row's list of this round.
+  // One reservation per wave in the row's list of this round, and the key
+  // rows the wave loaded.
   uint32_t base = 0;
   if (lane == 0 && listed)
     base = __hip_atomic_fetch_add(&a.ws.list_total[(size_t)row * kMaxRounds + rp.round], listed, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t rows_loaded = (uint32_t)__builtin_popcountll(__ballot(valid[0])) +
+                               (uint32_t)__builtin_popcountll(__ballot(valid[1]));
+  if (lane == 0 && rows_loaded && !a.source)
+    __hip_atomic_fetch_add(a.ws.loaded + row, rows_loaded, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
   uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity + base;
 #pragma unroll

@@ -53,6 +53,24 @@ def _workspace(device, stream, batch, length, k, block_size) -> torch.Tensor:
     return _lib.workspace("temporal", device, stream, need, zeroed=True, rows=0)
 
 
+def keys_loaded(step: TemporalStep, block_size: int) -> torch.Tensor:
+    """Key rows the last dynamic step on the current stream loaded, per row
+    (int32 [B]): the seeds plus every key of the blocks its rounds scored, a
+    superset of ``step.qk_scored`` (the keys the scan evaluates).  Read from
+    the step's workspace, so call it before another step runs on the stream.
+    No counterpart in the reference, whose replay prices bytes from the keys
+    scored (replay.py:369-371)."""
+
+    batch, length = step.scores.shape
+    k = step.topk.shape[1]
+    device = step.scores.device
+    stream = _lib.stream_of(step.scores)
+    ws = _workspace(device, stream, batch, length, k, block_size)
+    out = torch.empty(batch, device=device, dtype=torch.int32)
+    _lib.call("dsa_temporal_keys_loaded", _lib.ptr(ws), batch, length, k, block_size, _lib.ptr(out), stream)
+    return out
+
+
 def _outputs(device, batch: int, length: int, blocks: int, k: int):
     """The step's four outputs as views of one allocation (one allocator
     call per step instead of four): scores fp32 [B, L], top-k int64 [B, k],

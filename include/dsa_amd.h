@@ -342,14 +342,31 @@ int dsa_score_topk_noalloc(const void* queries, const float* weights, const void
  *               first use (the static step's generation-stamped exchange
  *               slots, which no later call misreads); calls that share it
  *               must be ordered (one stream).
- * Pruned blocks load no key bytes.  A static step (wave 0) whose shape fits
- * the decode step's candidate-list plan and whose workgroups fit on the
- * device at once is one scoring launch plus the list select; other steps
- * cost 4 + 2 * ceil(blocks / W) launches, or 6 with the persistent per-row
- * scan (more than 16 waves of W blocks).  DSA_AMD_TEMPORAL_PATH=launch in the
- * environment keeps static steps on the launch path.
+ * A static step (wave 0) loads only the seeds and the kept blocks: when its
+ * shape fits the decode step's candidate-list plan and its workgroups fit on
+ * the device at once it is one scoring launch plus the list select.  A
+ * dynamic step (wave > 0) runs in rounds that split the scan at group
+ * boundaries (DSA_AMD_TEMPORAL_ROUNDS: fractions of the groups, default 0.25,
+ * or 0.1,0.3 from 64K keys): each round scores every block of its positions
+ * whose bound clears the threshold at the round's start, over the whole GPU,
+ * then replays the scan's decisions exactly in one workgroup per row; blocks
+ * scored there and then pruned are reported by dsa_temporal_keys_loaded.
+ * DSA_AMD_TEMPORAL_PATH=launch in the environment keeps every step on the
+ * sequential launch paths (per-wave block and refresh launches, or the
+ * persistent per-row scan), which load only the blocks they keep.
  * ------------------------------------------------------------------------ */
 int64_t dsa_temporal_workspace_bytes(int64_t batch, int64_t length, int64_t k, int32_t block_size);
+
+/* Key rows the last dynamic temporal step on `workspace` loaded, per row
+ * (int32 [batch], device memory, written on `stream`): the seeds plus every
+ * key of the blocks its rounds scored, a superset of the keys it reports in
+ * qk_scored.  Defined after a dynamic step (wave > 0) on the default path;
+ * the other paths load the keys they score.  No counterpart in the reference,
+ * whose replay (replay.py:369-371) prices bytes from the keys scored: this is
+ * the measured side of that figure. */
+int dsa_temporal_keys_loaded(const void* workspace, int64_t batch, int64_t length, int64_t k, int32_t block_size,
+                             int32_t* out, void* stream);
+
 int dsa_temporal_step(const void* queries, const float* weights, const void* keys, int64_t key_stride,
                       const float* key_scales, const float* prev_block_max, int64_t prev_length,
                       const int64_t* prev_topk,

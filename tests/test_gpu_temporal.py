@@ -331,15 +331,22 @@ def test_dynamic_step_paths_agree(device, monkeypatch, block, order, wave, gamma
     dense = decode.indexer_topk(q_cur, w, keys, k, return_scores=True)[1].cpu().numpy()
     gamma = torch.full((batch,), gamma_sigma * float(prev_scores.std()), device=device)
 
-    def run():
+    def run(loads=None):
         s = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
                                    method="dynamic", scan_order=order, wave=wave)
+        if loads is not None:
+            loads.append(temporal.keys_loaded(s, block).cpu().numpy())
         return [x.cpu().numpy() for x in (s.scores, s.evaluated_blocks, s.qk_scored, s.topk)]
 
     results = {}
     for splits in ("1", "0.25", "0.1,0.3,0.6"):
         monkeypatch.setenv("DSA_AMD_TEMPORAL_ROUNDS", splits)
-        results[splits] = run()
+        loads = []
+        results[splits] = run(loads)
+        # Key rows loaded: every evaluated key (seeds are loaded by the seed
+        # pass, kept blocks by a round), at most the seeds and every key once.
+        qk = results[splits][2]
+        assert (loads[0] >= qk).all() and (loads[0] <= k + length).all(), (splits, loads[0], qk)
     monkeypatch.delenv("DSA_AMD_TEMPORAL_ROUNDS")
     monkeypatch.setenv("DSA_AMD_TEMPORAL_PATH", "launch")
     sequential = run()
