@@ -83,6 +83,14 @@ def test_approx_step_c3_shape_trajectory(device, policy, block, wave, gamma_sigm
     run_trajectory(device, policy, block, wave, gamma_sigma, batch=4, length=16384, steps=20, k=2048, seed=4242)
 
 
+def test_approx_step_c5_length_trajectory(device) -> None:
+    # The C5 length (131072 keys, block 64, 96-block groups): the dynamic scan
+    # runs in three rounds, with the policy's risk as the bound.
+    policy = A.ApproxPolicy(name="c5_dynamic_previous_max", dynamic_threshold=True, order="previous_max",
+                            cold_streak=0)
+    run_trajectory(device, policy, 64, 96, -0.3, batch=2, length=131069, steps=3, k=2048, seed=5150)
+
+
 def run_trajectory(device, policy, block, wave, gamma_sigma, *, batch, length, steps, k, seed) -> None:
     print(f"approx {policy.name} bs={block} wave={wave} gamma={gamma_sigma}sigma B={batch} L={length} "
           f"steps={steps} k={k}", flush=True)

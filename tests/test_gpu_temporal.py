@@ -307,6 +307,9 @@ DYNAMIC_CASES = [
     (128, "address", 5, -1.0, 16384, 16400, 2048, torch.bfloat16, 0),
     (16, "address", 64, -1.0, 8000, 8003, 512, torch.bfloat16, 37),   # 37 distinct keys: scores tie in crowds
     (64, "previous_hot", 8, -2.0, 3000, 3000, 1000, torch.bfloat16, 5),
+    # k = 4096 of 16K keys: a single round lists more keys than the replay's
+    # LDS holds, so its sort spills to the workspace
+    (16, "address", 64, -0.5, 16384, 16385, 4096, torch.bfloat16, 0),
 ]
 
 
@@ -376,3 +379,54 @@ def test_dynamic_step_paths_agree(device, monkeypatch, block, order, wave, gamma
         assert topk[b].tolist() == T.topk_index_order(masked, k).tolist(), b
     if not distinct:
         assert not kept.all(), "the margin pruned nothing: the case does not exercise the replay"
+
+
+def test_dynamic_step_keys_loaded_accounting(device, monkeypatch) -> None:
+    # Key rows a dynamic step loads on the rounds path: the seeds, then per
+    # round every non-seed key of the blocks whose bound clears the round's
+    # floor (the k-th largest evaluated score at the round's start: the seed
+    # threshold for the first round).  Recomputed on the host from the
+    # oracle's filter run up to each round boundary.
+    print("dynamic keys loaded accounting", flush=True)
+    batch, prev_length, length, k, block, wave = 2, 8000, 8003, 512, 16, 16
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=77)
+    q_prev, q_cur, w, keys = q_prev.to(device), q_cur.to(device), w.to(device), keys.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys[:, :prev_length].contiguous(), k, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys, k, return_scores=True)[1].cpu().numpy()
+    gamma = torch.full((batch,), -0.5 * float(prev_scores.std()), device=device)
+    seeds = prev_topk.cpu().numpy()
+    blocks = math.ceil(length / block)
+    groups = math.ceil(blocks / wave)
+    for splits, fractions in (("1", []), ("0.25", [0.25])):
+        monkeypatch.setenv("DSA_AMD_TEMPORAL_ROUNDS", splits)
+        step = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                      method="dynamic", scan_order="previous_hot", wave=wave)
+        got = temporal.keys_loaded(step, block).cpu().numpy()
+        cuts = [0] + [int(f * groups + 0.5) for f in fractions] + [groups]
+        for b in range(batch):
+            previous_max = np.full(blocks, -np.inf)
+            previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+            upper = R.upper_bounds(previous_max, float(gamma[b]), prev_length, length, block)
+            hot = np.zeros(blocks, dtype=bool)
+            hot[seeds[b] // block] = True
+            order = R.block_scan_order("previous_hot", upper, R.block_maxima(dense[b], block), hot)
+            current = dense[b].astype(np.float64)
+            tau_seed = float(current[seeds[b]].min())
+            is_seed = np.zeros(length, dtype=bool)
+            is_seed[seeds[b]] = True
+            want = k
+            for r in range(len(cuts) - 1):
+                lo, hi = cuts[r] * wave, min(cuts[r + 1] * wave, blocks)
+                if r == 0:
+                    floor = tau_seed
+                else:  # the k-th largest evaluated score after the scan's first lo positions
+                    trace = R.run_filter(current, seeds[b], k, block, upper, order[:lo], dynamic=True,
+                                         fixed_threshold=tau_seed, wave=wave)
+                    floor = trace.threshold_final
+                for blk in order[lo:hi]:
+                    if not upper[blk] < np.float32(floor):
+                        keys_b = np.arange(blk * block, min(length, (blk + 1) * block))
+                        want += int((~is_seed[keys_b]).sum())
+            assert int(got[b]) == want, (splits, b, int(got[b]), want)
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_ROUNDS")
