@@ -73,6 +73,29 @@ def test_many_short_rows(device, kind, length, k) -> None:
         assert np.all(np.isneginf(val_index[r].cpu().numpy()[~chosen]))
 
 
+@pytest.mark.parametrize("rows", [2049, 3001, 4096])
+def test_ragged_rows_beyond_resident(device, rows) -> None:
+    # More ragged rows than the chip holds at once (2048 256-thread
+    # workgroups), odd counts included.
+    print(f"topk ragged rows={rows}", flush=True)
+    length, k = 1024, 64
+    host = rows_for("ties", rows, length, seed=rows)
+    lengths = np.random.default_rng(rows).integers(0, length + 1, size=rows).astype(np.int32)
+    lengths[rows // 2] = length
+    x = torch.from_numpy(host).to(device)
+    lens = torch.from_numpy(lengths).to(device)
+    idx_sorted, val_sorted = metrics.topk(x, k, sorted=True, row_lengths=lens, return_values=True)
+    idx_index = metrics.topk(x, k, sorted=False, row_lengths=lens).cpu().numpy()
+    idx_sorted, val_sorted = idx_sorted.cpu().numpy(), val_sorted.cpu().numpy()
+    for r in range(rows):
+        n = int(lengths[r])
+        want = T.topk_sorted_padded(host[r], k, n)
+        assert idx_sorted[r].tolist() == want.tolist(), r
+        chosen = want >= 0
+        np.testing.assert_array_equal(val_sorted[r][chosen], host[r][want[chosen]])
+        assert idx_index[r].tolist() == T.topk_index_order(host[r], k, n).tolist(), r
+
+
 @pytest.mark.parametrize("kind", ["normal", "ties", "neginf"])
 @pytest.mark.parametrize("rows,length,k", [(1, 16384, 2048), (3, 32768, 2048), (2, 50000, 4096), (1, 262144, 100)])
 def test_few_long_rows_distributed(device, kind, rows, length, k) -> None:
