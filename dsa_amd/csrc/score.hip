@@ -267,27 +267,36 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
 
 // ---------------------------------------------------------------------------
 // Multi-query (prefill) scoring: many query blocks against one shared key set.
-// A workgroup owns kPrefillQueries consecutive queries of one key set
-// (kPrefillQPW per wave) and streams the key units they see through LDS: each 64-key unit is
-// loaded from memory once and scored for all eight queries, instead of once
-// per query.  Rows are padded to kPrefillRow bytes so the 16 rows a lane
+// A workgroup owns kPrefillQueries consecutive queries of one key set, one
+// per wave, and streams the key units they see through LDS: each 64-key unit
+// is loaded from memory once and scored for all eight queries, instead of
+// once per query.  Rows are padded to kPrefillRow bytes so the 16 rows a lane
 // group reads fall on different banks.  With a causal limit the heaviest
-// query blocks are dispatched first.
+// query blocks are dispatched first.  One query per wave needs about half the
+// registers of two, so two waves share each SIMD.
 // ---------------------------------------------------------------------------
 constexpr int kPrefillQueries = 8;
 constexpr int kPrefillRow = 272;
-constexpr int kPrefillQPW = 1;  // queries per wave
 
-// QPW queries per wave, kPrefillQueries / QPW waves per workgroup.  With one
-// query per wave the wave needs about half the registers of two, so two waves
-// share each SIMD and one's ReLU / weight / reduction VALU work runs under the
-// other's MFMAs.
-template <class Tag, int QPW>
-__global__ __launch_bounds__(64 * kPrefillQueries / QPW) void prefill_scores_kernel(DenseArgs a, int32_t qblocks,
-                                                                                    int32_t keysets) {
-  constexpr int kThreads = 64 * kPrefillQueries / QPW;
-  constexpr int kRowSplit = kThreads / 64;         // threads per staged key row
-  constexpr int kRowBytesPer = 256 / kRowSplit;    // bytes each of them moves
+// The unit loop is software-pipelined across tiles and units: step t issues
+// the MFMAs of tile t and the ReLU / weight work of tile t - 1 (tile 3 of the
+// previous unit at step 0), interleaved one MFMA to two VALU instructions by
+// scheduling groups, while the next tile's LDS reads are in flight.  The
+// previous unit's reduction and store follow step 0.
+__device__ __forceinline__ void mfma_valu_interleave() {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+  }
+}
+
+template <class Tag>
+__global__ __launch_bounds__(64 * kPrefillQueries) void prefill_scores_kernel(DenseArgs a, int32_t qblocks,
+                                                                            int32_t keysets) {
+  constexpr int kThreads = 64 * kPrefillQueries;
+  constexpr int kRowSplit = kThreads / 64;
+  constexpr int kRowBytesPer = 256 / kRowSplit;
   constexpr int kVecs = kRowBytesPer / 16;
   __shared__ __align__(16) uint8_t lds[2][64 * kPrefillRow];
   const int lane = threadIdx.x & 63;
@@ -302,28 +311,21 @@ __global__ __launch_bounds__(64 * kPrefillQueries / QPW) void prefill_scores_ker
   const int t_last = min(qpk - 1, qb * kPrefillQueries + kPrefillQueries - 1);
   const int units = (visible(t_last) + 63) >> 6;
 
-  uint4 qa[QPW][4][4];
-  float wr[QPW][4][4];
-  bool active[QPW];
-  int vis[QPW];
-  float* orow[QPW];
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi) {
-    const int t = qb * kPrefillQueries + QPW * wave + qi;
-    active[qi] = t < qpk;
-    const int64_t seq = keyset * qpk + (active[qi] ? t : 0);
-    load_dense_head_tiles<4, KeysB16::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa[qi],
-                                                 wr[qi]);
-    vis[qi] = active[qi] ? visible(t) : 0;
-    orow[qi] = a.out + seq * a.out_stride;
-  }
+  uint4 qa[4][4];
+  float wr[4][4];
+  const int t = qb * kPrefillQueries + wave;
+  const bool active = t < qpk;
+  const int64_t seq = keyset * qpk + (active ? t : 0);
+  load_dense_head_tiles<4, KeysB16::kNaturalK>(a.q + seq * a.q_stride, a.w + seq * a.w_stride, r, g, qa, wr);
+  const int vis = active ? visible(t) : 0;
+  float* orow = a.out + seq * a.out_stride;
+  const BufferRsrc orsrc = make_buffer(orow, active ? (uint32_t)L * 4u : 0u);
 
-  // Cooperative unit load: thread i moves kRowBytesPer bytes of row i / kRowSplit.
   const BufferRsrc kr = make_buffer(a.keys + keyset * a.key_stride * KeysB16::kRowBytes,
                                     (uint32_t)L * KeysB16::kRowBytes);
   const int lrow = threadIdx.x / kRowSplit;
   const int lpart = threadIdx.x % kRowSplit;
-  uint4 stage[kVecs];
+  uint4 stage[kVecs];  // the next unit, in flight while this one is scored
   auto fetch = [&](int u) {
     const uint32_t off = (uint32_t)(u * 64 + lrow) * KeysB16::kRowBytes + lpart * kRowBytesPer;
 #pragma unroll
@@ -334,48 +336,74 @@ __global__ __launch_bounds__(64 * kPrefillQueries / QPW) void prefill_scores_ker
 #pragma unroll
     for (int k = 0; k < kVecs; ++k) *reinterpret_cast<uint4*>(dst + 16 * k) = stage[k];
   };
-  if (units > 0) {
-    fetch(0);
-    put(0);
-  }
-  __syncthreads();
-  for (int u = 0; u < units; ++u) {
-    if (u + 1 < units) fetch(u + 1);  // in flight while this unit is scored
-    const uint8_t* base = lds[u & 1];
-    float s[QPW][4];
-    // Software-pipelined over the unit's four tiles: the MFMAs of tile t are
-    // issued before the ReLU / weight VALU work of tile t - 1, which depends
-    // only on the previous accumulators, so the two can co-execute.
-    floatx4 acc[2][QPW][4];
+  auto read_tile = [&](const uint8_t* base, int tile, uint4 (&raw)[KeysB16::kRaw]) {
+    const uint8_t* row = base + (16 * tile + r) * kPrefillRow + g * 16;
 #pragma unroll
-    for (int t = 0; t <= 4; ++t) {
-      if (t < 4) {
-        uint4 raw[KeysB16::kRaw];
-        const uint8_t* row = base + (16 * t + r) * kPrefillRow + g * 16;
-#pragma unroll
-        for (int c = 0; c < KeysB16::kRaw; ++c) raw[c] = *reinterpret_cast<const uint4*>(row + 64 * c);
-#pragma unroll
-        for (int qi = 0; qi < QPW; ++qi) tile_mfma<Tag, 4, KeysB16>(qa[qi], raw, acc[t & 1][qi]);
-      }
-      if (t > 0) {
-#pragma unroll
-        for (int qi = 0; qi < QPW; ++qi) s[qi][t - 1] = tile_reduce<4>(wr[qi], acc[(t - 1) & 1][qi]);
-      }
-    }
+    for (int c = 0; c < KeysB16::kRaw; ++c) raw[c] = *reinterpret_cast<const uint4*>(row + 64 * c);
+  };
+  // Stores are unconditional: the buffer bounds drop keys past L, every key
+  // of an inactive query and the "previous unit" of the first iteration.
+  auto store_unit = [&](const float (&sp)[4], int u) {
+    const float score = unit_reduce(sp, g);
     const int key = u * 64 + lane;
+    buffer_store_f32(orsrc, (uint32_t)key * 4u, key < vis ? score : -__builtin_inff());
+  };
+
+  // Every load is unconditional (a fetch past the last unit re-reads it), so
+  // that the compiler counts the memory operations in flight exactly.
+  const int last_unit = max(units - 1, 0);
+  fetch(0);
+  put(0);
+  // The query tiles, weights and first unit have landed.  Without this wait
+  // the compiler sees the query loads in flight at the loop head and places
+  // their waits inside the loop, where they also wait for each iteration's
+  // prefetch.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  floatx4 acc0[4], acc1[4];
 #pragma unroll
-    for (int qi = 0; qi < QPW; ++qi) {
-      const float score = unit_reduce(s[qi], g);
-      if (active[qi] && key < L) orow[qi][key] = key < vis[qi] ? score : -__builtin_inff();
-    }
-    if (u + 1 < units) put((u + 1) & 1);  // the buffer scored in the previous iteration
+  for (int m = 0; m < 4; ++m) acc1[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float sp[4] = {0.f, 0.f, 0.f, 0.f};
+  uint4 rawA[KeysB16::kRaw], rawB[KeysB16::kRaw];
+  for (int u = 0; u < units; ++u) {
+    fetch(min(u + 1, last_unit));
+    // Keep the loads ahead of the scoring: left to itself the scheduler
+    // sinks them to the put at the end of the iteration.
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* base = lds[u & 1];
+    read_tile(base, 0, rawA);
+    read_tile(base, 1, rawB);
+    // Step 0: tile 0's MFMAs; the previous unit's tile 3 reduced.
+    tile_mfma<Tag, 4, KeysB16>(qa, rawA, acc0);
+    sp[3] = tile_reduce<4>(wr, acc1);
+    mfma_valu_interleave();
+    store_unit(sp, u - 1);
+    read_tile(base, 2, rawA);
+    tile_mfma<Tag, 4, KeysB16>(qa, rawB, acc1);
+    sp[0] = tile_reduce<4>(wr, acc0);
+    mfma_valu_interleave();
+    read_tile(base, 3, rawB);
+    tile_mfma<Tag, 4, KeysB16>(qa, rawA, acc0);
+    sp[1] = tile_reduce<4>(wr, acc1);
+    mfma_valu_interleave();
+    tile_mfma<Tag, 4, KeysB16>(qa, rawB, acc1);
+    sp[2] = tile_reduce<4>(wr, acc0);
+    mfma_valu_interleave();
+    // Into the buffer scored last iteration; unconditional (past the last
+    // unit it stages a re-read nobody scores), so that the iteration is one
+    // basic block and no reduction is sunk below a branch, away from the
+    // MFMAs it is interleaved with.
+    put((u + 1) & 1);
     __syncthreads();
   }
+  if (units > 0) {
+    sp[3] = tile_reduce<4>(wr, acc1);
+    store_unit(sp, units - 1);
+  }
   // Keys past this workgroup's units are invisible to all of its queries.
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi)
-    if (active[qi])
-      for (int key = units * 64 + lane; key < L; key += 64) orow[qi][key] = -__builtin_inff();
+  if (active)
+    for (int key = units * 64 + lane; key < L; key += 64) orow[key] = -__builtin_inff();
 }
 
 // ---------------------------------------------------------------------------
@@ -628,9 +656,8 @@ int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
       const int64_t keysets = sequences / a.queries_per_keyset;
       const int64_t qblocks = (a.queries_per_keyset + kPrefillQueries - 1) / kPrefillQueries;
       if (keysets * a.queries_per_keyset == sequences && qblocks * keysets <= 0x7fffffffLL) {
-        hipLaunchKernelGGL((prefill_scores_kernel<Tag, kPrefillQPW>), dim3((unsigned)(qblocks * keysets)),
-                           dim3(64 * kPrefillQueries / kPrefillQPW), 0, stream, a,
-                           (int32_t)qblocks, (int32_t)keysets);
+        hipLaunchKernelGGL((prefill_scores_kernel<Tag>), dim3((unsigned)(qblocks * keysets)),
+                           dim3(64 * kPrefillQueries), 0, stream, a, (int32_t)qblocks, (int32_t)keysets);
         return check_launch("prefill_scores_kernel");
       }
     }
