@@ -49,17 +49,20 @@ static_assert(kRoundWaves * kRoundWaveKeys == kRoundKeys, "two 64-key units per 
 
 #ifdef DSA_PHASE_TRACE
 // Per row (trace builds only): wall-clock ticks of the replay's phases and
-// event counts: 0 total, 1 decisions, 2 exact selects, 3 select count,
-// 4 joins, 5 cut moves, 6 move count, 7 compactions.
+// event counts: 0 group loop, 1 decisions, 2 exact selects, 3 select count
+// (low half) and cut move count (high half), 4 joins, 5 cut moves, 6 listed
+// keys (low 48 bits) and rounds that sorted in the workspace (high 16), 7 setup
+// (kernel start to the group loop).  Accumulated in registers by wave 0 and added to memory once per
+// launch, so that the timing itself adds no memory round trip to the loop.
 __device__ uint64_t g_trace_resolve[kTraceWgs * kTraceMarks];
 #define RESOLVE_T0(v) uint64_t v = wall_clock64()
 #define RESOLVE_ADD(i, t0) \
   do {                     \
-    if (lane == 0 && row < kTraceWgs) g_trace_resolve[(size_t)row * kTraceMarks + (i)] += wall_clock64() - (t0); \
+    trace_acc[i] += wall_clock64() - (t0); \
   } while (0)
-#define RESOLVE_COUNT(i) \
-  do {                   \
-    if (lane == 0 && row < kTraceWgs) g_trace_resolve[(size_t)row * kTraceMarks + (i)] += 1; \
+#define RESOLVE_COUNT(i, n) \
+  do {                      \
+    trace_acc[i] += (n);    \
   } while (0)
 #else
 #define RESOLVE_T0(v) \
@@ -68,8 +71,8 @@ __device__ uint64_t g_trace_resolve[kTraceWgs * kTraceMarks];
 #define RESOLVE_ADD(i, t0) \
   do {                     \
   } while (0)
-#define RESOLVE_COUNT(i) \
-  do {                   \
+#define RESOLVE_COUNT(i, n) \
+  do {                      \
   } while (0)
 #endif
 
@@ -99,6 +102,27 @@ __device__ __forceinline__ bool prunes(uint32_t bound_key, uint32_t t) { return 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
+}
+
+// Calls use(i, load(i)) for i = first, first + stride, ... below n, the loads
+// of each batch of kBatch indices issued before any of them is used (a load
+// past n re-reads the batch's first index), so that a thread's loads cost one
+// memory latency per batch instead of one per index.
+template <int kBatch, class Load, class Use>
+__device__ __forceinline__ void batched(uint32_t first, uint32_t n, uint32_t stride, Load load, Use use) {
+  for (uint32_t i0 = first; i0 < n; i0 += kBatch * stride) {
+    decltype(load(i0)) v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const uint32_t i = i0 + (uint32_t)j * stride;
+      v[j] = load(i < n ? i : i0);
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const uint32_t i = i0 + (uint32_t)j * stride;
+      if (i < n) use(i, v[j]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -257,7 +281,7 @@ struct ResolveShared {
   uint32_t item[kSortCap];  // listed keys by group: slot | block << 18
   uint8_t join[kSortCap];   // joined (evaluated) flag of each slot
   uint32_t end[kBins];      // past-the-end slot of each bin (after the scatter)
-  uint32_t E[kBins];        // joined keys per bin
+  alignas(16) uint32_t E[kBins];  // joined keys per bin (read four at a time)
   uint32_t gend[kMaxTemporalBlocks];  // past-the-end item of each group (after the scatter)
   uint32_t uk[kMaxTemporalBlocks];    // bound key at each of the round's positions
   uint16_t blk[kMaxTemporalBlocks];   // block at each
@@ -325,7 +349,7 @@ __device__ __forceinline__ uint32_t cut_select(P32 val, P8 join, uint32_t s0, ui
 
 template <bool kSpill>
 __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPlan& rp, ResolveShared& sh,
-                                            uint32_t n_listed) {
+                                            uint32_t n_listed, uint64_t t_start) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -344,7 +368,16 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
   uint32_t* val = kSpill ? a.ws.spill_val + spill_at : sh.val;
   uint32_t* item = kSpill ? a.ws.spill_item + spill_at : sh.item;
   uint8_t* join = kSpill ? a.ws.spill_join + spill_at : sh.join;
+  const uint32_t* run = a.ws.run + (size_t)row * k;
   const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
+  auto each_run = [&](auto f) {
+    batched<4>((uint32_t)tid, (uint32_t)k, kResolveThreads, [&](uint32_t i) { return run[i]; },
+               [&](uint32_t, uint32_t v) { f(v); });
+  };
+  auto each_listed = [&](auto f) {
+    batched<4>((uint32_t)tid, n_listed, kResolveThreads, [&](uint32_t e) { return list[e]; },
+               [&](uint32_t, uint64_t x) { f(x); });
+  };
 
   // Bin and group counts (E counts the joined keys: run's).
   for (int i = tid; i < kBins; i += kResolveThreads) {
@@ -355,20 +388,19 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
   if (tid == 0) sh.above = 0;
   __syncthreads();
   uint32_t above = 0;
-  for (int i = tid; i < k; i += kResolveThreads) {
-    const uint32_t b = (a.ws.run[(size_t)row * k + i] - floor_key) >> shift;
+  each_run([&](uint32_t v) {
+    const uint32_t b = (v - floor_key) >> shift;
     __hip_atomic_fetch_add(&sh.end[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     __hip_atomic_fetch_add(&sh.E[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     above += b > 0 ? 1u : 0u;
-  }
+  });
   for (int off = 32; off > 0; off >>= 1) above += (uint32_t)__shfl_xor((int)above, off, kWave);
   if (lane == 0 && above) __hip_atomic_fetch_add(&sh.above, above, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
-    const uint64_t x = list[e];
+  each_listed([&](uint64_t x) {
     const uint32_t b = ((uint32_t)x - floor_key) >> shift;
     __hip_atomic_fetch_add(&sh.end[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     __hip_atomic_fetch_add(&sh.gend[(int)(x >> 49) - g_begin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
+  });
   __syncthreads();
   // Exclusive scans: end[b] <- first slot of bin b, gend[g] <- first item of
   // group g (the scatter's cursors; past it they hold each one's end).
@@ -408,15 +440,13 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
   }
   __syncthreads();
   // Scatter: run's keys joined, listed keys not yet; listed keys' items by group.
-  for (int i = tid; i < k; i += kResolveThreads) {
-    const uint32_t v = a.ws.run[(size_t)row * k + i];
+  each_run([&](uint32_t v) {
     const uint32_t slot = __hip_atomic_fetch_add(&sh.end[(v - floor_key) >> shift], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
     val[slot] = v;
     join[slot] = 1;
-  }
-  for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
-    const uint64_t x = list[e];
+  });
+  each_listed([&](uint64_t x) {
     const uint32_t v = (uint32_t)x;
     const uint32_t slot = __hip_atomic_fetch_add(&sh.end[(v - floor_key) >> shift], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -426,10 +456,15 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     const uint32_t at = __hip_atomic_fetch_add(&sh.gend[(int)(x >> 49) - g_begin], 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_WORKGROUP);
     item[at] = slot | (blk << 18);
-  }
+  });
   __syncthreads();
 
   if (wave == 0) {
+#ifdef DSA_PHASE_TRACE
+    uint64_t trace_acc[kTraceMarks] = {};
+    trace_acc[7] = wall_clock64() - t_start;
+    trace_acc[6] = n_listed + ((uint64_t)(kSpill ? 1 : 0) << 48);
+#endif
     uint32_t bin = 0;  // the cut bin: the floor (the k-th largest) is in bin 0
     uint32_t cut_above = sh.above;
     uint32_t tau = floor_key;
@@ -445,11 +480,42 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
                          shift, sh.digits);
         tau_ok = true;
         RESOLVE_ADD(2, t_sel);
-        RESOLVE_COUNT(3);
+        RESOLVE_COUNT(3, 1ull);
       }
       return tau;
     };
+    // Read ahead of each group: its first 64 decision inputs, and the items
+    // of its first 128 listed keys (items are stored by group, so the next
+    // group's start slot is this group's end), whose values are then read
+    // while the group's decisions are made.  Reads past a group's end are
+    // harmless (items of later groups, or the last item again) and unused.
+    uint32_t pf_uk = 0u;
+    int pf_blk = 0;
+    auto prefetch = [&](int gi) {
+      const int q = gi * W + lane;
+      const bool ok = gi < n_groups && q < min(gi * W + W, n_pos);
+      pf_uk = ok ? sh.uk[q] : 0u;
+      pf_blk = ok ? (int)sh.blk[q] : 0;
+    };
+    // (With no listed keys the read of item 0 is stale, so its slot and block
+    // are replaced by 0: slot 0 holds a run key, block 0 exists.)
+    const uint32_t item_last = n_listed ? n_listed - 1u : 0u;
+    uint32_t pf_it[2];
+    auto prefetch_items = [&](uint32_t start) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t it = item[min(start + (uint32_t)(h * kWave + lane), item_last)];
+        pf_it[h] = n_listed ? it : 0u;
+      }
+    };
+    prefetch(0);
+    prefetch_items(0u);
+    uint32_t i0 = 0u;  // the group's first item
     for (int gi = 0; gi < n_groups; ++gi) {
+      const uint32_t i1 = sh.gend[gi];
+      uint32_t pf_v[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) pf_v[h] = val[pf_it[h] & 0x3ffffu];
       const int q0 = gi * W;
       const int q1 = min(q0 + W, n_pos);
       const bool seed_group = rp.first_round && gi == 0;
@@ -462,8 +528,12 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       for (int c0 = q0; c0 < q1; c0 += kWave) {
         const int q = c0 + lane;
         const bool active = q < q1;
-        const uint32_t uk = active ? sh.uk[q] : 0u;
-        const int blk = active ? (int)sh.blk[q] : 0;
+        uint32_t uk = pf_uk;
+        int blk = pf_blk;
+        if (c0 != q0) {
+          uk = active ? sh.uk[q] : 0u;
+          blk = active ? (int)sh.blk[q] : 0;
+        }
         int verdict = 2;  // 0 pruned, 1 kept, 2 needs the exact threshold
         if (seed_group) {
           verdict = prunes(uk, seed_tau) ? 0 : 1;
@@ -484,53 +554,97 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
         nreset += (uint32_t)__builtin_popcountll(m);
       }
       wave_sync();
+      prefetch(gi + 1);
       RESOLVE_ADD(1, t_dec);
-      // The kept blocks' listed keys join.
+      // The kept blocks' listed keys join, 128 at a time: the first 128 from
+      // the values read ahead, the rest (long groups) read here, items and
+      // values of both halves issued before any is used.
       RESOLVE_T0(t_join);
-      const uint32_t i0 = gi ? sh.gend[gi - 1] : 0u;
-      const uint32_t i1 = sh.gend[gi];
-      for (uint32_t c0 = i0; c0 < i1; c0 += kWave) {
-        const uint32_t i = c0 + (uint32_t)lane;
-        const uint32_t it = i < i1 ? item[i] : 0u;
-        const bool in = i < i1 && sh.kept[it >> 18];
-        uint32_t b = 0;
-        if (in) {
-          const uint32_t slot = it & 0x3ffffu;
-          join[slot] = 1;
-          b = (val[slot] - floor_key) >> shift;
-          __hip_atomic_fetch_add(&sh.E[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      auto join_keys = [&](uint32_t c0, const uint32_t (&it)[2], const uint32_t (&v)[2]) {
+        uint32_t b[2];
+        bool in[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          b[h] = (v[h] - floor_key) >> shift;
+          in[h] = c0 + (uint32_t)(h * kWave + lane) < i1 && sh.kept[it[h] >> 18];
         }
-        cut_above += (uint32_t)__builtin_popcountll(__ballot(in && b > bin));
-        if (__ballot(in && b >= bin)) tau_ok = false;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (in[h]) {
+            join[it[h] & 0x3ffffu] = 1;
+            __hip_atomic_fetch_add(&sh.E[b[h]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+        cut_above += (uint32_t)__builtin_popcountll(__ballot(in[0] && b[0] > bin)) +
+                     (uint32_t)__builtin_popcountll(__ballot(in[1] && b[1] > bin));
+        if (__ballot((in[0] && b[0] >= bin) || (in[1] && b[1] >= bin))) tau_ok = false;
+      };
+      if (i0 < i1) join_keys(i0, pf_it, pf_v);
+      for (uint32_t c0 = i0 + 2 * kWave; c0 < i1; c0 += 2 * kWave) {
+        uint32_t it[2], v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) it[h] = item[min(c0 + (uint32_t)(h * kWave + lane), item_last)];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) v[h] = val[it[h] & 0x3ffffu];
+        join_keys(c0, it, v);
       }
+      prefetch_items(i1);
+      i0 = i1;
       wave_sync();
       RESOLVE_ADD(4, t_join);
       if (cut_above >= (uint32_t)k) {
         // The cut moves up to the highest bin b with at least k joined keys at
-        // or above it.  (c counts the keys of the bins at or above s, so the
-        // bin is found below kBins; the bound only guards the loop.)
+        // or above it.  Each step covers 256 bins, four per lane read at once
+        // (bins at or below the old cut count as empty); c counts the keys of
+        // the bins at or above the step's first, so the bin is found below
+        // kBins and the bound only guards the loop.
         RESOLVE_T0(t_move);
-        RESOLVE_COUNT(6);
-        uint32_t s = bin + 1;
+        RESOLVE_COUNT(3, 1ull << 32);
+        const uint32_t s_first = bin + 1;
+        uint32_t s = s_first & ~3u;
         uint32_t c = cut_above;
-        for (int guard = 0; guard < kBins / kWave; ++guard) {
-          const uint32_t eb = s + (uint32_t)lane < (uint32_t)kBins ? sh.E[s + lane] : 0u;
-          const uint32_t incl = wave_incl_scan(eb);
+        for (int guard = 0; guard < kBins / (4 * kWave); ++guard) {
+          const uint32_t base = s + 4u * (uint32_t)lane;
+          uint4 e4 = base < (uint32_t)kBins ? *reinterpret_cast<const uint4*>(&sh.E[base]) : make_uint4(0u, 0u, 0u, 0u);
+          if (base < s_first) e4.x = 0u;
+          if (base + 1u < s_first) e4.y = 0u;
+          if (base + 2u < s_first) e4.z = 0u;
+          const uint32_t sum4 = e4.x + e4.y + e4.z + e4.w;
+          const uint32_t incl = wave_incl_scan(sum4);
           const uint64_t m = __ballot(c - incl < (uint32_t)k);
           if (m) {
+            // In the lane that crosses: the first of its bins after which
+            // fewer than k keys remain above.
+            uint32_t rem = c - (incl - sum4) - e4.x;
+            uint32_t off = 0u;
+            if (rem >= (uint32_t)k) {
+              rem -= e4.y;
+              off = 1u;
+              if (rem >= (uint32_t)k) {
+                rem -= e4.z;
+                off = 2u;
+                if (rem >= (uint32_t)k) {
+                  rem -= e4.w;
+                  off = 3u;
+                }
+              }
+            }
             const uint32_t l = (uint32_t)__builtin_ctzll(m);
-            bin = s + l;
-            cut_above = c - (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)l);
+            bin = s + 4u * l + (uint32_t)__builtin_amdgcn_readlane((int)off, (int)l);
+            cut_above = (uint32_t)__builtin_amdgcn_readlane((int)rem, (int)l);
             break;
           }
           c -= (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
-          s += kWave;
+          s += 4u * kWave;
         }
         tau_ok = false;
         RESOLVE_ADD(5, t_move);
       }
     }
     RESOLVE_ADD(0, t_all);
+#ifdef DSA_PHASE_TRACE
+    if (lane == 0 && row < kTraceWgs)
+      for (int i = 0; i < kTraceMarks; ++i) g_trace_resolve[(size_t)row * kTraceMarks + i] += trace_acc[i];
+#endif
     if (lane == 0) {
       sh.nreset = nreset;
       sh.cut_bin = bin;
@@ -578,31 +692,41 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
 
 __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(TemporalArgs a, RoundPlan rp) {
   __shared__ ResolveShared sh;
+#ifdef DSA_PHASE_TRACE
+  const uint64_t t_start = wall_clock64();
+#else
+  const uint64_t t_start = 0;
+#endif
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int row = blockIdx.x;
   const int nb = a.blocks;
   const int k = a.k;
   const int n_pos = rp.pos_end - rp.pos_begin;
-  for (int i = tid; i < n_pos; i += kResolveThreads) {
-    sh.blk[i] = (uint16_t)a.ws.order[(size_t)row * nb + rp.pos_begin + i];
-    sh.uk[i] = upper_key(a.ws.upper_pos[(size_t)row * nb + rp.pos_begin + i]);
-  }
+  const auto* order = a.ws.order + (size_t)row * nb + rp.pos_begin;
+  const double* upper = a.ws.upper_pos + (size_t)row * nb + rp.pos_begin;
+  batched<4>((uint32_t)tid, (uint32_t)n_pos, kResolveThreads, [&](uint32_t i) { return order[i]; },
+             [&](uint32_t i, auto b) { sh.blk[i] = (uint16_t)b; });
+  batched<4>((uint32_t)tid, (uint32_t)n_pos, kResolveThreads, [&](uint32_t i) { return upper[i]; },
+             [&](uint32_t i, double u) { sh.uk[i] = upper_key(u); });
   if (tid == 0) sh.max_key = 0;
   __syncthreads();
   // Keys to sort and their largest (the span of the bins).
-  uint32_t mx = 0;
-  for (int i = tid; i < k; i += kResolveThreads) mx = max(mx, a.ws.run[(size_t)row * k + i]);
+  const uint32_t* run = a.ws.run + (size_t)row * k;
   const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
   const uint32_t n_listed = a.ws.list_total[(size_t)row * kMaxRounds + rp.round];
-  for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) mx = max(mx, (uint32_t)list[e]);
+  uint32_t mx = 0;
+  batched<4>((uint32_t)tid, (uint32_t)k, kResolveThreads, [&](uint32_t i) { return run[i]; },
+             [&](uint32_t, uint32_t v) { mx = max(mx, v); });
+  batched<4>((uint32_t)tid, n_listed, kResolveThreads, [&](uint32_t e) { return list[e]; },
+             [&](uint32_t, uint64_t x) { mx = max(mx, (uint32_t)x); });
   for (int off = 32; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, kWave));
   if (lane == 0) __hip_atomic_fetch_max(&sh.max_key, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   __syncthreads();
   if ((uint32_t)k + n_listed <= (uint32_t)kSortCap)
-    resolve_row<false>(a, rp, sh, n_listed);
+    resolve_row<false>(a, rp, sh, n_listed, t_start);
   else
-    resolve_row<true>(a, rp, sh, n_listed);
+    resolve_row<true>(a, rp, sh, n_listed, t_start);
 }
 
 // Round splits, as fractions of the scan's groups: DSA_AMD_TEMPORAL_ROUNDS, a
