@@ -280,14 +280,17 @@ constexpr int kPrefillRow = 272;
 
 // The unit loop is software-pipelined across tiles and units: step t issues
 // the MFMAs of tile t and the ReLU / weight work of tile t - 1 (tile 3 of the
-// previous unit at step 0), interleaved one MFMA to two VALU instructions by
-// scheduling groups, while the next tile's LDS reads are in flight.  The
+// previous unit at step 0), interleaved by scheduling groups, while the next
+// tile's LDS reads are in flight.  The
 // previous unit's reduction and store follow step 0.
 __device__ __forceinline__ void mfma_valu_interleave() {
+  // One MFMA to up to three VALU instructions (a tile's 32 ReLU / FMA
+  // instructions, plus the unit reduction's after step 0); one to two and two
+  // to four measured 1-2 % slower.
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
   }
 }
 
