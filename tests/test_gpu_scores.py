@@ -100,17 +100,22 @@ def test_batched_decode_each_sequence(device) -> None:
         assert_scores_close(out[b, 0], q[b], w[b], k[b])
 
 
-def test_score_encoded_multi_query_causal(device) -> None:
-    print("score_encoded multi-query causal", flush=True)
-    gen = torch.Generator().manual_seed(5)
-    q = (torch.randn(2, 37, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
-    w = torch.randn(2, 37, 64, generator=gen) / 8
-    k = torch.randn(2, 150, 128, generator=gen).to(torch.bfloat16)
+@pytest.mark.parametrize("batch,queries,length", [(2, 37, 150), (3, 16, 327), (1, 9, 40), (2, 24, 1000)])
+def test_score_encoded_multi_query_causal(device, batch, queries, length) -> None:
+    # The multi-query kernel (eight queries per workgroup, 64-key units
+    # pipelined across tiles and units): query counts that are and are not a
+    # multiple of eight, lengths below one unit and between units, every
+    # query of every key set checked, causal and not.
+    print(f"score_encoded multi-query causal B={batch} T={queries} L={length}", flush=True)
+    gen = torch.Generator().manual_seed(5 + length)
+    q = (torch.randn(batch, queries, 64, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16)
+    w = torch.randn(batch, queries, 64, generator=gen) / 8
+    k = torch.randn(batch, length, 128, generator=gen).to(torch.bfloat16)
     dense = sidecar.score_encoded(q.to(device), w.to(device), k.to(device)).cpu()
     causal = sidecar.score_encoded(q.to(device), w.to(device), k.to(device), causal=True).cpu()
-    offset = 150 - 37
-    for b in range(2):
-        for t in (0, 1, 20, 36):
+    offset = length - queries
+    for b in range(batch):
+        for t in range(queries):
             assert_scores_close(dense[b, t], q[b, t], w[b, t], k[b])
             valid = t + offset + 1
             assert torch.equal(causal[b, t, :valid], dense[b, t, :valid])
