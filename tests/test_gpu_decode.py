@@ -162,28 +162,51 @@ def test_graph_replays_match_eager(device, batch) -> None:
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("batch,length,k", [(16, 32768, 2048), (3, 4096, 256), (1, 524288, 2048)])
-def test_two_halves_match_fused_step(device, batch, length, k) -> None:
+@pytest.mark.parametrize(
+    "batch,length,k,ties",
+    [
+        (16, 32768, 2048, False),
+        (16, 32768, 2048, "all"),
+        (16, 32768, 2048, "region"),
+        (4, 131072, 2048, False),
+        (3, 4096, 256, False),
+        (2, 700, 2048, False),
+        (2, 6001, 500, True),
+        (64, 32768, 2048, False),
+        (1, 524288, 2048, False),
+    ],
+)
+def test_two_halves_match_fused_step(device, batch, length, k, ties) -> None:
     # dsa_score_hist + dsa_select_topk (the halves a caller may time apart)
-    # equal dsa_score_topk on the same workspace, for a shape on the
-    # candidate-list plan and one on the histogram plan.
+    # equal dsa_score_topk on the same workspace, indices and values, three
+    # calls in a row: the C2 shape with every score equal (heavy ties) and
+    # with one row's top-K crowded into two chunks (lists miss, raw scores
+    # replace them), the C5 row count and length, k > length, a wider batch
+    # (8192-key chunks), and one long row on the histogram plan.
     from dsa_amd import _lib
 
-    q, w, keys = inputs(batch, length, seed=5 + length, hot=0.01)
+    print(f"halves vs step B={batch} L={length} k={k} ties={ties}", flush=True)
+    q, w, keys = inputs(batch, length, seed=5 + length, hot=0.0 if ties else 0.01, ties=ties)
     q, w, keys = q.to(device), w.to(device).float(), keys.to(device)
     ws = torch.zeros(int(_lib.query("dsa_score_topk_workspace_bytes", batch, length)), device=device, dtype=torch.uint8)
     stream = torch.cuda.current_stream().cuda_stream
     scores = torch.empty(batch, length, device=device)
-    fused = torch.empty(batch, k, device=device, dtype=torch.int64)
     halves = torch.full((batch, k), -7, device=device, dtype=torch.int64)
-    _lib.call("dsa_score_topk", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(), batch, length, k,
-              _lib.DTYPE_BF16, fused.data_ptr(), None, ws.data_ptr(), ws.numel(), stream)
+    halves_v = torch.empty(batch, k, device=device)
     _lib.call("dsa_score_hist", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(), batch, length, k,
               _lib.DTYPE_BF16, ws.data_ptr(), ws.numel(), stream)
-    _lib.call("dsa_select_topk", scores.data_ptr(), batch, length, k, halves.data_ptr(), None, ws.data_ptr(), ws.numel(),
-              stream)
-    torch.cuda.synchronize()
-    assert torch.equal(fused, halves)
+    _lib.call("dsa_select_topk", scores.data_ptr(), batch, length, k, halves.data_ptr(), halves_v.data_ptr(),
+              ws.data_ptr(), ws.numel(), stream)
+    for call in range(3):
+        fused = torch.full((batch, k), -7, device=device, dtype=torch.int64)
+        fused_v = torch.empty(batch, k, device=device)
+        _lib.call("dsa_score_topk", q.data_ptr(), w.data_ptr(), keys.data_ptr(), None, scores.data_ptr(), batch,
+                  length, k, _lib.DTYPE_BF16, fused.data_ptr(), fused_v.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, halves), call
+        assert torch.equal(fused_v.view(torch.int32), halves_v.view(torch.int32)), call
+    # The workspace's per-row histograms are left at zero.
+    assert not ws[: batch * 4096 * 4].any()
     host = scores.cpu().numpy()
     for b in (0, batch - 1):
         assert halves[b].cpu().tolist() == T.topk_index_order(host[b], k).tolist()
