@@ -529,10 +529,21 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
   // (With at most k entries, every entry of the earlier sources is chosen.)
   uint32_t before = (bin == kNoBin && tid == 0) ? sh.base[c] : 0u;
   uint64_t cstar = uint64_t(1) << 32;  // every listed key when they number at most k
-  if (bin != kNoBin) {
-    // Count, scan, then place the entries of the cut's bin: from the
-    // registers that fetched them where they still hold them, else from the
-    // stage (or memory).
+  if (bin != kNoBin && staged) {
+    // Staged entries: the radix cut runs over the whole stage, counting only
+    // the cut bin's entries (its prefix), with no compaction of the bin
+    // first (a count, a scan and a placement, 0.6 us at C2); then the chosen
+    // entries of the earlier lists are counted off the stage.
+    uint32_t (*digits)[kDigitBins] = reinterpret_cast<uint32_t (*)[kDigitBins]>(sh.hist);
+    for (uint32_t i = tid; i < (uint32_t)kDigitBins; i += kSelThreads) digits[0][i] = 0;
+    __syncthreads();
+    cstar = radix_cut(bin, sh.want, entries, [&](uint32_t i) { return sh.stage[i]; }, digits, sh.radix);
+    before = 0;
+    for (uint32_t i = tid; i < sh.base[c]; i += kSelThreads) before += sh.stage[i] >= cstar ? 1u : 0u;
+  } else if (bin != kNoBin) {
+    // Entries read in place (raw rounds past the stage): count, scan, then
+    // place the entries of the cut's bin, from the registers that fetched
+    // them where they still hold them, else from memory.
     const bool in_regs = !raw;
     const uint32_t spec_end = in_regs ? min(src_len, tpl * kListSpec) : 0u;
     uint32_t n_cand = 0;
