@@ -67,6 +67,10 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   __shared__ uint32_t s_nseeds;
   __shared__ uint32_t tile_bits[kListChunkMax / 512];  // 16-key tiles of the chunk's kept blocks
   __shared__ uint32_t s_least, s_tau, s_count, s_list_bin;
+  // Scaled keys: the chunk's 128-key block scales, read once here, so that
+  // no scale load sits behind a unit's MFMAs (waiting for one there made the
+  // compiler drain every unit in flight).
+  __shared__ float s_scales[KF::kScaled ? kListChunkMax / 128 + 1 : 1];
   __shared__ __align__(16) uint32_t s_wsum[kFusedWaves];
   extern __shared__ float chunk_scores[];
   const int tid = threadIdx.x;
@@ -88,6 +92,12 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   for (int i = tid; i < kSelectBins; i += kFusedThreads) hist[i] = 0;
   for (int i = tid; i < kListChunkMax / 32; i += kFusedThreads) seed_bits[i] = 0;
   if (tid < kListChunkMax / 512) tile_bits[tid] = 0;
+  if constexpr (KF::kScaled) {
+    const int s_first = base >> 7;
+    const int n_scales = n_chunk > 0 ? ((base + n_chunk - 1) >> 7) - s_first + 1 : 0;
+    if (tid < n_scales)
+      s_scales[tid] = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + s_first + tid];
+  }
   if (tid == 0) {
     s_least = 0xffffffffu;
     s_count = 0;
@@ -141,7 +151,6 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
 
   const uint8_t* row_keys = a.keys + (size_t)row * a.key_stride * KF::kRowBytes;
   const int valid_bytes = L * KF::kRowBytes;  // below 2^31 (L <= 131072)
-  const float* row_scales = KF::kScaled ? a.scales + (size_t)row * ((a.key_stride + 127) / 128) : nullptr;
   uint32_t loff[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) loff[t] = KF::lane_offset(t, r, g);
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
 #pragma unroll
     for (int t = 0; t < 4; ++t) s[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[t]);
     float v = unit_reduce(s, g);
-    if constexpr (KF::kScaled) v *= row_scales[(base + 64 * ul + lane) >> 7];
+    if constexpr (KF::kScaled) v *= s_scales[((base + 64 * ul) >> 7) - (base >> 7)];
     return v;
   };
 
@@ -194,7 +203,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
         float v = unit_reduce(sc, g);
         if (e < n_seeds) {
           const int local = seed_list[e];
-          if constexpr (KF::kScaled) v *= row_scales[(base + local) >> 7];
+          if constexpr (KF::kScaled) v *= s_scales[((base + local) >> 7) - (base >> 7)];
           chunk_scores[local] = v;
           least = min(least, float_to_ordered(v));
         }
