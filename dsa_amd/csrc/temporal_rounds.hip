@@ -132,7 +132,7 @@ __device__ __forceinline__ void batched(uint32_t first, uint32_t n, uint32_t str
 // which the four waves score four at a time (one MFMA unit, two units per
 // wave) with the dense kernel's tile code.  Every scored key's score goes to
 // the scores row; a non-seed key above the floor is listed, with its group,
-// in the wave's own region of the row's list (no atomics).
+// in the row's list of the round (one atomic reservation per wave).
 // ---------------------------------------------------------------------------
 template <class Tag, class KF>
 __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalArgs a, RoundPlan rp) {

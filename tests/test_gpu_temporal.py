@@ -381,6 +381,48 @@ def test_dynamic_step_paths_agree(device, monkeypatch, block, order, wave, gamma
         assert not kept.all(), "the margin pruned nothing: the case does not exercise the replay"
 
 
+@pytest.mark.parametrize("gamma_sigma", [-2.0, 0.5])
+def test_dynamic_step_topk_with_invalid_and_repeated_seeds(device, monkeypatch, gamma_sigma) -> None:
+    # The rounds path takes the step's top-k from its last replay, whose k-th
+    # largest evaluated score is checked against the scores row; seeds that
+    # are out of range or repeated make the run's k-th largest differ from the
+    # row's, so the row's own k-th largest is found instead.  Every output must equal the
+    # sequential scan's (histogram select), and the top-k must be the stable
+    # top-k of the returned scores row, -inf keys included.
+    print(f"dynamic top-k with invalid/repeated seeds gs={gamma_sigma}", flush=True)
+    batch, prev_length, length, k, block, wave = 2, 4096, 4100, 256, 16, 8
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=4242)
+    q_prev, q_cur, w, keys = q_prev.to(device), q_cur.to(device), w.to(device), keys.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys[:, :prev_length].contiguous(), k, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    seeds = prev_topk.clone()
+    seeds[0, :40] = -1                   # no key
+    seeds[0, 40:80] = seeds[0, 80:120]   # the same keys twice
+    seeds[1, 10:] = length + 5           # past the row: ten valid seeds
+    gamma = torch.full((batch,), gamma_sigma * float(prev_scores.std()), device=device)
+
+    def run():
+        s = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, seeds, gamma, block_size=block,
+                                   method="dynamic", scan_order="address", wave=wave)
+        return [x.cpu().numpy() for x in (s.scores, s.evaluated_blocks, s.qk_scored, s.topk)]
+
+    results = {}
+    for splits in ("1", "0.25"):
+        monkeypatch.setenv("DSA_AMD_TEMPORAL_ROUNDS", splits)
+        results[splits] = run()
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_ROUNDS")
+    monkeypatch.setenv("DSA_AMD_TEMPORAL_PATH", "launch")
+    sequential = run()
+    monkeypatch.delenv("DSA_AMD_TEMPORAL_PATH")
+    for splits, got in results.items():
+        for name, a, b in zip(("scores", "kept", "qk", "topk"), got, sequential):
+            np.testing.assert_array_equal(a, b, err_msg=f"rounds {splits} vs the sequential scan: {name}")
+    scores, _, qk, topk = sequential
+    for b in range(batch):
+        assert topk[b].tolist() == T.topk_index_order(scores[b], k).tolist(), b
+        assert int(qk[b]) == int(np.isfinite(scores[b]).sum()), b
+
+
 def test_dynamic_step_keys_loaded_accounting(device, monkeypatch) -> None:
     # Key rows a dynamic step loads on the rounds path: the seeds, then per
     # round every non-seed key of the blocks whose bound clears the round's
