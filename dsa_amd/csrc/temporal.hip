@@ -32,7 +32,7 @@
 namespace dsa {
 namespace {
 
-// Scan orders ranked by temporal_rank_kernel (every sorted order but the
+// Scan orders ranked by rank_blocks (every sorted order but the
 // policy's buckets, which the prep kernel sorts itself).
 __host__ __device__ inline bool ranked_order(const TemporalArgs& a) {
   const bool policy = a.policy_mode != 0;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
       a.ws.sort_lo[(size_t)row * nb + b] = l[j];
     }
   }
-  if (ranked_order(a)) return;  // temporal_rank_kernel orders the blocks
+  if (ranked_order(a)) return;  // rank_blocks orders the blocks
   if (!sorted) {
     for (int b = tid; b < nb; b += 1024) {
       a.ws.order[(size_t)row * nb + b] = b;
@@ -210,15 +210,15 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
 constexpr int kRankTargets = 16;
 constexpr int kRankParts = 16;
 
-__global__ __launch_bounds__(kRankTargets * kRankParts) void temporal_rank_kernel(TemporalArgs a) {
+__device__ __forceinline__ void rank_blocks(const TemporalArgs& a, int block) {
   __shared__ uint64_t s_hi[kMaxTemporalBlocks];
   __shared__ uint32_t s_lo[kMaxTemporalBlocks];
   __shared__ uint32_t s_part[kRankParts][kRankTargets];
   const int tid = threadIdx.x;
   const int nb = a.blocks;
   const int per_row = (nb + kRankTargets - 1) / kRankTargets;
-  const int row = blockIdx.x / per_row;
-  const int target = (blockIdx.x % per_row) * kRankTargets + tid % kRankTargets;
+  const int row = block / per_row;
+  const int target = (block % per_row) * kRankTargets + tid % kRankTargets;
   const int part = tid / kRankTargets;
   for (int i = tid; i < nb; i += kRankTargets * kRankParts) {
     s_hi[i] = a.ws.sort_hi[(size_t)row * nb + i];
@@ -243,16 +243,16 @@ __global__ __launch_bounds__(kRankTargets * kRankParts) void temporal_rank_kerne
   }
 }
 
-// The seeds: 64 per wave, gathered by index.
+// The seeds: 64 per wave, gathered by index (block: the seed workgroup).
 template <class Tag, class KF>
-__global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
+__device__ __forceinline__ void score_seeds(const TemporalArgs& a, int block) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15;
   const int g = lane >> 4;
   const int per_row = (a.k + 255) / 256;
-  const int row = blockIdx.x / per_row;
-  const int base = (blockIdx.x % per_row) * 256 + wave * 64;
+  const int row = block / per_row;
+  const int base = (block % per_row) * 256 + wave * 64;
   if (base >= a.k) return;
   const int64_t* seeds = a.seeds + (size_t)row * a.k;
   int tile_key[4];
@@ -302,6 +302,24 @@ __global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
     __hip_atomic_fetch_min(a.ws.tau + row, least, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (lane == 0 && lowest != 0xffffffffu)
     __hip_atomic_fetch_min(a.ws.floor + row, lowest, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class Tag, class KF>
+__global__ __launch_bounds__(256) void temporal_seed_kernel(TemporalArgs a) {
+  score_seeds<Tag, KF>(a, blockIdx.x);
+}
+
+// The seeds and the ranked scan order in one launch: they are independent
+// (the ranks read the prep's sort keys; the seeds score the previous top-k
+// into the cleared scores row), so the seeds' gathers run beside the ranking
+// instead of after it.  Workgroups [0, seed_wgs) score seeds, the rest rank.
+static_assert(kRankTargets * kRankParts == 256, "rank and seed workgroups share one shape");
+template <class Tag, class KF>
+__global__ __launch_bounds__(256) void temporal_seed_rank_kernel(TemporalArgs a, int32_t seed_wgs) {
+  if ((int)blockIdx.x < seed_wgs)
+    score_seeds<Tag, KF>(a, blockIdx.x);
+  else
+    rank_blocks(a, (int)blockIdx.x - seed_wgs);
 }
 
 // One block per wave: scan positions [wave_start, wave_start + wave_len) of
@@ -751,14 +769,16 @@ template <class Tag, class KF>
 int launch_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(temporal_prep_kernel, dim3(a.rows), dim3(1024), 0, stream, a);
   if (int st = check_launch("temporal_prep_kernel")) return st;
+  const int seed_wgs = a.rows * ((a.k + 255) / 256);
   if (ranked_order(a)) {
     const int per_row = (a.blocks + kRankTargets - 1) / kRankTargets;
-    hipLaunchKernelGGL(temporal_rank_kernel, dim3((unsigned)(a.rows * per_row)), dim3(kRankTargets * kRankParts), 0,
-                       stream, a);
-    if (int st = check_launch("temporal_rank_kernel")) return st;
+    hipLaunchKernelGGL((temporal_seed_rank_kernel<Tag, KF>), dim3((unsigned)(seed_wgs + a.rows * per_row)), dim3(256),
+                       0, stream, a, seed_wgs);
+    if (int st = check_launch("temporal_seed_rank_kernel")) return st;
+  } else {
+    hipLaunchKernelGGL((temporal_seed_kernel<Tag, KF>), dim3(seed_wgs), dim3(256), 0, stream, a);
+    if (int st = check_launch("temporal_seed_kernel")) return st;
   }
-  hipLaunchKernelGGL((temporal_seed_kernel<Tag, KF>), dim3(a.rows * ((a.k + 255) / 256)), dim3(256), 0, stream, a);
-  if (int st = check_launch("temporal_seed_kernel")) return st;
   if (wave > 0 && !legacy_paths_forced()) return temporal_rounds(a, wave, key_dtype, stream);
   const int step = wave > 0 ? wave : a.blocks;
   const int waves = (a.blocks + step - 1) / step;
