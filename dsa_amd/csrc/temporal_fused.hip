@@ -107,37 +107,41 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   float wr[4][4];
   load_dense_head_tiles<4, KF::kNaturalK>(a.q + (size_t)row * kHeads * kHeadDim, a.w + (size_t)row * kHeads, r, g,
                                           qa, wr);
-  // The bounds of the chunk's blocks (at most 512: two per thread), loaded
-  // now so that the decisions after the exchange need no memory round trip.
+  // The bounds of the chunk's blocks (at most 512: two per thread) and the
+  // first seeds are loaded now, with the query tiles, unconditionally (clamped
+  // indices), so that their latencies overlap: the bounds are combined only
+  // after the exchange, which needs no memory round trip for them.
   const int first_new = a.prev_length / bs;
   const bool grown = a.prev_length < L;
   const int b_first = base / bs;
   const int b_end = (base + n_chunk + bs - 1) / bs;
-  double upper[2];
+  const int last_prev = a.prev_blocks - 1;  // prev_blocks >= 1
+  float pm_raw[2];
+  double margin_raw[2] = {0.0, 0.0};
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int b = b_first + tid + kFusedThreads * j;
-    upper[j] = HUGE_VAL;
-    if (b < b_end && !(grown && b >= first_new)) {
-      const float pm = b < a.prev_blocks ? a.prev_max[(size_t)row * a.prev_blocks + b] : -__builtin_inff();
-      const double margin = a.margins ? a.margins[(size_t)row * a.prev_blocks + min(b, a.prev_blocks - 1)]
-                                      : (a.gamma_d ? a.gamma_d[row] : (double)a.gamma[row]);
-      upper[j] = (double)pm + margin;
-    }
+    const size_t at = (size_t)row * a.prev_blocks + min(b_first + tid + kFusedThreads * j, last_prev);
+    pm_raw[j] = a.prev_max[at];
+    if (a.margins) margin_raw[j] = a.margins[at];  // uniform
+  }
+  const int64_t* seeds = a.seeds + (size_t)row * a.k;
+  int64_t first_keys[8];  // seeds tid + kFusedThreads * j
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = tid + kFusedThreads * j;
+    first_keys[j] = seeds[min(i, a.k - 1)];
   }
 
+  const double gamma = a.margins ? 0.0 : (a.gamma_d ? a.gamma_d[row] : (double)a.gamma[row]);
+
   __syncthreads();
-  const int64_t* seeds = a.seeds + (size_t)row * a.k;
-  for (int i0 = 0; i0 < a.k; i0 += 8 * kFusedThreads) {  // eight loads in flight per thread
-    int64_t key[8];
+  // The chunk's seeds into its bitmask and position list (seeds i0 + tid +
+  // kFusedThreads * j; entries past k are -1).
+  auto list_seeds = [&](int i0, const int64_t (&key)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int i = i0 + tid + kFusedThreads * j;
-      key[j] = i < a.k ? seeds[i] : -1;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (key[j] >= base && key[j] < base + n_chunk) {
+      const bool in = i0 + tid + kFusedThreads * j < a.k && key[j] >= base && key[j] < base + n_chunk;
+      if (in) {
         const uint32_t bit = 1u << (key[j] & 31);
         const uint32_t was = __hip_atomic_fetch_or(&seed_bits[(key[j] - base) >> 5], bit, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -145,6 +149,14 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
           seed_list[__hip_atomic_fetch_add(&s_nseeds, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] =
               (uint16_t)(key[j] - base);
       }
+    }
+  };
+  list_seeds(0, first_keys);
+  for (int i0 = 8 * kFusedThreads; i0 < a.k; i0 += 8 * kFusedThreads) {  // eight loads in flight per thread
+    int64_t key[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) key[j] = seeds[min(i0 + tid + kFusedThreads * j, a.k - 1)];
+    list_seeds(i0, key);
   }
   __syncthreads();
   DSA_TRACE_MARK(g_trace_static, blockIdx.x, 1);
@@ -252,7 +264,10 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   for (int j = 0; j < 2; ++j) {
     const int b = b_first + tid + kFusedThreads * j;
     if (b >= b_end) continue;
-    const bool keep = !(upper[j] < bound);
+    // U_b: +inf for a block with keys the previous step did not have.
+    const float pm = b < a.prev_blocks ? pm_raw[j] : -__builtin_inff();
+    const double upper = grown && b >= first_new ? HUGE_VAL : (double)pm + (a.margins ? margin_raw[j] : gamma);
+    const bool keep = !(upper < bound);
     a.evaluated[(size_t)row * a.blocks + b] = keep ? 1 : 0;
     const int k0 = b * bs;
     const int k1 = min(L, k0 + bs);
