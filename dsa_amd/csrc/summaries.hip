@@ -117,14 +117,15 @@ __global__ __launch_bounds__(256) void temporal_radius_kernel(const double* q_no
 // sum_h |w_h| ||q_h|| ||k|| of its exact value, so
 //   margin_b = n_b * (C + 2^-15 * sum_h (|w_now|_h ||q_now,h|| + |w_prev|_h ||q_prev,h||))
 // bounds |score_now - score_prev| of every key of the block as computed here.
-// Everything is float64 and the result is scaled by kRadiusRoundUp.  A
-// workgroup takes a run of whole blocks (256 keys, or one block when blocks
-// are longer): each thread the float64 norm of one key row at a time (its 256
-// contiguous bytes), the workgroup's head sums from 16-byte query loads (four
-// threads per head), then one thread per block the maximum over its keys.
+// Everything is float64 and the result is scaled by kRadiusRoundUp (which
+// also covers the summation order).  A workgroup takes a run of whole blocks
+// (256 keys, or one block when blocks are longer): the head sums from 16-byte
+// query loads (four threads per head), the float64 norm of each key row by
+// sixteen lanes, each block's largest norm, then one thread per block the
+// margin.
 constexpr double kScoreRoundingAllowance = 0x1p-15;
 constexpr int kMarginThreads = 256;
-constexpr int kMaxMarginBlock = 4096;  // keys per block (the norms of one workgroup's keys sit in LDS)
+constexpr int kMaxMarginBlock = 4096;  // keys per block the entry point accepts
 
 __device__ __forceinline__ double half_to_double(uint32_t bits16, int dtype) {
   return dtype == kBF16 ? (double)__uint_as_float(bits16 << 16)
@@ -152,7 +153,8 @@ __global__ __launch_bounds__(kMarginThreads) void certified_margins_kernel(const
                                                                            int q_dtype, double* margins) {
   __shared__ double s_radius[kHeads];
   __shared__ double s_slack[kHeads];
-  __shared__ double s_norm[kMaxMarginBlock];
+  __shared__ double s_total[2];
+  __shared__ unsigned long long s_block_max[kMarginThreads];  // blocks_per_wg <= kMarginThreads
   const int row = blockIdx.y;
   const int tid = threadIdx.x;
   {
@@ -191,31 +193,60 @@ __global__ __launch_bounds__(kMarginThreads) void certified_margins_kernel(const
       s_slack[h] = fabs(wn) * sqrt(now_sq) + fabs(wp) * sqrt(prev_sq);
     }
   }
-  // Key norms of the workgroup's blocks (0 past prev_length).
+  // Key norms of the workgroup's blocks (0 past prev_length): sixteen lanes
+  // per key row, one 16-byte vector each, so that one load instruction of a
+  // wave reads four whole rows; each block's largest norm by a 64-bit LDS
+  // maximum (norms are non-negative, so their bits order as their values).
+  if (tid < blocks_per_wg) s_block_max[tid] = 0ull;
+  const int lane = tid & (kWave - 1);
+  const int sub = lane & 15;
   const int first = blockIdx.x * blocks_per_wg * block_size;
   const int count = blocks_per_wg * block_size;
-  for (int i = tid; i < count; i += kMarginThreads) {
-    const int key = first + i;
-    double acc = 0.0;
-    if (key < prev_length) {
-      const uint4* kp = reinterpret_cast<const uint4*>(keys + ((size_t)row * key_stride + key) * kHeadDim);
+  constexpr int kRowsPerStep = kMarginThreads / 16;  // 16 key rows per workgroup step
+  constexpr int kSteps = 8;                           // steps whose loads are in flight together
+  const uint4* key_row0 = reinterpret_cast<const uint4*>(keys + (size_t)row * key_stride * kHeadDim);
+  __syncthreads();
+  for (int i0 = 0; i0 < count; i0 += kRowsPerStep * kSteps) {
+    uint4 v[kSteps];
 #pragma unroll
-      for (int v = 0; v < kHeadDim / 8; ++v) acc = sum_squares8(kp[v], q_dtype, acc);
+    for (int j = 0; j < kSteps; ++j) {
+      const int key = first + min(i0 + kRowsPerStep * j + (tid >> 4), count - 1);
+      v[j] = key_row0[(size_t)min(key, prev_length - 1) * (kHeadDim / 8) + sub];
     }
-    s_norm[i] = sqrt(acc);
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      const int i = i0 + kRowsPerStep * j + (tid >> 4);
+      double acc = sum_squares8(v[j], q_dtype, 0.0);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, kWave);
+      const bool mine = sub == 0 && i < count;
+      const double norm = first + i < prev_length ? sqrt(acc) : 0.0;
+      if (mine)
+        __hip_atomic_fetch_max(&s_block_max[i / block_size], (unsigned long long)__double_as_longlong(norm),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  // The heads' totals, once per workgroup (wave 0, one head per lane).
+  if (tid < kWave) {
+    double radius = s_radius[tid];
+    double slack = s_slack[tid];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      radius += __shfl_xor(radius, off, kWave);
+      slack += __shfl_xor(slack, off, kWave);
+    }
+    if (tid == 0) {
+      s_total[0] = radius;
+      s_total[1] = slack;
+    }
   }
   __syncthreads();
   if (tid < blocks_per_wg) {
     const int b = blockIdx.x * blocks_per_wg + tid;
     if (b < blocks_per_row) {
-      double radius = 0.0, slack = 0.0;
-      for (int h = 0; h < kHeads; ++h) {
-        radius += s_radius[h];
-        slack += s_slack[h];
-      }
-      double best = 0.0;
-      for (int j = 0; j < block_size; ++j) best = fmax(best, s_norm[tid * block_size + j]);
-      margins[(size_t)row * blocks_per_row + b] = best * (radius + kScoreRoundingAllowance * slack) * kRadiusRoundUp;
+      const double best = __longlong_as_double((long long)s_block_max[tid]);
+      margins[(size_t)row * blocks_per_row + b] =
+          best * (s_total[0] + kScoreRoundingAllowance * s_total[1]) * kRadiusRoundUp;
     }
   }
 }
