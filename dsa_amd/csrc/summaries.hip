@@ -26,6 +26,30 @@ __global__ __launch_bounds__(256) void block_max_kernel(const float* scores, int
   out[row * nb + block] = m;
 }
 
+// Power-of-two blocks of at most 128 keys, read coalesced: wave w takes run
+// w of a row, 64 consecutive keys (128 for 128-key blocks: lane l reads keys
+// l and l + 64), and reduces each block across its lanes by shuffles; the
+// block's first lane writes its maximum.  Same fmaxf from -inf as above.
+__global__ __launch_bounds__(256) void block_max_runs_kernel(const float* scores, int64_t rows, int length,
+                                                             int64_t row_stride, int bs, int runs_per_row,
+                                                             float* out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t run = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int64_t row = run / runs_per_row;
+  if (row >= rows) return;  // whole waves
+  const int span = bs > kWave ? 2 * kWave : kWave;
+  const int reach = min(bs, kWave);
+  const int base = (int)(run % runs_per_row) * span;
+  const float* x = scores + row * row_stride;
+  float m = -__builtin_inff();
+  if (base + lane < length) m = fmaxf(m, x[base + lane]);
+  if (span > kWave && base + kWave + lane < length) m = fmaxf(m, x[base + kWave + lane]);
+  for (int off = 1; off < reach; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  const int nb = (length + bs - 1) / bs;
+  const int block = (base + lane) / bs;
+  if (lane % reach == 0 && block < nb) out[row * nb + block] = m;
+}
+
 __device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dtype) {
   switch (dtype) {
     case kF32: return static_cast<const float*>(p)[i];
@@ -285,6 +309,16 @@ extern "C" int dsa_block_max(const float* scores, int64_t rows, int64_t length,
   DSA_REQUIRE(row_stride >= length, "row_stride < length");
   DSA_REQUIRE(block_size > 0, "block_size must be positive");
   const int64_t nb = (length + block_size - 1) / block_size;
+  if (block_size <= 2 * kWave && (block_size & (block_size - 1)) == 0) {
+    const int64_t span = block_size > kWave ? 2 * kWave : kWave;
+    const int64_t runs = (length + span - 1) / span;
+    const int64_t waves = rows * runs;
+    DSA_REQUIRE((waves + 3) / 4 < (int64_t(1) << 31), "too many score rows");
+    hipLaunchKernelGGL(block_max_runs_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), scores, rows, (int)length, row_stride, (int)block_size,
+                       (int)runs, out);
+    return check_launch("block_max_runs_kernel");
+  }
   const int64_t total = rows * nb;
   hipLaunchKernelGGL(block_max_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), scores, rows, (int)length, row_stride,

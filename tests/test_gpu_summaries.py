@@ -15,7 +15,8 @@ from oracle import replay as R
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("block_size", [16, 32, 64, 128, 7])
+# Powers of two up to 128 take the coalesced run kernel; 7 and 200 the per-block one.
+@pytest.mark.parametrize("block_size", [1, 16, 32, 64, 128, 7, 200])
 def test_block_max_exact(device, block_size) -> None:
     rng = np.random.default_rng(block_size)
     host = rng.normal(size=(3, 1001)).astype(np.float32)
