@@ -708,6 +708,28 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
   const int row = blockIdx.x;
   const int nb = s.blocks;
   const int bs = s.block_size;
+  // A thread's blocks (at most two: nb <= 2048): their refresh flags and
+  // stored state are loaded first, unconditionally (clamped block; the state
+  // rows hold at least nb entries), so that their latency overlaps the top-k
+  // reads below.
+  constexpr int kPer = kMaxTemporalBlocks / 1024;
+  bool refreshed[kPer];
+  float last_in[kPer], ema_in[kPer], vol_in[kPer];
+  int age_in[kPer], cold_in[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int bc = min(tid + 1024 * j, nb - 1);
+    const size_t at = (size_t)row * s.ap.stride + bc;
+    refreshed[j] = kInit || kTeacher || s.evaluated[(size_t)row * nb + bc] ||
+                   (s.rescued && s.rescued[(size_t)row * nb + bc]);
+    if constexpr (!kInit) cold_in[j] = s.ap.cold[at];
+    if constexpr (!kInit && !kTeacher) {
+      last_in[j] = s.ap.last_max[at];
+      ema_in[j] = s.ap.ema[at];
+      vol_in[j] = s.ap.vol[at];
+      age_in[j] = s.ap.age[at];
+    }
+  }
   for (int b = tid; b < nb; b += 1024) hot[b] = 0;
   __syncthreads();
   for (int i = tid; i < s.k; i += 1024) {
@@ -717,10 +739,12 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
   __syncthreads();
   const float* srow = s.scores + (size_t)row * s.score_stride;
   const dsa_approx_policy& p = s.ap.p;
-  for (int b = tid; b < nb; b += 1024) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int b = tid + 1024 * j;
+    if (b >= nb) break;
     const size_t at = (size_t)row * s.ap.stride + b;
-    const bool refresh =
-        kInit || kTeacher || s.evaluated[(size_t)row * nb + b] || (s.rescued && s.rescued[(size_t)row * nb + b]);
+    const bool refresh = refreshed[j];
     float seen = -__builtin_inff();
     if (refresh) {
       const int end = min(s.length, (b + 1) * bs);
@@ -733,7 +757,7 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
       s.ap.age[at] = 0;
       s.ap.cold[at] = hot[b] ? 0 : 1;
     } else if constexpr (kTeacher) {
-      const int cold = b < s.state_blocks ? (int)s.ap.cold[at] : 1;
+      const int cold = b < s.state_blocks ? cold_in[j] : 1;
       s.ap.last_max[at] = seen;
       s.ap.ema[at] = seen;
       s.ap.vol[at] = 0.f;
@@ -741,11 +765,11 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
       s.ap.cold[at] = (int16_t)(hot[b] ? 0 : min(cold + 1, 32767));
     } else {
       const bool stored = b < s.state_blocks;
-      float last = stored ? s.ap.last_max[at] : -__builtin_inff();
-      float ema = stored ? s.ap.ema[at] : -__builtin_inff();
-      float vol = stored ? s.ap.vol[at] : 0.f;
-      int age = min((stored ? (int)s.ap.age[at] : 0) + 1, 32767);
-      const int cold = stored ? (int)s.ap.cold[at] : 1;
+      float last = stored ? last_in[j] : -__builtin_inff();
+      float ema = stored ? ema_in[j] : -__builtin_inff();
+      float vol = stored ? vol_in[j] : 0.f;
+      int age = min((stored ? age_in[j] : 0) + 1, 32767);
+      const int cold = stored ? cold_in[j] : 1;
       if (refresh) {
         const double observed = (double)seen;
         const double mean = __builtin_isfinite(ema) ? (double)ema : observed;
