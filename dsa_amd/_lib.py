@@ -69,7 +69,7 @@ _SIGNATURES: dict[str, list] = {
     "dsa_block_key_norms": [_p, _i64, _i64, _i64, _i32, _i32, _p, _p],
     "dsa_temporal_score_radius": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "dsa_temporal_step": [
-        _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
+        _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
         _p, _i64, _p,
     ],
     "dsa_temporal_keys_loaded": [_p, _i64, _i64, _i64, _i32, _p, _p],

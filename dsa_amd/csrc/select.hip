@@ -402,8 +402,10 @@ struct ListArgs {
   uint32_t total_wgs;       // rows * chunks (the grid is padded to a multiple of 8)
   int64_t* out_idx;         // [rows, k]
   float* out_val;           // [rows, k] or null
-  const uint32_t* count_parts;  // [rows * chunks] or null: per-chunk counts summed into count_out
+  const uint32_t* count_parts;  // [rows * chunks] or null: per-chunk counts (bits 0-30) summed into count_out,
+                                // bit 31 a per-chunk flag counted into flag_out
   int32_t* count_out;           // [rows]
+  int32_t* flag_out;            // [rows] or null
 };
 
 struct ListShared {
@@ -436,9 +438,20 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
   const uint64_t* lrow = a.lists + (size_t)row * n;
   if (a.count_parts && c == 0 && wave == 0) {
     uint32_t sum = 0;
-    for (uint32_t j = lane; j < chunks; j += kWave) sum += a.count_parts[(size_t)row * chunks + j];
-    for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
-    if (lane == 0) a.count_out[row] = (int32_t)sum;
+    uint32_t flags = 0;
+    for (uint32_t j = lane; j < chunks; j += kWave) {
+      const uint32_t part = a.count_parts[(size_t)row * chunks + j];
+      sum += part & 0x7fffffffu;
+      flags += part >> 31;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      sum += (uint32_t)__shfl_xor((int)sum, off, kWave);
+      flags += (uint32_t)__shfl_xor((int)flags, off, kWave);
+    }
+    if (lane == 0) {
+      a.count_out[row] = (int32_t)sum;
+      if (a.flag_out) a.flag_out[row] = (int32_t)flags;
+    }
   }
 
   // This thread's list j and its place r among the list's threads.
@@ -744,10 +757,11 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
 int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64_t k,
                         const ListPlan& plan, const SelectWorkspace& ws, int64_t* out_idx,
                         float* out_val, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
-                        const uint32_t* count_parts, int32_t* count_out) {
+                        const uint32_t* count_parts, int32_t* count_out, int32_t* flag_out) {
   ListArgs a;
   a.count_parts = count_parts;
   a.count_out = count_out;
+  a.flag_out = flag_out;
   a.scores = scores;
   a.lists = ws.cand;
   a.meta = ws.list_meta;

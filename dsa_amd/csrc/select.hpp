@@ -102,12 +102,13 @@ int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
 
 // Selects the top-k of scores [rows, length] from the candidate lists that
 // the scoring kernel wrote to ws under `plan`.
-// With count_parts, also writes count_out[row] = the sum of the row's
-// count_parts[row * plan.chunks + j] over its chunks j.
+// With count_parts, also writes count_out[row] = the sum of bits 0-30 of the
+// row's count_parts[row * plan.chunks + j] over its chunks j, and, with
+// flag_out, flag_out[row] = the number of those parts with bit 31 set.
 int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64_t k,
                         const ListPlan& plan, const SelectWorkspace& ws, int64_t* out_idx,
                         float* out_val, hipStream_t stream, hipEvent_t start = nullptr,
                         hipEvent_t stop = nullptr, const uint32_t* count_parts = nullptr,
-                        int32_t* count_out = nullptr);
+                        int32_t* count_out = nullptr, int32_t* flag_out = nullptr);
 
 }  // namespace dsa

@@ -69,6 +69,7 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
     a.ws.floor[row] = 0xffffffffu;
     a.ws.loaded[row] = 0;
     a.qk_scored[row] = 0;
+    if (a.waits_given_up) a.waits_given_up[row] = 0;  // only the fused static step waits
     s_exact = 0;
   }
   const int first_new = a.prev_length / bs;
@@ -936,6 +937,7 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
                                  const int64_t* prev_topk, const float* gamma, const double* block_margins,
                                  float* scores,
                                  uint8_t* evaluated_blocks, int64_t* out_topk, int32_t* qk_scored,
+                                 int32_t* waits_given_up,
                                  int64_t batch, int64_t length, int64_t k, int32_t block_size,
                                  int32_t scan_order, int32_t wave, int32_t key_dtype, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
@@ -963,6 +965,7 @@ extern "C" int dsa_temporal_step(const void* queries, const float* weights, cons
   a.scores = scores;
   a.evaluated = evaluated_blocks;
   a.qk_scored = qk_scored;
+  a.waits_given_up = waits_given_up;
   a.rows = (int32_t)batch;
   a.length = (int32_t)length;
   a.k = (int32_t)k;

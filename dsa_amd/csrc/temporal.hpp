@@ -27,7 +27,7 @@ constexpr int kMaxFusedWgs = 4096;
 struct TemporalWorkspace {
   uint64_t* slots;      // [kMaxFusedWgs] (generation << 32) | least seed key of each fused workgroup; zero
                         // before the workspace's first use
-  uint32_t* qk_parts;   // [kMaxFusedWgs] keys each fused workgroup scored
+  uint32_t* qk_parts;   // [kMaxFusedWgs] keys each fused workgroup scored; bit 31: its wait gave up
   uint32_t* tau;        // [rows] ordered key of the threshold in force
   uint32_t* floor;      // [rows] least of run (the k-th largest evaluated score), dynamic rounds
   uint32_t* loaded;     // [rows] key rows a dynamic step loaded (seeds + every key of its rounds' scored blocks)
@@ -139,6 +139,7 @@ struct TemporalArgs {
   float* scores;          // [rows][length]
   uint8_t* evaluated;     // [rows][blocks]
   int32_t* qk_scored;     // [rows]
+  int32_t* waits_given_up;  // [rows] or null: fused static workgroups whose wait for the row's seed minima ran out
   int32_t rows, length, k, block_size, blocks, prev_length, prev_blocks;
   int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper, 3 order_key
   int32_t wave_start, wave_len;

@@ -22,15 +22,22 @@
 // a 64-bit atomic written once per call; nothing else needs ordering.  The
 // grid is launched only when all of it fits on the device at once (at most
 // the occupancy limit times the CU count), so every workgroup a row waits for
-// becomes resident once the work ahead of it on the stream drains.  The wait
-// is also bounded: a workgroup that gives up keeps every block of its chunk
-// (a superset, visible in qk_scored) and the kernel still ends.  (A
-// cooperative launch would promise residency outright, but costs ~20 us of
-// host-side setup per call here.)
+// becomes resident once the work ahead of it on the stream drains.  The
+// residency check counts the device's whole capacity, not the CUs other work
+// holds, so the wait is also bounded: a workgroup that gives up keeps every
+// block of its chunk (a superset of the filter's decisions) and the kernel
+// still ends.  It marks bit 31 of its scored-key count, and the list select
+// reports the row's marks in waits_given_up.  (A cooperative launch would
+// promise residency outright, but costs ~20 us of host-side setup per call
+// here.)
 //
 // Scores use the dense kernel's tile code (indexer.hpp), so an evaluated key
 // gets the dense score bit for bit.
+#include <unistd.h>
+
 #include <atomic>
+#include <chrono>
+#include <cstdlib>
 #include <mutex>
 
 #include "lists.hpp"
@@ -44,6 +51,7 @@ constexpr int kFusedWaves = kDecodeWaves;
 constexpr int kFusedThreads = 64 * kFusedWaves;
 constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer offset past every unit resource
 constexpr uint32_t kSpinLimit = 1u << 22;      // polls (each ~1 us) before a workgroup stops waiting
+constexpr uint32_t kGaveUp = 0x80000000u;      // scored-key count bit: the workgroup's wait ran out
 
 #ifdef DSA_PHASE_TRACE
 // Per workgroup (by blockIdx.x): 0 start, 1 seeds listed, 2 seeds scored,
@@ -57,6 +65,7 @@ struct FusedPlan {
   uint32_t quota;
   uint32_t total_wgs;
   uint32_t gen;
+  uint32_t spin_limit;  // polls of the exchange before giving up
 };
 
 template <class Tag, class KF>
@@ -66,7 +75,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   __shared__ uint16_t seed_list[kListChunkMax];         // the same, as chunk-local positions
   __shared__ uint32_t s_nseeds;
   __shared__ uint32_t tile_bits[kListChunkMax / 512];  // 16-key tiles of the chunk's kept blocks
-  __shared__ uint32_t s_least, s_tau, s_count, s_list_bin;
+  __shared__ uint32_t s_least, s_tau, s_count, s_list_bin, s_gave_up;
   // Scaled keys: the chunk's 128-key block scales, read once here, so that
   // no scale load sits behind a unit's MFMAs (waiting for one there made the
   // compiler drain every unit in flight).
@@ -236,7 +245,8 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   if (wave == 0) {
     const uint32_t first = (uint32_t)row * (uint32_t)p.chunks;
     uint32_t tau = float_to_ordered(-__builtin_inff());  // if the wait gives up: keep every block
-    for (uint32_t it = 0; it < kSpinLimit; ++it) {
+    uint32_t gave_up = kGaveUp;
+    for (uint32_t it = 0; it < p.spin_limit; ++it) {
       bool ready = true;
       uint32_t mn = 0xffffffffu;
       for (int j = lane; j < p.chunks; j += kWave) {
@@ -247,11 +257,15 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
       if (__ballot(!ready) == 0) {
         for (int off = 32; off > 0; off >>= 1) mn = min(mn, (uint32_t)__shfl_xor((int)mn, off, kWave));
         tau = mn;
+        gave_up = 0;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
     }
-    if (lane == 0) s_tau = tau;
+    if (lane == 0) {
+      s_tau = tau;
+      s_gave_up = gave_up;
+    }
   }
   __syncthreads();
 
@@ -285,7 +299,7 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   }
   if (count) __hip_atomic_fetch_add(&s_count, count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   __syncthreads();
-  if (tid == 0) a.ws.qk_parts[logical] = s_count;
+  if (tid == 0) a.ws.qk_parts[logical] = s_count | s_gave_up;  // s_count <= chunk_keys < 2^31
 
   DSA_TRACE_MARK(g_trace_static, blockIdx.x, 4);
   // 4. The chunk's scores: kept tiles scored, the rest -inf but for seeds.
@@ -341,7 +355,32 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   DSA_TRACE_MARK(g_trace_static, blockIdx.x, 6);
 }
 
-std::atomic<uint32_t> g_generation{0};
+// Calls are stamped with consecutive generations from a start drawn per
+// library load (clock and process id), so that a workspace whose slots an
+// earlier load of the library stamped is not read as this call's.
+uint32_t first_generation() {
+  const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
+  uint64_t x = t ^ ((uint64_t)getpid() << 32) ^ (uint64_t)reinterpret_cast<uintptr_t>(&t);
+  x ^= x >> 33;  // splitmix64 finaliser
+  x *= 0xff51afd7ed558ccdull;
+  x ^= x >> 33;
+  x *= 0xc4ceb9fe1a85ec53ull;
+  x ^= x >> 33;
+  return (uint32_t)x;
+}
+
+std::atomic<uint32_t> g_generation{first_generation()};
+
+// Polls of the exchange before a workgroup gives up: kSpinLimit, or
+// DSA_AMD_STATIC_SPIN_LIMIT from the environment (a test sets 0 to make
+// every wait give up from the host, so the kernel still ends normally).
+uint32_t spin_limit() {
+  const char* v = std::getenv("DSA_AMD_STATIC_SPIN_LIMIT");
+  if (!v || !*v) return kSpinLimit;
+  char* end = nullptr;
+  const unsigned long n = std::strtoul(v, &end, 10);
+  return (end && *end == 0 && n < kSpinLimit) ? (uint32_t)n : kSpinLimit;
+}
 
 // Workgroups of one temporal_static_kernel instance resident at once on the
 // current device (cached per device and instance).
@@ -388,6 +427,7 @@ int launch_static(TemporalArgs& a, const ListPlan& plan, hipStream_t stream, boo
   uint32_t gen = 0;
   while (gen == 0) gen = ++g_generation;  // 0 never names a call (a zeroed slot)
   p.gen = gen;
+  p.spin_limit = spin_limit();
   hipLaunchKernelGGL((temporal_static_kernel<Tag, KF>), dim3((unsigned)grid), dim3(kFusedThreads), (uint32_t)lds,
                      stream, a, p);
   if (int st = check_launch("temporal_static_kernel")) return st;
@@ -410,7 +450,7 @@ int temporal_static_fused(TemporalArgs& a, int32_t key_dtype, int64_t* out_topk,
   }
   if (st || !ran) return st;
   return launch_select_lists(a.scores, a.rows, a.length, a.k, plan, a.ws.select, out_topk, nullptr, stream, nullptr,
-                             nullptr, a.ws.qk_parts, a.qk_scored);
+                             nullptr, a.ws.qk_parts, a.qk_scored, a.waits_given_up);
 }
 
 }  // namespace dsa

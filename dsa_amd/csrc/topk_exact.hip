@@ -34,10 +34,6 @@ __device__ __forceinline__ uint64_t f64_to_ordered(double d) {
   if (u == 0x8000000000000000ull) u = 0ull;
   return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
 }
-__device__ __forceinline__ double ordered_to_f64(uint64_t o) {
-  const uint64_t u = (o >> 63) ? (o & 0x7fffffffffffffffull) : ~o;
-  return __longlong_as_double((long long)u);
-}
 
 struct ExactArgs {
   const void* values;  // [rows][row_stride] float64 or float32
@@ -57,10 +53,12 @@ __device__ __forceinline__ uint64_t key_at(const void* row, int64_t i) {
   else return (uint64_t)float_to_ordered(static_cast<const float*>(row)[i]) << 32;
 }
 
+// Output values are copied from the input row at the chosen index, bits and
+// all, not rebuilt from the order key (which folds -0.0 onto +0.0).
 template <bool kF64>
-__device__ __forceinline__ void put_value(void* out, int64_t at, uint64_t key) {
-  if constexpr (kF64) static_cast<double*>(out)[at] = ordered_to_f64(key);
-  else static_cast<float*>(out)[at] = ordered_to_float((uint32_t)(key >> 32));
+__device__ __forceinline__ void put_value(void* out, int64_t at, const void* row, int64_t i) {
+  if constexpr (kF64) static_cast<double*>(out)[at] = static_cast<const double*>(row)[i];
+  else static_cast<float*>(out)[at] = static_cast<const float*>(row)[i];
 }
 
 struct ExactShared {
@@ -143,7 +141,7 @@ __global__ __launch_bounds__(kExactThreads) void topk_exact_kernel(ExactArgs a) 
           idx_a[pos] = (uint32_t)i;
         } else {
           oidx[pos] = i;
-          if (a.out_val) put_value<kF64>(a.out_val, row * (int64_t)k + pos, key);
+          if (a.out_val) put_value<kF64>(a.out_val, row * (int64_t)k + pos, rbase, i);
         }
       }
     }
@@ -236,7 +234,7 @@ __global__ __launch_bounds__(kExactThreads) void topk_exact_kernel(ExactArgs a) 
   }
   for (uint32_t j = tid; j < k; j += kExactThreads) {
     oidx[j] = (int64_t)src_i[j];
-    if (a.out_val) put_value<kF64>(a.out_val, row * (int64_t)k + j, src_k[j]);
+    if (a.out_val) put_value<kF64>(a.out_val, row * (int64_t)k + j, rbase, src_i[j]);
   }
 }
 

@@ -133,10 +133,28 @@ def _exact_dtype(matrix: torch.Tensor) -> torch.Tensor:
     if matrix.dtype == torch.float64:
         return matrix
     if matrix.dtype == torch.bool or not matrix.dtype.is_floating_point:
-        if matrix.numel() and matrix.dtype == torch.int64 and int(matrix.abs().max()) > 2**53:
-            raise ValueError("integer values beyond 2^53 in magnitude cannot be ordered exactly")
-        return matrix.to(torch.float64)
+        return _integers_as_float64(matrix)
     raise ValueError(f"unsupported dtype {matrix.dtype}")
+
+
+def _integers_as_float64(matrix: torch.Tensor) -> torch.Tensor:
+    """Integer or bool values as float64, which holds every integer up to
+    2^53 in magnitude exactly; anything beyond raises ValueError (it would be
+    rounded into a tie, e.g. 2^63 and 2^63 + 1).  The check reads the extremes
+    without abs(), which overflows at -2^63; uint64 is read through its int64
+    bits, since torch has no reductions over it (a value of 2^63 or more has
+    its top bit set and reads negative)."""
+
+    limit = 2**53
+    if matrix.dtype == torch.uint64:
+        bits = matrix.view(torch.int64)
+        if bits.numel() and (bool((bits < 0).any()) or int(bits.max()) > limit):
+            raise ValueError("integer values beyond 2^53 in magnitude cannot be ordered exactly")
+        return bits.to(torch.float64)
+    if matrix.dtype == torch.int64 and matrix.numel():
+        if int(matrix.max()) > limit or int(matrix.min()) < -limit:
+            raise ValueError("integer values beyond 2^53 in magnitude cannot be ordered exactly")
+    return matrix.to(torch.float64)
 
 
 def _exact_topk(matrix: torch.Tensor, k: int, *, sorted: bool, return_values: bool):

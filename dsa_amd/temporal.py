@@ -41,6 +41,11 @@ class TemporalStep:
     scores: torch.Tensor  # fp32 [B, L], -inf for keys that were not scored
     evaluated_blocks: torch.Tensor  # bool [B, ceil(L / block_size)]
     qk_scored: torch.Tensor  # int32 [B]
+    # int32 [B]: workgroups of the fused static launch whose bounded wait for
+    # the row's seed minima ran out; they kept every block of their chunk, so
+    # a nonzero row holds a superset of the filter's decisions.  Always 0 on
+    # the other paths (and None where the step does not report it).
+    waits_given_up: torch.Tensor | None = None
 
 
 def _workspace(device, stream, batch, length, k, block_size) -> torch.Tensor:
@@ -72,14 +77,15 @@ def keys_loaded(step: TemporalStep, block_size: int) -> torch.Tensor:
 
 
 def _outputs(device, batch: int, length: int, blocks: int, k: int):
-    """The step's four outputs as views of one allocation (one allocator
-    call per step instead of four): scores fp32 [B, L], top-k int64 [B, k],
-    keys scored int32 [B] and kept-block flags uint8 [B, blocks]."""
+    """The step's outputs as views of one allocation (one allocator call per
+    step instead of five): scores fp32 [B, L], top-k int64 [B, k], keys
+    scored int32 [B], kept-block flags uint8 [B, blocks] and given-up waits
+    int32 [B]."""
 
     def up(n: int) -> int:
         return (n + 255) // 256 * 256
 
-    sizes = (batch * length * 4, batch * k * 8, batch * 4, batch * blocks)
+    sizes = (batch * length * 4, batch * k * 8, batch * 4, batch * blocks, batch * 4)
     offsets, total = [], 0
     for size in sizes:
         offsets.append(total)
@@ -89,7 +95,8 @@ def _outputs(device, batch: int, length: int, blocks: int, k: int):
     topk = buf[offsets[1] : offsets[1] + sizes[1]].view(torch.int64).view(batch, k)
     qk = buf[offsets[2] : offsets[2] + sizes[2]].view(torch.int32)
     evaluated = buf[offsets[3] : offsets[3] + sizes[3]].view(batch, blocks)
-    return scores, evaluated, topk, qk
+    gave_up = buf[offsets[4] : offsets[4] + sizes[4]].view(torch.int32)
+    return scores, evaluated, topk, qk, gave_up
 
 
 def temporal_step(
@@ -186,15 +193,15 @@ def temporal_step(
         margins = block_margins.to(device=device, dtype=torch.float64).contiguous()
     stream = _lib.stream_of(keys)
     blocks = math.ceil(length / block_size)
-    scores, evaluated, topk, qk = _outputs(device, batch, length, blocks, k)
+    scores, evaluated, topk, qk, gave_up = _outputs(device, batch, length, blocks, k)
     ws = _workspace(device, stream, batch, length, k, block_size)
     _lib.call(
         "dsa_temporal_step", _lib.ptr(queries), _lib.ptr(weights), _lib.ptr(keys), key_stride, _lib.ptr(key_scales),
         _lib.ptr(prev_max), previous_length, _lib.ptr(seeds), _lib.ptr(gamma_t), _lib.ptr(margins), _lib.ptr(scores),
-        _lib.ptr(evaluated), _lib.ptr(topk), _lib.ptr(qk), batch, length, k, block_size,
+        _lib.ptr(evaluated), _lib.ptr(topk), _lib.ptr(qk), _lib.ptr(gave_up), batch, length, k, block_size,
         SCAN_ORDERS[scan_order], wave, _lib.dtype_code(keys.dtype), _lib.ptr(ws), ws.numel(), stream,
     )
-    return TemporalStep(topk, scores, evaluated.view(torch.bool), qk)
+    return TemporalStep(topk, scores, evaluated.view(torch.bool), qk, gave_up)
 
 
 def block_max(scores: torch.Tensor, block_size: int) -> torch.Tensor:

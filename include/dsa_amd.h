@@ -330,6 +330,13 @@ int dsa_score_topk_noalloc(const void* queries, const float* weights, const void
  *   out_topk    [batch, k] int64 out: stable top-k of the evaluated keys, in
  *               ascending index order
  *   qk_scored   [batch] int32 out: keys scored (seeds + kept blocks, once each)
+ *   waits_given_up [batch] int32 out, or NULL: workgroups of the fused static
+ *               launch (below) whose bounded wait for the row's seed minima
+ *               ran out (other work held the CUs it needed for ~4 s).  Such a
+ *               workgroup keeps every block of its chunk, so the row's kept
+ *               blocks, qk_scored and top-k are a superset of the filter's;
+ *               0 means the decisions are exactly the filter's.  Always 0 on
+ *               the other paths, which do not wait.
  *   keys        [batch, key_stride, 128]: the first `length` rows of each
  *               sequence are scored (a KV cache with spare capacity needs no
  *               copy); fp8 key_scales are [batch, ceil(key_stride / 128)]
@@ -372,7 +379,8 @@ int dsa_temporal_step(const void* queries, const float* weights, const void* key
                       const int64_t* prev_topk,
                       const float* gamma, const double* block_margins, float* scores, uint8_t* evaluated_blocks,
                       int64_t* out_topk,
-                      int32_t* qk_scored, int64_t batch, int64_t length, int64_t k, int32_t block_size,
+                      int32_t* qk_scored, int32_t* waits_given_up, int64_t batch, int64_t length, int64_t k,
+                      int32_t block_size,
                       int32_t scan_order, int32_t wave, int32_t key_dtype, void* workspace,
                       int64_t workspace_bytes, void* stream);
 

@@ -212,6 +212,7 @@ def test_static_step_paths_agree(device, monkeypatch, block, gamma_sigma, prev_l
     def run():
         s = temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
                                    method="static")
+        assert s.waits_given_up.cpu().numpy().tolist() == [0] * batch, "a wait gave up"
         return (s.scores.cpu().numpy(), s.evaluated_blocks.cpu().numpy(), s.qk_scored.cpu().numpy(),
                 s.topk.cpu().numpy())
 
@@ -247,6 +248,56 @@ def test_static_step_paths_agree(device, monkeypatch, block, gamma_sigma, prev_l
         assert not kept.all(), "the negative margin pruned nothing"
     if gamma_sigma <= -4.0:  # below the seeds' own drift: blocks holding seeds are pruned too
         assert seeds_in_pruned > 0, "no pruned block holds a seed"
+
+
+def test_static_step_reports_given_up_waits(device, monkeypatch) -> None:
+    # The host makes every fused workgroup's bounded wait for its row's seed
+    # minima give up at once (a spin limit of 0 polls): the kernel still ends
+    # normally, each workgroup keeps every block of its chunk, and the step
+    # reports the given-up waits.  The documented superset is then the dense
+    # step: every block kept, every key scored with its dense score, and the
+    # dense top-k.  The next call, with the default limit, is the filter's
+    # exact step again and reports none.
+    print("static step: given-up waits forced from the host", flush=True)
+    batch, prev_length, length, k, block = 4, 16384, 16385, 2048, 64
+    q_prev, q_cur, w, keys = transition(batch, prev_length, length, seed=77)
+    q_prev, q_cur, w, keys = q_prev.to(device), q_cur.to(device), w.to(device), keys.to(device)
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys[:, :prev_length].contiguous(), k, return_scores=True)
+    prev_max = temporal.block_max(prev_scores, block)
+    dense = decode.indexer_topk(q_cur, w, keys, k, return_scores=True)[1].cpu().numpy()
+    gamma = torch.full((batch,), -3.0 * float(prev_scores.std()), device=device)
+
+    def run():
+        return temporal.temporal_step(q_cur, w, keys, prev_max, prev_length, prev_topk, gamma, block_size=block,
+                                      method="static")
+
+    monkeypatch.setenv("DSA_AMD_STATIC_SPIN_LIMIT", "0")
+    forced = run()
+    monkeypatch.delenv("DSA_AMD_STATIC_SPIN_LIMIT")
+    gave_up = forced.waits_given_up.cpu().numpy()
+    assert (gave_up > 0).all(), gave_up
+    assert forced.evaluated_blocks.cpu().numpy().all()
+    assert forced.qk_scored.cpu().numpy().tolist() == [length] * batch
+    np.testing.assert_array_equal(forced.scores.cpu().numpy(), dense)
+    for b in range(batch):
+        assert forced.topk[b].cpu().numpy().tolist() == T.topk_index_order(dense[b], k).tolist(), b
+
+    exact = run()
+    assert exact.waits_given_up.cpu().numpy().tolist() == [0] * batch
+    kept = exact.evaluated_blocks.cpu().numpy()
+    assert not kept.all(), "the negative margin pruned nothing"
+    seeds = prev_topk.cpu().numpy()
+    blocks = math.ceil(length / block)
+    for b in range(batch):
+        previous_max = np.full(blocks, -np.inf)
+        previous_max[: prev_max.shape[1]] = prev_max[b].cpu().double().numpy()
+        upper = R.upper_bounds(previous_max, float(gamma[b]), prev_length, length, block)
+        scan = R.block_scan_order("address", upper, R.block_maxima(dense[b], block), np.zeros(blocks, dtype=bool))
+        current = dense[b].astype(np.float64)
+        trace = R.run_filter(current, seeds[b], k, block, upper, scan, dynamic=False,
+                             fixed_threshold=float(current[seeds[b]].min()), wave=1)
+        np.testing.assert_array_equal(kept[b], trace.kept, err_msg=f"row {b}: kept blocks")
+        assert int(exact.qk_scored[b]) == trace.scored
 
 
 @pytest.mark.parametrize("batch,prev_length,length,k,block,capacity", [

@@ -173,15 +173,16 @@ def test_float64_rows_exact(device, kind, length, k) -> None:
     host = _f64_rows(kind, 2, length, seed=length + k)
     x = torch.from_numpy(host).to(device)
     idx_sorted, val_sorted = metrics.topk(x, k, sorted=True, return_values=True)
-    idx_index = metrics.topk(x, k, sorted=False)
+    idx_index, val_index = metrics.topk(x, k, sorted=False, return_values=True)
     assert val_sorted.dtype == torch.float64
     for r in range(2):
         want = T.stable_topk(host[r], k)
         assert idx_sorted[r].cpu().numpy().tolist() == want.tolist(), r
-        np.testing.assert_array_equal(val_sorted[r].cpu().numpy().view(np.uint64),
-                                      np.where(host[r][want] == 0, 0.0, host[r][want]).view(np.uint64)
-                                      if kind == "zeros_inf" else host[r][want].view(np.uint64))
+        # values are x[idx] bit for bit: -0.0 stays -0.0 (it only orders as +0.0)
+        np.testing.assert_array_equal(val_sorted[r].cpu().numpy().view(np.uint64), host[r][want].view(np.uint64))
         assert idx_index[r].cpu().numpy().tolist() == np.sort(want).tolist(), r
+        np.testing.assert_array_equal(val_index[r].cpu().numpy().view(np.uint64),
+                                      host[r][np.sort(want)].view(np.uint64))
     # the reference's own API: a host float64 vector in, a numpy int64 array out
     got = metrics.stable_topk(host[0], k)
     assert isinstance(got, np.ndarray) and got.tolist() == T.stable_topk(host[0], k).tolist()

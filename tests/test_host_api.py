@@ -133,3 +133,20 @@ def test_zeroed_workspaces_are_kept_per_row_count() -> None:
     large = _lib.workspace("test_rows", cpu, 0, 1000, zeroed=True, rows=16)
     assert large is not small and not large.any()
     assert _lib.workspace("test_rows", cpu, 0, 1000, zeroed=True, rows=3) is small
+
+
+@pytest.mark.parametrize("values,dtype", [
+    ([2**63, 2**63 + 1], np.uint64),  # would round into a tie broken by index (the reference returns [1])
+    ([-(2**63), 5], np.int64),        # abs() of -2^63 overflows, so the extremes are compared directly
+    ([2**53 + 1, 1], np.int64),
+    ([-(2**53) - 1, 1], np.int64),
+])
+def test_exact_order_rejects_integers_beyond_float64(values, dtype) -> None:
+    with pytest.raises(ValueError, match="2\\^53"):
+        metrics._exact_dtype(torch.from_numpy(np.array(values, dtype=dtype)))
+
+
+def test_exact_order_keeps_integers_within_float64() -> None:
+    for values, dtype in (([2**53, 7], np.uint64), ([-(2**53), 7], np.int64), ([3, 1], np.uint32)):
+        got = metrics._exact_dtype(torch.from_numpy(np.array(values, dtype=dtype)))
+        assert got.dtype == torch.float64 and [int(v) for v in got.tolist()] == values

@@ -1,11 +1,15 @@
 """The allocation-free decode step (dsa_score_topk_noalloc) against the
 workspace-taking dsa_score_topk, called through the C ABI.
 
-Three calls in a row share the GPU's scratch array: the C2 shape (candidate
-list plan), then a smaller one that takes the histogram plan, then a small
-list-plan one.  Each must equal dsa_score_topk on the same inputs bit for
-bit (scores, indices and values), whatever the previous call left in the
-array.  Shapes beyond the array are rejected with a clear error.
+Calls in a row share the GPU's scratch array.  A one-row call of the
+candidate-list plan (64 lists of a 16384-key row) writes its lists from
+about 19 KiB to 147 KiB into the array, past its 16 KiB histogram, where the
+next call, a sixteen-row call of the histogram plan, keeps its 256 KiB of
+histograms: that call is only right if the entry point clears them first.
+The C2 shape (list plan), a smaller histogram-plan call and a small list-plan
+call follow.  Each must equal dsa_score_topk on the same inputs bit for bit
+(scores, indices and values), whatever the previous call left in the array.
+Shapes beyond the array are rejected with a clear error.
 """
 
 from __future__ import annotations
@@ -41,7 +45,8 @@ def _run(name, q, w, keys, k, *extra):
     return scores, idx, val
 
 
-@pytest.mark.parametrize("shapes", [[(16, 32768, 2048, 1), (2, 16384, 6000, 2), (3, 4099, 256, 3)]])
+@pytest.mark.parametrize("shapes", [[(1, 16384, 2048, 4), (16, 16384, 6000, 5), (16, 32768, 2048, 1),
+                                     (2, 16384, 6000, 2), (3, 4099, 256, 3)]])
 def test_noalloc_step_matches_workspace_step(device, shapes) -> None:
     for batch, length, k, seed in shapes:
         print(f"noalloc B={batch} L={length} k={k}", flush=True)
