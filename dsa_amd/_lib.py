@@ -7,6 +7,7 @@ point raises ``RuntimeError("HIP extension not built ...")``.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import threading
 from pathlib import Path
@@ -14,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libdsa_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -190,8 +191,28 @@ def load() -> ctypes.CDLL:
         version = lib.dsa_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libdsa_amd ABI {version} != expected {ABI_VERSION}; rebuild")
+        atexit.register(_release)
         _lib = lib
         return lib
+
+
+def _release() -> None:
+    """Interpreter-exit hook (registered when the library loads): waits for
+    the device work still queued on this process's streams and hands the
+    cached workspaces back to torch's allocator.  Python runs it before its
+    own teardown and before the C exit handlers (torch's and the HIP runtime's
+    destructors, the library's code-object unregistration), so that nothing
+    of this package is released while they tear down."""
+
+    try:
+        if torch.cuda.is_initialized():
+            with _workspace_lock:
+                devices = {key[1] for key in _workspace_cache} | {torch.cuda.current_device()}
+            for index in sorted(d for d in devices if d is not None):
+                torch.cuda.synchronize(index)
+    finally:
+        with _workspace_lock:
+            _workspace_cache.clear()
 
 
 def call(name: str, *args) -> None:

@@ -33,12 +33,6 @@
 //
 // Scores use the dense kernel's tile code (indexer.hpp), so an evaluated key
 // gets the dense score bit for bit.
-#include <unistd.h>
-
-#include <atomic>
-#include <chrono>
-#include <cstdlib>
-#include <mutex>
 
 #include "lists.hpp"
 #include "status.hpp"
@@ -355,61 +349,10 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
   DSA_TRACE_MARK(g_trace_static, blockIdx.x, 6);
 }
 
-// Calls are stamped with consecutive generations from a start drawn per
-// library load (clock and process id), so that a workspace whose slots an
-// earlier load of the library stamped is not read as this call's.
-uint32_t first_generation() {
-  const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
-  uint64_t x = t ^ ((uint64_t)getpid() << 32) ^ (uint64_t)reinterpret_cast<uintptr_t>(&t);
-  x ^= x >> 33;  // splitmix64 finaliser
-  x *= 0xff51afd7ed558ccdull;
-  x ^= x >> 33;
-  x *= 0xc4ceb9fe1a85ec53ull;
-  x ^= x >> 33;
-  return (uint32_t)x;
-}
-
-std::atomic<uint32_t> g_generation{first_generation()};
-
 // Polls of the exchange before a workgroup gives up: kSpinLimit, or
 // DSA_AMD_STATIC_SPIN_LIMIT from the environment (a test sets 0 to make
 // every wait give up from the host, so the kernel still ends normally).
-uint32_t spin_limit() {
-  const char* v = std::getenv("DSA_AMD_STATIC_SPIN_LIMIT");
-  if (!v || !*v) return kSpinLimit;
-  char* end = nullptr;
-  const unsigned long n = std::strtoul(v, &end, 10);
-  return (end && *end == 0 && n < kSpinLimit) ? (uint32_t)n : kSpinLimit;
-}
-
-// Workgroups of one temporal_static_kernel instance resident at once on the
-// current device (cached per device and instance).
-template <class Tag, class KF>
-int resident_capacity(size_t lds, int64_t& capacity) {
-  static std::mutex mutex;
-  static int64_t cached[64] = {};
-  static size_t cached_lds[64] = {};
-  int device = 0;
-  if (int st = check_hip(hipGetDevice(&device), "hipGetDevice")) return st;
-  if (device < 0 || device >= 64) return fail(DSA_STATUS_INVALID_ARGUMENT, "device %d out of range", device);
-  std::lock_guard<std::mutex> lock(mutex);
-  if (cached[device] == 0 || cached_lds[device] != lds) {
-    int per_cu = 0;
-    int cus = 0;
-    if (int st = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                               &per_cu, reinterpret_cast<const void*>(&temporal_static_kernel<Tag, KF>),
-                               kFusedThreads, lds),
-                           "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
-      return st;
-    if (int st = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
-                           "hipDeviceGetAttribute"))
-      return st;
-    cached[device] = (int64_t)per_cu * cus;
-    cached_lds[device] = lds;
-  }
-  capacity = cached[device];
-  return DSA_STATUS_OK;
-}
+uint32_t spin_limit() { return env_limit("DSA_AMD_STATIC_SPIN_LIMIT", kSpinLimit, kSpinLimit); }
 
 template <class Tag, class KF>
 int launch_static(TemporalArgs& a, const ListPlan& plan, hipStream_t stream, bool& ran) {
@@ -417,16 +360,16 @@ int launch_static(TemporalArgs& a, const ListPlan& plan, hipStream_t stream, boo
   const int64_t grid = (total + kXcds - 1) / kXcds * kXcds;
   const size_t lds = (size_t)plan.chunk_keys * sizeof(float);
   int64_t capacity = 0;
-  if (int st = resident_capacity<Tag, KF>(lds, capacity)) return st;
+  if (int st = resident_capacity(reinterpret_cast<const void*>(&temporal_static_kernel<Tag, KF>), kFusedThreads, lds,
+                                 capacity))
+    return st;
   if (total > kMaxFusedWgs || grid > capacity) return DSA_STATUS_OK;  // not resident at once: the launch path
   FusedPlan p;
   p.chunk_keys = plan.chunk_keys;
   p.chunks = plan.chunks;
   p.quota = (uint32_t)plan.quota;
   p.total_wgs = (uint32_t)total;
-  uint32_t gen = 0;
-  while (gen == 0) gen = ++g_generation;  // 0 never names a call (a zeroed slot)
-  p.gen = gen;
+  p.gen = next_generation();
   p.spin_limit = spin_limit();
   hipLaunchKernelGGL((temporal_static_kernel<Tag, KF>), dim3((unsigned)grid), dim3(kFusedThreads), (uint32_t)lds,
                      stream, a, p);

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 1
+#define DSA_ABI_VERSION 2
 
 #define DSA_STATUS_OK 0
 #define DSA_STATUS_INVALID_ARGUMENT 1
