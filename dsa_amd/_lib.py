@@ -62,6 +62,8 @@ _SIGNATURES: dict[str, list] = {
     "dsa_topk_long": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_topk_exact": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_block_max": [_p, _i64, _i64, _i64, _i32, _p, _p],
+    "dsa_project_gemm": [_p, _i32, _i64, _i64, _i64, _p, _i32, _i64, _p, _i64, ctypes.c_float, _p, ctypes.c_float,
+                         _p, _i64, _p],
     "dsa_rope": [_p, _p, _p, _i64, _i32, _i32, _i32, ctypes.c_float, _i32, _p],
     "dsa_encode_keys_epilogue": [_p, _i32, _i64, _p, _p, ctypes.c_float, _p, _i32, ctypes.c_float, _p, _i32, _i64,
                                  _p, _i64, _i64, _i32, _p],
@@ -111,6 +113,7 @@ _RESTYPES: dict[str, object] = {
     "dsa_score_topk_workspace_bytes": (_i64, [_i64, _i64]),
     "dsa_temporal_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
     "dsa_topk_exact_workspace_bytes": (_i64, [_i64, _i64, _i32]),
+    "dsa_project_gemm_workspace_bytes": (_i64, [_i64]),
 }
 
 

@@ -3,12 +3,15 @@
 Reference: ``temporal_dsa/sidecar.py``.
   * ``apply_noninterleaved_rope`` (sidecar.py:10-28) and the encoders of
     ``LightningIndexerSidecar`` (sidecar.py:31-88): the projections wq / wk /
-    weights_proj are plain GEMMs (the platform BLAS through torch); the
-    LayerNorm, RoPE, head-weight scaling and the key-cache append after them
-    run in one HIP pass per row (``dsa_encode_keys_epilogue``,
-    ``dsa_encode_queries_epilogue``, ``dsa_rope``), with torch's per-op
-    rounding in the row dtype.  The module runs in its parameter dtype
-    (fp32 or bf16); autocast's mixed flow is not reproduced.
+    weights_proj run in the library's own kernels, a weight-streaming kernel
+    for a decode step (``dsa_project_rows``) and an MFMA GEMM for larger
+    batches (``dsa_project_gemm``); the LayerNorm, RoPE, head-weight scaling
+    and the key-cache append after them run in one HIP pass per row
+    (``dsa_encode_keys_epilogue``, ``dsa_encode_queries_epilogue``,
+    ``dsa_rope``), with torch's per-op rounding in the row dtype, or, for
+    the queries of a bf16 batch, inside the GEMM's output stage.  The module
+    runs in its parameter dtype (fp32 or bf16); autocast's mixed flow is not
+    reproduced.
   * ``score_encoded`` (sidecar.py:89-107): ``[B,Q,H,D] x [B,K,D] -> [B,Q,K]``
     fp32, ``ReLU(q.k) * w`` summed over heads.
 
@@ -29,7 +32,6 @@ import math
 
 import torch
 from torch import nn
-from torch.nn import functional as F
 
 from . import _lib
 from .progressive_kernel import HEAD_DIM, HEADS
@@ -172,32 +174,62 @@ class LightningIndexerSidecar(nn.Module):
         nn.init.normal_(self.wk.weight, mean=0.0, std=self.hidden_size**-0.5)
         nn.init.normal_(self.weights_proj.weight, mean=0.0, std=self.hidden_size**-0.5)
 
-    def _project(self, hidden: torch.Tensor, weight: torch.Tensor, *, fp32: bool = False) -> torch.Tensor:
-        """A Linear without bias: ``hidden @ weight.T`` (bf16, or on
-        ``hidden.float()`` in fp32 for ``weights_proj``).  A decode step (at
-        most 16 tokens, bf16 hidden) streams the weights in the HIP projection
-        kernel (``dsa_project_rows``); larger batches use the platform GEMM."""
+    def _project(self, hidden: torch.Tensor, weight: torch.Tensor, *, fp32: bool = False,
+                 scale: float | None = None, positions: torch.Tensor | None = None) -> torch.Tensor:
+        """A Linear without bias (sidecar.py:55-58): ``hidden @ weight.T``, in
+        the weight's dtype (bf16, or fp32 on ``hidden.float()`` with ``fp32``
+        as weights_proj runs), times ``scale`` in fp32 when given.  A decode
+        step (at most 16 bf16 tokens) streams the weights in
+        ``dsa_project_rows``; larger batches, and fp32 modules, run the MFMA
+        GEMM ``dsa_project_gemm``, which with ``positions`` also applies
+        encode_queries' RoPE to every 128-dim head (bf16, rope_dim 64).
+        Inference only: no autograd graph is kept."""
 
-        tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
         kdim = hidden.shape[-1]
-        # The projection kernel takes no weight width: a weight that is not
-        # [features, kdim] goes to F.linear, which raises its shape error on
-        # the host before anything is launched.
-        fits = (hidden.is_cuda and 0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0
-                and not torch.is_grad_enabled() and weight.ndim == 2 and weight.shape[1] == kdim
-                and (weight.dtype == torch.float32 if fp32 else (weight.dtype == torch.bfloat16 and weight.shape[0] % 16 == 0)))
-        if not fits:
-            return F.linear(hidden.float(), weight.float()) if fp32 else F.linear(hidden, weight)
+        if weight.ndim != 2 or weight.shape[1] != kdim:
+            raise ValueError(f"hidden width {kdim} does not match the weight's {tuple(weight.shape)}")
+        if not hidden.is_cuda or not weight.is_cuda:
+            raise ValueError("HIP kernels require GPU tensors")
+        tokens = hidden.numel() // kdim if kdim else 0
+        features = weight.shape[0]
+        w = weight.detach()
+        if fp32 and w.dtype != torch.float32:
+            w = w.float()
+        if hidden.dtype not in (torch.bfloat16, torch.float32) or w.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("sidecar projections take bf16 or fp32 hidden states and weights")
+        if w.dtype == torch.bfloat16 and hidden.dtype != torch.bfloat16:
+            raise ValueError("a bf16 projection takes bf16 hidden states")
+        w = w.contiguous()
+        out_dtype = torch.float32 if w.dtype == torch.float32 else torch.bfloat16
+        lead = hidden.shape[:-1]
+        out = torch.empty((tokens, features), device=hidden.device, dtype=out_dtype)
+        if tokens == 0:
+            return out.reshape(*lead, features)
         flat = hidden.reshape(tokens, kdim)
         if flat.stride(-1) != 1 or flat.stride(0) % 8 or flat.data_ptr() % 16:
             flat = flat.contiguous()
-        w = weight.detach().contiguous()
-        features = w.shape[0]
-        out = torch.empty((tokens, features), device=hidden.device, dtype=torch.float32 if fp32 else torch.bfloat16)
-        _lib.call("dsa_project_rows", _lib.ptr(flat), flat.stride(0), tokens, _lib.ptr(w),
-                  _lib.DTYPE_F32 if fp32 else _lib.DTYPE_BF16, features, kdim, _lib.ptr(out), features,
-                  _lib.stream_of(flat))
-        return out.reshape(*hidden.shape[:-1], features)
+        stream = _lib.stream_of(flat)
+        decode = (tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0 and scale is None
+                  and positions is None and (w.dtype == torch.float32 or features % 16 == 0))
+        if decode:
+            _lib.call("dsa_project_rows", _lib.ptr(flat), flat.stride(0), tokens, _lib.ptr(w),
+                      _lib.DTYPE_F32 if w.dtype == torch.float32 else _lib.DTYPE_BF16, features, kdim, _lib.ptr(out),
+                      features, stream)
+            return out.reshape(*lead, features)
+        if kdim % 8 or features % 4:
+            raise ValueError("sidecar projections need a hidden width that is a multiple of 8 and a multiple of "
+                             "4 output features")
+        pos = None
+        ws = None
+        need = 0
+        if positions is not None:
+            pos = _token_positions(positions, lead, hidden.device)
+            need = int(_lib.query("dsa_project_gemm_workspace_bytes", tokens))
+            ws = _lib.workspace("rope_table", hidden.device, stream, need, zeroed=False)
+        _lib.call("dsa_project_gemm", _lib.ptr(flat), _row_dtype(flat), flat.stride(0), tokens, kdim, _lib.ptr(w),
+                  _row_dtype(w), features, _lib.ptr(out), features, float(1.0 if scale is None else scale),
+                  _lib.ptr(pos), float(self.rope_theta), _lib.ptr(ws), need, stream)
+        return out.reshape(*lead, features)
 
     def _project_pair(self, hidden: torch.Tensor, weight: torch.Tensor, weight_f32: torch.Tensor):
         """``(hidden @ weight.T, hidden.float() @ weight_f32.T)`` in one
@@ -208,7 +240,6 @@ class LightningIndexerSidecar(nn.Module):
         tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
         kdim = hidden.shape[-1]
         if not (hidden.is_cuda and 0 < tokens <= 16 and hidden.dtype == torch.bfloat16 and kdim % 32 == 0
-                and not torch.is_grad_enabled()
                 and weight.ndim == 2 and weight.shape[1] == kdim and weight_f32.ndim == 2 and weight_f32.shape[1] == kdim
                 and weight.dtype == torch.bfloat16 and weight.shape[0] % 16 == 0 and weight_f32.dtype == torch.float32):
             return None
@@ -279,6 +310,17 @@ class LightningIndexerSidecar(nn.Module):
 
         if not hidden.is_cuda:
             raise ValueError("HIP kernels require GPU tensors")
+        scale = float((self.heads * self.head_dim) ** -0.5)
+        tokens = hidden.numel() // hidden.shape[-1] if hidden.shape[-1] else 0
+        if (tokens > 16 and hidden.dtype == torch.bfloat16 and self.wq.weight.dtype == torch.bfloat16
+                and self.head_dim == 128 and self.rope_dim == 64 and (self.heads * self.head_dim) % 256 == 0
+                and hidden.shape[-1] % 8 == 0):
+            # The RoPE of every head in the wq GEMM's output stage and the
+            # head-weight scale in weights_proj's: no epilogue pass.
+            lead = hidden.shape[:-1]
+            queries = self._project(hidden, self.wq.weight, positions=positions)
+            weights = self._project(hidden, self.weights_proj.weight, fp32=True, scale=scale)
+            return queries.reshape(*lead, self.heads, self.head_dim), weights.reshape(*lead, self.heads)
         pair = self._project_pair(hidden, self.wq.weight, self.weights_proj.weight)
         if pair is None:
             proj = self._project(hidden, self.wq.weight)
@@ -294,7 +336,7 @@ class LightningIndexerSidecar(nn.Module):
         weights = torch.empty_like(flat_w)
         _lib.call(
             "dsa_encode_queries_epilogue", _lib.ptr(flat), _lib.ptr(flat_w), _lib.ptr(pos), self.rope_dim,
-            float(self.rope_theta), float((self.heads * self.head_dim) ** -0.5), _lib.ptr(queries),
+            float(self.rope_theta), scale, _lib.ptr(queries),
             _lib.ptr(weights), tokens, self.heads, self.head_dim, _row_dtype(flat), _lib.stream_of(flat),
         )
         return (queries.reshape(*tokens_shape, self.heads, self.head_dim), weights.reshape(*tokens_shape, self.heads))

@@ -673,6 +673,31 @@ int dsa_project_rows_pair(const void* hidden, int64_t hidden_stride, int64_t tok
                           const float* weight_f32, int64_t features_f32, float* out_f32, int64_t out_f32_stride,
                           void* stream);
 
+/* The sidecar's projections for batches of tokens (sidecar.py:55-58 wq /
+ * wk / weights_proj as used by encode_keys / encode_queries, :74-88), on
+ * MFMA: out[t][f] = sum_k hidden[t][k] * weight[f][k].  The reference's
+ * nn.Linear calls; dsa_project_rows serves a decode step of at most 16
+ * tokens, this entry point any token count.
+ *   weight_dtype DSA_DTYPE_BF16: hidden bf16, fp32 accumulation, out bf16
+ *     (rounded once).  With positions (int64 [tokens]) the output stage also
+ *     applies encode_queries' RoPE (sidecar.py:10-28, 81-82) to every
+ *     128-feature head: dims 0..63 rotated, dim d with d + 32, by
+ *     position * theta^(-d / 32), with cos / sin and every product and sum
+ *     rounded to bf16 as the encoder epilogues round them.  That needs
+ *     features a multiple of 256 and dsa_project_gemm_workspace_bytes(tokens)
+ *     bytes of workspace (the per-token rotation table); out_scale must be 1.
+ *   weight_dtype DSA_DTYPE_F32: hidden bf16 (widened exactly) or fp32, out
+ *     fp32 = (hidden . weight) * out_scale, one fp32 product: weights_proj on
+ *     hidden.float() times (heads * head_dim)^-0.5 in one pass.
+ * kdim a multiple of 8, features a multiple of 4,
+ * hidden_stride a multiple of 8 and out_stride of 4 elements; pointers
+ * 16-byte aligned; each of hidden, weight and out below 2 GiB. */
+int64_t dsa_project_gemm_workspace_bytes(int64_t tokens);
+int dsa_project_gemm(const void* hidden, int32_t hidden_dtype, int64_t hidden_stride, int64_t tokens, int64_t kdim,
+                     const void* weight, int32_t weight_dtype, int64_t features, void* out, int64_t out_stride,
+                     float out_scale, const int64_t* positions, float theta, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
 /* encode_keys after wk (sidecar.py:74-76 and 67-72): LayerNorm over dim
  * (fp32 weight/bias, biased variance, eps), then RoPE on the first rope_dim
  * dims, written to out row out_rows[t] (or t when out_rows is NULL) so that a

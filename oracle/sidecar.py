@@ -1,7 +1,7 @@
 """CPU restatement of the sidecar encoders (reference sidecar.py:10-88).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of the HIP
-encoder epilogues, never by the product path.
+encoder projections and epilogues, never by the product path.
 
 Follows, per op, the rounding torch applies in the tensor's dtype:
   * ``apply_noninterleaved_rope`` (sidecar.py:10-28): inv_freq = theta ^
@@ -11,14 +11,19 @@ Follows, per op, the rounding torch applies in the tensor's dtype:
     rounding is emulated on float32 values);
   * ``LayerNorm`` (sidecar.py:58, eps 1e-6): float32 mean, biased variance
     and (x - mean) * rstd * weight + bias, rounded once to the row dtype;
+  * ``project``: the bias-free Linear projections (sidecar.py:55-58) in
+    float64, rounded once to the Linear's dtype;
   * ``encode_keys`` (sidecar.py:74-76) = RoPE(LayerNorm(projection));
     ``encode_queries`` (sidecar.py:78-88) = RoPE on every head of the
     projection, head weights = projection * (heads * head_dim) ^ -0.5 (fp32).
 
 Pinned in tests/test_oracle_sidecar.py against closed forms: identity at
 position 0, the float64 rotation, preserved pair norms, rotation by -p
-undoing +p, LayerNorm's zero mean / unit variance, and bfloat16 rounding
-against torch's own cast.
+undoing +p, LayerNorm's zero mean / unit variance, bfloat16 rounding
+against torch's own cast, and for ``project`` an identity weight, a
+hand-computed product whose sum lands exactly between two bfloat16 values
+(ties to even), a non-square weight with distinct rows (a transposed
+operand fails it) and torch's own float64 matmul.
 """
 
 from __future__ import annotations
@@ -87,6 +92,24 @@ def layer_norm(x, weight, bias, eps: float = 1e-6, *, bf16: bool = False) -> np.
     rstd = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
     y = (centered * rstd * np.asarray(weight, np.float32) + np.asarray(bias, np.float32)).astype(np.float32)
     return round_bf16(y) if bf16 else y
+
+
+def project(hidden, weight, *, bf16: bool = False, scale: float | None = None) -> np.ndarray:
+    """A bias-free Linear (sidecar.py:55-58, the projections of :74-88):
+    hidden [..., k] @ weight [features, k].T computed in float64, then
+    rounded as torch stores the Linear's output: to float32, and then to
+    bfloat16 for a bf16 Linear (this double rounding differs from a single
+    one by a bfloat16 ulp only when the float32 value is a tie; the kernels
+    are held to one ulp), times ``scale`` as one float32 product when given
+    (weights_proj's head-weight scale)."""
+
+    exact = np.asarray(hidden, dtype=np.float64) @ np.asarray(weight, dtype=np.float64).T
+    out = exact.astype(np.float32)
+    if bf16:
+        return round_bf16(out)
+    if scale is not None:
+        out = (out * np.float32(scale)).astype(np.float32)
+    return out
 
 
 def encode_keys_epilogue(proj, ln_weight, ln_bias, positions, rope_dim: int, *, eps: float = 1e-6,

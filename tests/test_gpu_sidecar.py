@@ -110,8 +110,10 @@ def test_query_epilogue(device) -> None:
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_module_encoders_match_oracle(device, dtype) -> None:
-    """LightningIndexerSidecar's encoders against the oracle fed the module's
-    own projections (the platform GEMM's output), at the default shape."""
+    """LightningIndexerSidecar's encoders (18 tokens: the projection GEMM,
+    with the query RoPE fused in bf16) against the oracle: its float64
+    projections (the kernel's may differ by one bf16 rounding, or by fp32
+    accumulation order) through its epilogues."""
 
     torch.manual_seed(13)
     module = sidecar.LightningIndexerSidecar(hidden_size=512).to(device=device, dtype=dtype)
@@ -123,10 +125,11 @@ def test_module_encoders_match_oracle(device, dtype) -> None:
     with torch.no_grad():
         keys = module.encode_keys(hidden, pos)
         queries, weights = module.encode_queries(hidden, pos)
-        proj_k = torch.nn.functional.linear(hidden, module.wk.weight).float().cpu().numpy()
-        proj_q = torch.nn.functional.linear(hidden, module.wq.weight).float().cpu().numpy().reshape(2, 9, 64, 128)
-        proj_w = torch.nn.functional.linear(hidden.float(), module.weights_proj.weight.float()).cpu().numpy()
     bf16 = dtype == torch.bfloat16
+    h = hidden.float().cpu().numpy()
+    proj_k = O.project(h, module.wk.weight.detach().float().cpu().numpy(), bf16=bf16)
+    proj_q = O.project(h, module.wq.weight.detach().float().cpu().numpy(), bf16=bf16).reshape(2, 9, 64, 128)
+    proj_w = O.project(h, module.weights_proj.weight.detach().float().cpu().numpy())
     p = pos.cpu().numpy()
     want_k = O.encode_keys_epilogue(proj_k, module.k_norm.weight.detach().float().cpu().numpy(),
                                     module.k_norm.bias.detach().float().cpu().numpy(), p, 64, bf16=bf16)
@@ -135,7 +138,7 @@ def test_module_encoders_match_oracle(device, dtype) -> None:
     tol_k = _tol(want_k, p, bf16, 1) + np.abs(want_k) * (2.0**-7 if bf16 else 4e-6)
     assert np.all(np.abs(got_k - want_k) <= tol_k)
     assert np.all(np.abs(queries.float().cpu().numpy() - want_q) <= _tol(want_q, p, bf16, 2))
-    np.testing.assert_allclose(weights.cpu().numpy(), want_w, rtol=1e-6)
+    np.testing.assert_allclose(weights.cpu().numpy(), want_w, rtol=1e-5, atol=1e-6 * np.abs(want_w).max())
 
 
 def test_reference_toy_shapes(device) -> None:
@@ -208,8 +211,8 @@ def test_forward_scores_match_float64(device) -> None:
 @pytest.mark.parametrize("tokens", [1, 5, 16])
 def test_decode_projection_kernel_matches_float64(device, tokens) -> None:
     """dsa_project_rows (the decode-step projections): bf16 outputs within one
-    bf16 rounding of the float64 product, fp32 weights_proj to 1e-5; a batch
-    above 16 tokens takes the platform GEMM path with the same result."""
+    bf16 rounding of the float64 product, fp32 weights_proj to 1e-5 (larger
+    batches run dsa_project_gemm, tested in test_gpu_sidecar_gemm.py)."""
 
     torch.manual_seed(tokens)
     module = sidecar.LightningIndexerSidecar(hidden_size=2048).to(device=device, dtype=torch.bfloat16).eval()

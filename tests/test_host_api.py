@@ -111,11 +111,11 @@ def test_workspace_cache_grows_geometrically() -> None:
 
 
 def test_projection_width_mismatch_raises_on_the_host() -> None:
-    # The HIP projection kernel takes no weight width, so a hidden state whose
-    # width differs from the weight's must never reach it: F.linear raises.
+    # The HIP projection kernels take no weight width, so a hidden state whose
+    # width differs from the weight's must never reach them: the host raises.
     module = sidecar.LightningIndexerSidecar(hidden_size=64, heads=4, head_dim=32, rope_dim=8).to(torch.bfloat16)
     hidden = torch.zeros(2, 96, dtype=torch.bfloat16)
-    with torch.no_grad(), pytest.raises(RuntimeError):
+    with torch.no_grad(), pytest.raises(ValueError, match="does not match"):
         module._project(hidden, module.wq.weight)
     with torch.no_grad():
         assert module._project_pair(hidden, module.wq.weight, module.weights_proj.weight.float()) is None

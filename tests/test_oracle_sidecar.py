@@ -92,3 +92,29 @@ def test_layer_norm_closed_form() -> None:
 def test_query_weight_scale() -> None:
     _, weights = O.encode_queries_epilogue(np.zeros((2, 64, 128)), np.full((2, 64), 2.0), np.zeros(2), 64)
     np.testing.assert_allclose(weights, 2.0 / np.sqrt(64 * 128), rtol=1e-7)
+
+
+def test_project_identity_and_rounding() -> None:
+    # Identity weight: the projection is the input itself (bf16 values stay).
+    x = O.round_bf16(np.random.default_rng(0).standard_normal((5, 8)).astype(np.float32))
+    np.testing.assert_array_equal(O.project(x, np.eye(8), bf16=True), x)
+    # 1 + 2^-8 lies exactly between the bf16 values 1 and 1 + 2^-7: ties to
+    # even gives 1.  1 + 3 * 2^-8 lies between 1 + 2^-7 and 1 + 2^-6: even is
+    # 1 + 2^-6.  (Sums of products 1*1 + 2^-8*1 and 1*1 + 3*2^-8*1.)
+    h = np.array([[1.0, 2.0**-8], [1.0, 3 * 2.0**-8]], dtype=np.float32)
+    w = np.array([[1.0, 1.0]], dtype=np.float32)
+    assert O.project(h, w, bf16=True)[:, 0].tolist() == [1.0, 1.0 + 2.0**-6]
+    assert O.project(h, w)[:, 0].tolist() == [1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8]
+
+
+def test_project_orientation_and_scale() -> None:
+    # weight [features=3, k=2] with distinct rows: out[t, f] = sum_k h[t, k] w[f, k].
+    h = np.array([[1.0, 10.0], [2.0, 20.0]])
+    w = np.array([[1.0, 0.0], [0.0, 1.0], [3.0, -1.0]])
+    assert O.project(h, w).tolist() == [[1.0, 10.0, -7.0], [2.0, 20.0, -14.0]]
+    assert O.project(h, w, scale=0.5).tolist() == [[0.5, 5.0, -3.5], [1.0, 10.0, -7.0]]
+    rng = np.random.default_rng(3)
+    hb = rng.standard_normal((7, 64))
+    wb = rng.standard_normal((16, 64))
+    want = (torch.from_numpy(hb) @ torch.from_numpy(wb).T).float().numpy()
+    np.testing.assert_allclose(O.project(hb, wb), want, rtol=1e-6, atol=1e-6)
