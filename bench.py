@@ -60,6 +60,8 @@ def parse_args() -> argparse.Namespace:
                         "add 1 to it as the reference does (leaves the last-level cache full of dirty lines)")
     parser.add_argument("--c3-out", default=None, help="c3: also write the per-variant table (JSON) here")
     parser.add_argument("--c3-blocks", default=",".join(map(str, C3_BLOCKS)), help="c3: block sizes to replay")
+    parser.add_argument("--c3-wave1-blocks", default="64",
+                        help="c3: block sizes that also replay the dynamic scans at the reference's per-block refresh")
     parser.add_argument("--c3-gamma", default=",".join(map(str, C3_GAMMA_SIGMA)), help="c3: gamma_sigma values")
     parser.add_argument("--c3-refreshes", type=int, default=32,
                         help="c3: threshold refreshes per dynamic scan (the reference refreshes after every block)")
@@ -537,23 +539,40 @@ def run_c3(args) -> None:
                 variants.append({"kind": "replay", "block_size": bs, "method": method, "scan_order": order,
                                  "gamma_sigma": gamma_sigma, "wave": wave if method == "dynamic" else 0,
                                  **c3_summary(rows)})
+        # The reference's own schedule: the dynamic threshold refreshed after
+        # every block (wave 1, replay.py:218-219), for the block sizes asked.
+        wave1 = bs in [int(x) for x in args.c3_wave1_blocks.split(",") if x]
+        if wave1:
+            for gamma_sigma in gammas_run:
+                for method, order in (("dynamic", "address"), ("dynamic", "previous_hot")):
+                    rows = []
+                    for t in range(1, C3_STEPS):
+                        gamma = gamma_sigma * sigma[t]
+                        step, us = timed(lambda: temporal.temporal_step(
+                            queries[t], w, keys[:, : lengths[t]], prev_max[t - 1], lengths[t - 1], dense_topk[t - 1],
+                            gamma, block_size=bs, method=method, scan_order=order, wave=1))
+                        record(rows, t, bs, step, us, dynamic=True)
+                    variants.append({"kind": "replay", "block_size": bs, "method": method, "scan_order": order,
+                                     "gamma_sigma": gamma_sigma, "wave": 1, **c3_summary(rows)})
         # Certified bound (reference certified.py:18-62): U_b = previous block
         # max + the certified margin of the block (radius + fp32 rounding
         # allowance, dsa_certified_margins), computed per step from the two
         # queries and the keys; the margins are part of the timed step.
-        for method, order in (("static", "address"), ("dynamic", "previous_hot")):
+        certified_scans = [("static", "address", 0), ("dynamic", "previous_hot", wave)]
+        if wave1:
+            certified_scans.append(("dynamic", "previous_hot", 1))
+        for method, order, cwave in certified_scans:
             rows = []
             for t in range(1, C3_STEPS):
                 def certified_step():
                     margins = certified.certified_margins(queries[t], queries[t - 1], w, w, keys, lengths[t - 1], bs)
                     return temporal.temporal_step(
                         queries[t], w, keys[:, : lengths[t]], prev_max[t - 1], lengths[t - 1], dense_topk[t - 1], 0.0,
-                        block_size=bs, method=method, scan_order=order, wave=wave, block_margins=margins)
+                        block_size=bs, method=method, scan_order=order, wave=cwave or wave, block_margins=margins)
                 step, us = timed(certified_step)
                 record(rows, t, bs, step, us, dynamic=method == "dynamic")
             variants.append({"kind": "certified", "block_size": bs, "method": method, "scan_order": order,
-                             "gamma_sigma": "certified", "wave": wave if method == "dynamic" else 0,
-                             **c3_summary(rows)})
+                             "gamma_sigma": "certified", "wave": cwave, **c3_summary(rows)})
         # Own trajectory: the policy state is initialised from the dense step 0
         # and then only sees what its own pruned steps scored.
         own = (
@@ -883,7 +902,7 @@ def run_c5(args) -> None:
     print(json.dumps(line), flush=True)
 
 
-C5_TEMPORAL_GAMMA_SIGMA = (-0.25, 0.0, 0.25, 0.5, 1.0)
+C5_TEMPORAL_GAMMA_SIGMA = (-0.25, 0.0, 0.25, 0.5, 1.0, 2.0, 3.0, 4.0)
 C5_TEMPORAL_RHO = 0.95
 
 
@@ -900,12 +919,16 @@ def c5_temporal(q, w, sets, flush, device) -> dict:
     step's rounds load the blocks they score and then prune as well, so its
     key rows loaded exceed its keys scored) against the dense step's, the
     same from the keys scored (the reference's accounting), and Recall@K
-    against the dense top-2048."""
+    against the dense top-2048.  The dynamic scan also runs at the
+    reference's schedule, a refresh after every block (wave 1,
+    replay.py:218-219), and every scan also with the certified margins
+    (certified.py:18-48 over the fp8 keys, dsa_certified_margins, computed
+    inside the timed step) in place of gamma."""
 
     import numpy as np
     import torch
 
-    from dsa_amd import decode, temporal
+    from dsa_amd import certified, decode, temporal
 
     block = 64
     keys8, scales = sets[0]
@@ -927,40 +950,47 @@ def c5_temporal(q, w, sets, flush, device) -> dict:
     variants = []
     stream = torch.cuda.current_stream(device)
     # the dynamic scan refreshes after the largest wave the step's merge allows
-    # (k + wave * block <= 8192: 96 blocks, 22 refreshes per scan)
-    for method, order, wave in (("static", "address", 0), ("dynamic", "previous_hot", (8192 - TOPK) // block)):
-        for gs in C5_TEMPORAL_GAMMA_SIGMA:
-            gamma = gs * sigma
+    # (k + wave * block <= 8192: 96 blocks, 22 refreshes per scan), or after
+    # every block (the reference's schedule)
+    scans = (("static", "address", 0), ("dynamic", "previous_hot", (8192 - TOPK) // block),
+             ("dynamic", "previous_hot", 1))
+    for (method, order, wave), gs in [(m, g) for m in scans for g in (*C5_TEMPORAL_GAMMA_SIGMA, "certified")]:
+        gamma = 0.0 if gs == "certified" else gs * sigma
 
-            def run():
-                return temporal.temporal_step(q_now, w, keys8, prev_max, prev_len, prev_top, gamma, block_size=block,
-                                              method=method, scan_order=order, wave=max(wave, 1), key_scales=scales)
+        def run():
+            margins = None
+            if gs == "certified":
+                margins = certified.certified_margins(q_now, q_prev, w, w, keys8, prev_len, block,
+                                                      key_scales=scales)
+            return temporal.temporal_step(q_now, w, keys8, prev_max, prev_len, prev_top, gamma, block_size=block,
+                                          method=method, scan_order=order, wave=max(wave, 1), key_scales=scales,
+                                          block_margins=margins)
 
-            times = []
-            for it in range(12):
-                flush()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                step = run()
-                e1.record(stream)
-                torch.cuda.synchronize()
-                if it >= 2:
-                    times.append(e0.elapsed_time(e1) * 1e3)
-            qk = step.qk_scored.double().cpu().numpy()
-            # key rows loaded: a dynamic step's rounds also load the blocks they
-            # score and then prune; a static step loads the keys it scores
-            loaded = (temporal.keys_loaded(step, block) if method == "dynamic" else step.qk_scored).double().cpu().numpy()
-            hits = truth.gather(1, step.topk).sum(dim=1).cpu().numpy()
-            read = loaded * 128 + (C5_LENGTH // 128) * 4 + nb * 8
-            scored_read = qk * 128 + (C5_LENGTH // 128) * 4 + nb * 8
-            variants.append({
-                "method": method, "scan_order": order, "wave": wave, "gamma_sigma": gs,
-                "us_per_step": float(np.median(times)),
-                "key_bytes_skipped": float(np.mean(1.0 - read / dense_bytes)),
-                "key_bytes_skipped_scored": float(np.mean(1.0 - scored_read / dense_bytes)),
-                "qk_reduction": float(np.mean(1.0 - qk / C5_LENGTH)),
-                "recall": float(np.mean(hits / TOPK)),
-            })
+        times = []
+        for it in range(12):
+            flush()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            step = run()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            if it >= 2:
+                times.append(e0.elapsed_time(e1) * 1e3)
+        qk = step.qk_scored.double().cpu().numpy()
+        # key rows loaded: a dynamic step's rounds also load the blocks they
+        # score and then prune; a static step loads the keys it scores
+        loaded = (temporal.keys_loaded(step, block) if method == "dynamic" else step.qk_scored).double().cpu().numpy()
+        hits = truth.gather(1, step.topk).sum(dim=1).cpu().numpy()
+        read = loaded * 128 + (C5_LENGTH // 128) * 4 + nb * 8
+        scored_read = qk * 128 + (C5_LENGTH // 128) * 4 + nb * 8
+        variants.append({
+            "method": method, "scan_order": order, "wave": wave, "gamma_sigma": gs,
+            "us_per_step": float(np.median(times)),
+            "key_bytes_skipped": float(np.mean(1.0 - read / dense_bytes)),
+            "key_bytes_skipped_scored": float(np.mean(1.0 - scored_read / dense_bytes)),
+            "qk_reduction": float(np.mean(1.0 - qk / C5_LENGTH)),
+            "recall": float(np.mean(hits / TOPK)),
+        })
     eligible = [v for v in variants if v["recall"] >= 0.999]
     best = max(eligible, key=lambda v: v["key_bytes_skipped"]) if eligible else None
     return {"block_size": block, "rho": C5_TEMPORAL_RHO, "variants": variants, "best_at_recall_0.999": best}

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libdsa_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -76,7 +76,7 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _p,
     ],
     "dsa_temporal_keys_loaded": [_p, _i64, _i64, _i64, _i32, _p, _p],
-    "dsa_certified_margins": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p],
+    "dsa_certified_margins": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p],
     "dsa_approx_step": [
         _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64,
         _i32, _i32, _i32, _p, _i64, _p,

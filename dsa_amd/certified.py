@@ -11,6 +11,8 @@ reference's float64 value.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -88,6 +90,8 @@ def certified_margins(
     keys: torch.Tensor,
     previous_length: int,
     block_size: int,
+    *,
+    key_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Certified per-block margins ``[B, ceil(previous_length / block_size)]``
     (float64) of a temporal step over shared-key caches.
@@ -97,8 +101,9 @@ def certified_margins(
     rounding of both steps' scores; with the previous step's dense block
     maxima, ``temporal_step(..., block_margins=...)`` then keeps every key of
     the dense top-k.  queries ``[B, 64, 128]`` and keys ``[B, C, 128]``
-    (bf16/fp16, the first ``previous_length`` keys are summarised), weights
-    ``[B, 64]``.
+    (bf16/fp16, the first ``previous_length`` keys are summarised; or fp8
+    e4m3fn keys with ``key_scales`` ``[B, ceil(C / 128)]`` and bf16 queries, a
+    key's norm then being scale * its fp8 norm), weights ``[B, 64]``.
     """
 
     tensors = (q_now, q_prev, w_now, w_prev, keys)
@@ -111,7 +116,13 @@ def certified_margins(
         raise ValueError("weights must be [batch,64]")
     if keys.ndim != 3 or keys.shape[0] != batch or keys.shape[2] != 128:
         raise ValueError("keys must be [batch,C,128]")
-    if keys.dtype not in (torch.bfloat16, torch.float16) or q_now.dtype != keys.dtype or q_prev.dtype != keys.dtype:
+    if keys.dtype == torch.float8_e4m3fn:
+        if q_now.dtype != torch.bfloat16 or q_prev.dtype != torch.bfloat16:
+            raise ValueError("fp8 keys are summarised against BF16 queries")
+        if key_scales is None or key_scales.shape != (batch, math.ceil(keys.shape[1] / 128)):
+            raise ValueError("fp8 keys need key_scales [batch, ceil(capacity/128)]")
+        key_scales = key_scales.to(device=keys.device, dtype=torch.float32).contiguous()
+    elif keys.dtype not in (torch.bfloat16, torch.float16) or q_now.dtype != keys.dtype or q_prev.dtype != keys.dtype:
         raise ValueError("queries and keys must share FP16/BF16 dtype")
     if not 0 < previous_length <= keys.shape[1]:
         raise ValueError("previous_length outside the key buffer")
@@ -125,7 +136,8 @@ def certified_margins(
     qn, qp = q_now.contiguous(), q_prev.contiguous()
     wn, wp = w_now.to(torch.float32).contiguous(), w_prev.to(torch.float32).contiguous()
     _lib.call(
-        "dsa_certified_margins", _lib.ptr(qn), _lib.ptr(qp), _lib.ptr(wn), _lib.ptr(wp), _lib.ptr(keys), key_stride,
+        "dsa_certified_margins", _lib.ptr(qn), _lib.ptr(qp), _lib.ptr(wn), _lib.ptr(wp), _lib.ptr(keys),
+        _lib.ptr(key_scales), key_stride,
         batch, previous_length, block_size, _lib.dtype_code(keys.dtype), _lib.ptr(out), _lib.stream_of(keys),
     )
     return out

@@ -169,12 +169,17 @@ __device__ __forceinline__ double sum_squares8(uint4 v, int dtype, double acc) {
   return acc;
 }
 
+// kFp8: keys are fp8 e4m3fn rows (128 bytes) with one fp32 scale per 128
+// keys; a key's norm is scale * ||k8|| (the key the scoring kernel scores is
+// scale * k8), the fp8 values being exact in float64.
+template <bool kFp8>
 __global__ __launch_bounds__(kMarginThreads) void certified_margins_kernel(const uint16_t* q_now, const uint16_t* q_prev,
                                                                            const float* w_now, const float* w_prev,
-                                                                           const uint16_t* keys, int64_t key_stride,
-                                                                           int prev_length, int block_size,
-                                                                           int blocks_per_row, int blocks_per_wg,
-                                                                           int q_dtype, double* margins) {
+                                                                           const void* keys, const float* scales,
+                                                                           int64_t key_stride, int prev_length,
+                                                                           int block_size, int blocks_per_row,
+                                                                           int blocks_per_wg, int q_dtype,
+                                                                           double* margins) {
   __shared__ double s_radius[kHeads];
   __shared__ double s_slack[kHeads];
   __shared__ double s_total[2];
@@ -228,23 +233,32 @@ __global__ __launch_bounds__(kMarginThreads) void certified_margins_kernel(const
   const int count = blocks_per_wg * block_size;
   constexpr int kRowsPerStep = kMarginThreads / 16;  // 16 key rows per workgroup step
   constexpr int kSteps = 8;                           // steps whose loads are in flight together
-  const uint4* key_row0 = reinterpret_cast<const uint4*>(keys + (size_t)row * key_stride * kHeadDim);
+  const size_t row_bytes = kFp8 ? kHeadDim : kHeadDim * 2;
+  const uint8_t* key_row0 = static_cast<const uint8_t*>(keys) + (size_t)row * key_stride * row_bytes;
+  const float* row_scales = kFp8 ? scales + (size_t)row * ((key_stride + 127) / 128) : nullptr;
   __syncthreads();
   for (int i0 = 0; i0 < count; i0 += kRowsPerStep * kSteps) {
-    uint4 v[kSteps];
+    uint4 v[kSteps];  // eight key values per lane (bf16 / fp16, or fp8 widened exactly to bf16)
+    float sc[kSteps];
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
-      const int key = first + min(i0 + kRowsPerStep * j + (tid >> 4), count - 1);
-      v[j] = key_row0[(size_t)min(key, prev_length - 1) * (kHeadDim / 8) + sub];
+      const int key = min(first + min(i0 + kRowsPerStep * j + (tid >> 4), count - 1), prev_length - 1);
+      if constexpr (kFp8) {
+        v[j] = fp8x8_to_bf16x8(reinterpret_cast<const uint2*>(key_row0 + (size_t)key * row_bytes)[sub]);
+        sc[j] = row_scales[key >> 7];
+      } else {
+        v[j] = reinterpret_cast<const uint4*>(key_row0 + (size_t)key * row_bytes)[sub];
+        sc[j] = 1.f;
+      }
     }
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
       const int i = i0 + kRowsPerStep * j + (tid >> 4);
-      double acc = sum_squares8(v[j], q_dtype, 0.0);
+      double acc = sum_squares8(v[j], kFp8 ? (int)kBF16 : q_dtype, 0.0);
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) acc += __shfl_xor(acc, off, kWave);
       const bool mine = sub == 0 && i < count;
-      const double norm = first + i < prev_length ? sqrt(acc) : 0.0;
+      const double norm = first + i < prev_length ? sqrt(acc) * (double)sc[j] : 0.0;
       if (mine)
         __hip_atomic_fetch_max(&s_block_max[i / block_size], (unsigned long long)__double_as_longlong(norm),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -281,24 +295,34 @@ __global__ __launch_bounds__(kMarginThreads) void certified_margins_kernel(const
 using namespace dsa;
 
 extern "C" int dsa_certified_margins(const void* q_now, const void* q_prev, const float* w_now, const float* w_prev,
-                                     const void* keys, int64_t key_stride, int64_t batch, int64_t prev_length,
-                                     int32_t block_size, int32_t key_dtype, double* margins, void* stream) {
+                                     const void* keys, const float* key_scales, int64_t key_stride, int64_t batch,
+                                     int64_t prev_length, int32_t block_size, int32_t key_dtype, double* margins,
+                                     void* stream) {
   DSA_REQUIRE(q_now && q_prev && w_now && w_prev && keys && margins, "null pointer argument");
+  DSA_REQUIRE(key_dtype != kFP8E4M3 || key_scales, "fp8 keys need key_scales");
   DSA_REQUIRE(batch > 0 && batch <= 65535, "batch %lld out of range", (long long)batch);
   DSA_REQUIRE(prev_length > 0 && prev_length <= key_stride && prev_length < (int64_t(1) << 31),
               "prev_length %lld invalid", (long long)prev_length);
   DSA_REQUIRE(block_size > 0, "block_size must be positive");
-  DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16, "certified margins take bf16/fp16 queries and keys");
+  DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16 || key_dtype == kFP8E4M3,
+              "certified margins take bf16/fp16 keys (queries of the same dtype) or fp8 keys (bf16 queries)");
   DSA_REQUIRE(block_size <= kMaxMarginBlock, "block_size %d above %d", block_size, kMaxMarginBlock);
   DSA_REQUIRE(reinterpret_cast<uintptr_t>(keys) % 16 == 0 && reinterpret_cast<uintptr_t>(q_now) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(q_prev) % 16 == 0,
               "queries and keys must be 16-byte aligned");
   const int64_t blocks = (prev_length + block_size - 1) / block_size;
   const int per_wg = block_size < kMarginThreads ? kMarginThreads / block_size : 1;
-  hipLaunchKernelGGL(certified_margins_kernel, dim3((unsigned)((blocks + per_wg - 1) / per_wg), (unsigned)batch),
-                     dim3(kMarginThreads), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q_now),
-                     static_cast<const uint16_t*>(q_prev), w_now, w_prev, static_cast<const uint16_t*>(keys),
-                     key_stride, (int)prev_length, (int)block_size, (int)blocks, per_wg, (int)key_dtype, margins);
+  const dim3 grid((unsigned)((blocks + per_wg - 1) / per_wg), (unsigned)batch);
+  auto go = [&](auto kernel, int q_dtype) {
+    hipLaunchKernelGGL(kernel, grid, dim3(kMarginThreads), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(q_now), static_cast<const uint16_t*>(q_prev), w_now, w_prev, keys,
+                       key_scales, key_stride, (int)prev_length, (int)block_size, (int)blocks, per_wg, q_dtype,
+                       margins);
+  };
+  if (key_dtype == kFP8E4M3)
+    go(certified_margins_kernel<true>, (int)kBF16);
+  else
+    go(certified_margins_kernel<false>, (int)key_dtype);
   return check_launch("certified_margins_kernel");
 }
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 2
+#define DSA_ABI_VERSION 3
 
 #define DSA_STATUS_OK 0
 #define DSA_STATUS_INVALID_ARGUMENT 1
@@ -630,18 +630,21 @@ int dsa_temporal_score_radius(const double* q_now, const double* q_prev, const d
  * block maxima, U_b = prev max + margin_b bounds every current score of
  * block b as the scoring kernels compute it: a step pruning with these
  * margins keeps every key of the dense top-k.  q_now, q_prev [batch, 64, 128]
- * and keys [batch, key_stride, 128] in key_dtype (bf16/fp16), w_now, w_prev
- * [batch, 64] fp32; margins [batch, ceil(prev_length / block_size)] float64
- * over the first prev_length keys, block_size <= 4096; queries and keys
- * 16-byte aligned.  Computed in float64. */
+ * and keys [batch, key_stride, 128] in key_dtype (bf16/fp16), or fp8 e4m3fn
+ * keys with key_scales [batch, ceil(key_stride / 128)] fp32 and bf16 queries
+ * (a key's norm is then scale * ||k8||, the key the scoring kernel scores);
+ * w_now, w_prev [batch, 64] fp32; margins [batch, ceil(prev_length /
+ * block_size)] float64 over the first prev_length keys, block_size <= 4096;
+ * queries and keys 16-byte aligned.  Computed in float64. */
 int dsa_certified_margins(const void* q_now, const void* q_prev, const float* w_now, const float* w_prev,
-                          const void* keys, int64_t key_stride, int64_t batch, int64_t prev_length,
-                          int32_t block_size, int32_t key_dtype, double* margins, void* stream);
+                          const void* keys, const float* key_scales, int64_t key_stride, int64_t batch,
+                          int64_t prev_length, int32_t block_size, int32_t key_dtype, double* margins, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sidecar encoder epilogues (sidecar.py:10-88).  The projections wq / wk /
- * weights_proj are plain GEMMs done by the caller's BLAS; these entry points
- * run everything after them in one pass per row.  dtype codes: DSA_DTYPE_F32
+ * weights_proj run in dsa_project_rows / dsa_project_rows_pair (a decode
+ * step) or dsa_project_gemm (below); these entry points run everything after
+ * them in one pass per row.  dtype codes: DSA_DTYPE_F32
  * or DSA_DTYPE_BF16; arithmetic follows torch's per-op rounding in that dtype.
  * ------------------------------------------------------------------------ */
 

@@ -79,3 +79,52 @@ def test_certified_step_keeps_the_dense_topk(device, block, method, order, wave,
     print(f"  pruned {pruned} of {step.evaluated_blocks.numel()} blocks", flush=True)
     if must_prune:
         assert pruned > 0, "a slow drift leaves blocks below the threshold: the case must prune"
+
+
+def _fp8(keys: torch.Tensor):
+    """Keys quantised as C5's: fp8 e4m3fn with scale = max |k| / 448 per 128 keys."""
+
+    raw = keys.float()
+    batch, length, _ = raw.shape
+    blocks = math.ceil(length / 128)
+    pad = torch.zeros(batch, blocks * 128, 128)
+    pad[:, :length] = raw
+    scales = pad.reshape(batch, blocks, 128 * 128).abs().amax(dim=2) / 448
+    keys8 = (raw / scales.repeat_interleave(128, dim=1)[:, :length, None]).to(torch.float8_e4m3fn)
+    return keys8, scales
+
+
+def test_fp8_margins_match_oracle_and_keep_the_dense_topk(device) -> None:
+    # fp8 keys (C5's format): the margins are never below the float64 oracle
+    # on the dequantised keys (scale * k8), and a certified static and dynamic
+    # step over the fp8 keys keep the dense top-k exactly.
+    print("certified fp8 keys", flush=True)
+    batch, prev_length, length, k, block = 2, 8192, 8195, 256, 64
+    q_prev, q_now, w, keys = drifting(batch, prev_length, length, 0.99999, seed=5)
+    keys8, scales = _fp8(keys)
+    q_prev, q_now, w = q_prev.to(device), q_now.to(device), w.to(device)
+    keys8, scales = keys8.to(device), scales.to(device)
+    margins = certified.certified_margins(q_now, q_prev, w, w, keys8, prev_length, block, key_scales=scales)
+    # scale * k8 in float64 (exact: a float32 product would round each key value)
+    deq = (keys8.double() * scales.double().repeat_interleave(128, dim=1)[:, :length, None]).cpu().numpy()
+    got = margins.cpu().numpy()
+    for b in range(batch):
+        want = C.certified_margins(q_now[b].float().cpu().numpy(), q_prev[b].float().cpu().numpy(), w[b].cpu().numpy(),
+                                   w[b].cpu().numpy(), deq[b, :prev_length], block)
+        assert np.all(got[b] >= want) and np.all(got[b] <= want * (1 + 2.0**-34)), b
+    prev_scales = scales[:, : math.ceil(prev_length / 128)].contiguous()
+    prev_topk, prev_scores = decode.indexer_topk(q_prev, w, keys8[:, :prev_length].contiguous(), k,
+                                                 key_scales=prev_scales, return_scores=True)
+    dense_topk, dense = decode.indexer_topk(q_now, w, keys8, k, key_scales=scales, return_scores=True)
+    change = (dense[:, :prev_length] - prev_scores).abs().double()
+    blocks = math.ceil(prev_length / block)
+    pad = torch.zeros(batch, blocks * block, device=device, dtype=torch.float64)
+    pad[:, :prev_length] = change
+    assert bool((pad.reshape(batch, blocks, block).amax(dim=2) <= margins).all())
+    for method, order, wave in (("static", "address", 1), ("dynamic", "previous_hot", 16)):
+        step = temporal.temporal_step(q_now, w, keys8, temporal.block_max(prev_scores, block), prev_length, prev_topk,
+                                      0.0, block_size=block, method=method, scan_order=order, wave=wave,
+                                      key_scales=scales, block_margins=margins)
+        assert torch.equal(step.topk, dense_topk), method
+        print(f"  {method}: pruned {int((~step.evaluated_blocks).sum())} of {step.evaluated_blocks.numel()} blocks",
+              flush=True)
