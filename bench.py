@@ -262,11 +262,16 @@ def main() -> None:
     # kernels record HIP events at their own start and end (hipExtLaunchKernel),
     # on the stream they run on, so each interval is the kernels' execution
     # alone, as rocprofv3's kernel trace reports it.
+    # The launches queue behind a hold on the stream (a bounded spin kernel
+    # sized to outlast their issue), so that they run back to back as in the
+    # graph replays instead of paced by the host's calls.
     timed = max(20, min(args.steps, 100))
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(4 * timed)]
     for m in marks:  # the events must exist before a launch records them
         m.record(stream)
     torch.cuda.synchronize()
+    hold = stream_hold(stream, 2.0 + 0.06 * timed)
+    hold()
     for i in range(timed):
         keys = key_sets[i % ROTATIONS]
         _lib.call(
@@ -282,6 +287,10 @@ def main() -> None:
     torch.cuda.synchronize()
     score_ms = [marks[4 * i].elapsed_time(marks[4 * i + 1]) for i in range(timed)]
     topk_ms = [marks[4 * i + 2].elapsed_time(marks[4 * i + 3]) for i in range(timed)]
+    # idle time between one step's selection and the next step's scoring: near
+    # zero when the launches ran back to back behind the hold
+    gaps = sorted(marks[4 * i + 3].elapsed_time(marks[4 * i + 4]) * 1e3 for i in range(timed - 1))
+    gap_us = gaps[len(gaps) // 2]
 
     # Algorithmic bytes per step, the measurement contract's figure: every key
     # row once (256 B), the query block and weights once per sequence, and
@@ -308,6 +317,7 @@ def main() -> None:
     for m in smarks:
         m.record(stream)
     torch.cuda.synchronize()
+    hold()
     for i in range(timed):
         _lib.call("dsa_stream_read", key_sets[i % ROTATIONS].data_ptr(), key_bytes, 256, sink.data_ptr(),
                   stream.cuda_stream, smarks[2 * i].cuda_event, smarks[2 * i + 1].cuda_event)
@@ -367,7 +377,9 @@ def main() -> None:
             "hbm_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "wall_s": round(wall, 3),
             "timing": f"value: HIP events around {replays} replays of a graph of {ROTATIONS} steps; "
-            f"score_us/topk_us: HIP events recorded by the kernels themselves (hipExtLaunchKernel) over {timed} eager steps",
+            f"score_us/topk_us: HIP events recorded by the kernels themselves (hipExtLaunchKernel) over {timed} eager steps "
+            "queued behind a hold on the stream, so they run back to back",
+            "launch_gap_us": round(gap_us, 3),
         },
         "recall_at_k": recall,
         "cpu_baseline": baseline,
@@ -701,6 +713,26 @@ def write_table(args, line: dict, rows: list) -> None:
 
 
 FLUSH_BYTES = 512 * 1024 * 1024  # twice the 256 MB last-level cache
+
+
+def stream_hold(stream, ms: float):
+    """A callable that occupies `stream` for about `ms` milliseconds with a
+    bounded spin kernel (torch.cuda._sleep), so that launches issued behind it
+    queue up and then run back to back.  The spin's cycles per millisecond are
+    measured once here."""
+
+    import torch
+
+    probe = 2_000_000
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(probe // 10)  # first launch outside the measurement
+    e0.record(stream)
+    torch.cuda._sleep(probe)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per_ms = probe / max(e0.elapsed_time(e1), 1e-3)
+    cycles = int(min(per_ms * ms, 50 * probe))
+    return lambda: torch.cuda._sleep(cycles)
 
 
 def make_flush(args, device):
