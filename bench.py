@@ -761,9 +761,11 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 def run_c4(args) -> None:
     """T=4096 queries x L=4096 causal keys per layer, 8
     independent layers, bf16 ~ N(0,1)/sqrt(128) queries and keys, fp32
-    weights ~ N(0,1/64); per layer the causal score matrix (dsa_score_queries)
-    and every query's top-512 over its visible keys (dsa_topk with row
-    lengths).  MFMA work = 64 heads x 128 dims x 2 FLOP per visible pair."""
+    weights ~ N(0,1/64); per layer the causal score matrix and every
+    query's top-512 over its visible keys in one launch
+    (dsa_score_queries_topk); the scoring alone (dsa_score_queries) and the
+    separate select (dsa_topk with row lengths) are timed beside it.  MFMA
+    work = 64 heads x 128 dims x 2 FLOP per visible pair."""
 
     import torch
 
@@ -793,10 +795,17 @@ def run_c4(args) -> None:
         _lib.call("dsa_topk", scores.data_ptr(), None, C4_T, C4_T, C4_T, visible.data_ptr(), C4_TOPK, 0,
                   idx.data_ptr(), None, torch.cuda.current_stream().cuda_stream)
 
+    def fused(i):
+        q, w, keys = layers[i]
+        _lib.call("dsa_score_queries_topk", q.data_ptr(), 64 * 128, w.data_ptr(), 64, keys.data_ptr(), C4_T, C4_T,
+                  scores.data_ptr(), C4_T, C4_T, C4_T, 0, _lib.DTYPE_BF16, C4_TOPK, idx.data_ptr(), None, C4_TOPK,
+                  torch.cuda.current_stream().cuda_stream)
+
     flush = make_flush(args, device)
     score_ms = graph_times(score, C4_LAYERS, flush, 5, 40, device)
     select_ms = graph_times(select, C4_LAYERS, flush, 5, 40, device)
-    step_ms = graph_times(lambda i: (score(i), select(i)), C4_LAYERS, flush, 5, 40, device)
+    split_ms = graph_times(lambda i: (score(i), select(i)), C4_LAYERS, flush, 5, 40, device)
+    step_ms = graph_times(fused, C4_LAYERS, flush, 5, 40, device)
     pairs = C4_T * (C4_T + 1) // 2
     flops = pairs * 64 * 128 * 2
     st = time_stats(step_ms)
@@ -821,7 +830,10 @@ def run_c4(args) -> None:
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "prefill_scores_kernel<bf16> (multi-query, causal, dsa_score_queries)",
                      "kernel_median_us": sc["median_us"], "flops": flops},
-        "layer": {"step": st, "score": sc, "topk": time_stats(select_ms)},
+        "layer": {"step": st, "score": sc, "topk": time_stats(select_ms), "split_step": time_stats(split_ms),
+                  "topk_share_us": round(st["median_us"] - sc["median_us"], 3)},
+        "step_kernel": "dsa_score_queries_topk: the scoring kernel with each query's top-512 selected by its wave "
+                       "after its row is stored (split_step: dsa_score_queries then dsa_topk)",
         "timing": f"HIP events around one layer's launches, 512 MiB {args.flush} flush before each, median over 40",
     }
     write_table(args, line, [])

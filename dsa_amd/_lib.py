@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libdsa_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -40,6 +40,9 @@ _SIGNATURES: dict[str, list] = {
     "dsa_score_queries": [
         _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64,
         _i64, _i32, _p,
+    ],
+    "dsa_score_queries_topk": [
+        _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _i64, _p,
     ],
     "dsa_route_heads": [_p, _i64, _i64, _i64, _i32, _p, _p, _p],
     "dsa_score_topk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],

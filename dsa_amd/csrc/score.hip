@@ -61,6 +61,11 @@ struct DenseArgs {
   uint64_t* lists;
   uint32_t* list_meta;  // [sequences][kMaxListChunks][2]: length, lowest bin listed
   int32_t list_quota;
+  // Top-k of every score row inside the prefill kernel (kTopK only).
+  int32_t topk;
+  int64_t* topk_idx;  // [sequences][topk_stride]
+  float* topk_val;    // nullable, same layout
+  int64_t topk_stride;
 };
 
 // The key rows a wave streams: the key set's base, its valid bytes (below
@@ -278,6 +283,224 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
 constexpr int kPrefillQueries = 8;
 constexpr int kPrefillRow = 272;
 
+// ---------------------------------------------------------------------------
+// Exact top-k of one query's score row at the end of the prefill kernel, with
+// stable_topk's set (metrics.py:9-22: every score above the k-th largest, ties
+// at it to the lower index, -0.0 equal to +0.0) written in ascending index
+// order.  One wave per row of at most kTopKRowMax keys, after the wave's own
+// score stores have completed: it reads the row back (lane l holds keys
+// 256 j + 4 l + c), counts the valid scores into kTopKBins LDS bins spaced
+// linearly between the row's minimum and maximum, and finds the bin of the
+// k-th largest.  Inside that bin the cut is resolved by ranking its keys
+// against each other when there are at most 64 of them, else by a radix over
+// their order-preserving keys (digits of 10, 10, 10 and 2 bits).  The cut is
+// a (value, index) pair of the (value desc, index asc) order; a last pass
+// writes every valid key at or above it.  Rows with at most k valid keys
+// return all of them, padded with index -1 / value -inf.
+// ---------------------------------------------------------------------------
+constexpr int kTopKRowMax = 4096;
+constexpr int kTopKBins = 1024;
+// the bins, then 64 candidates (values, indices), then 4 spare words
+constexpr int kTopKScratch = kTopKBins + 2 * kWave + 4;
+
+// Completes this wave's LDS operations before the next ones are issued (a
+// wave's own LDS traffic, so no barrier).
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ void zero_wave_bins(uint32_t* bins, int lane) {
+  uint4* b4 = reinterpret_cast<uint4*>(bins);
+#pragma unroll
+  for (int q = 0; q < kTopKBins / 4 / kWave; ++q) b4[lane + kWave * q] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Key of register slot e of a lane in the read-back row, and the linear bin
+// of a value.
+__device__ __forceinline__ int topk_key(int e, int lane) { return 256 * (e >> 2) + 4 * lane + (e & 3); }
+__device__ __forceinline__ int topk_bin(float x, float lo, float scale) {
+  return min(kTopKBins - 1, (int)((x - lo) * scale));
+}
+
+// Every pass below walks the row in blocks of 256 keys (one float4 per lane):
+// blocks wholly past the visible keys are skipped (a wave-uniform branch),
+// and within the others each key is tested against the visible count.
+#define DSA_TOPK_BLOCKS(BODY)                                  \
+  _Pragma("unroll") for (int j = 0; j < 16; ++j) {             \
+    if (256 * j < vis) {                                       \
+      constexpr bool kPartial = true;                          \
+      BODY                                                     \
+    }                                                          \
+  }
+
+__device__ __forceinline__ void prefill_topk_row(BufferRsrc row, int vis, int k, int64_t* out_idx, float* out_val,
+                                                 uint32_t* scratch, int lane) {
+  float v[64];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    if (256 * j < vis) q = buffer_load_16(row, (uint32_t)(256 * j + 4 * lane) * 4u);
+    v[4 * j + 0] = __uint_as_float(q.x);
+    v[4 * j + 1] = __uint_as_float(q.y);
+    v[4 * j + 2] = __uint_as_float(q.z);
+    v[4 * j + 3] = __uint_as_float(q.w);
+  }
+  // key 256 j + 4 lane + t of the last block is visible iff t < tail
+  const int tail = vis - 4 * lane;
+  const bool all = vis <= k;
+  float tv = 0.f;  // the cut: key i with value x is kept iff x > tv or (x == tv and i <= ti)
+  int ti = -1;
+  if (!all) {
+    float lo = __builtin_inff(), hi = -__builtin_inff();
+    DSA_TOPK_BLOCKS(
+_Pragma("unroll")
+      for (int t = 0; t < 4; ++t) {
+        const float x = v[4 * j + t];
+        const bool ok = !kPartial || 256 * j + t < tail;
+        lo = ok && x < lo ? x : lo;
+        hi = ok && x > hi ? x : hi;
+      })
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    // Monotone binning: bin(x) > bin(y) implies x > y.  A single value, or a
+    // span that overflows, puts every key in bin 0 (the radix below resolves it).
+    float scale = (float)kTopKBins / (hi - lo);
+    if (!(scale <= 3.0e38f)) scale = 0.f;
+    zero_wave_bins(scratch, lane);
+    wave_lds_fence();
+    // Keys past the visible ones count into a spare word after the candidates.
+    DSA_TOPK_BLOCKS(
+_Pragma("unroll")
+      for (int t = 0; t < 4; ++t) {
+        int at = topk_bin(v[4 * j + t], lo, scale);
+        if (kPartial) at = 256 * j + t < tail ? at : kTopKScratch - 1;
+        __hip_atomic_fetch_add(&scratch[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      })
+    wave_lds_fence();
+    const Locate loc = wave_locate<kTopKBins / kWave>(scratch, (uint32_t)k, false);
+    const int cut_bin = (int)loc.digit;
+    if (loc.count <= (uint32_t)kWave) {
+      // The cut bin's keys, listed in index order, each ranked against all.
+      float* cval = reinterpret_cast<float*>(scratch + kTopKBins);
+      int* cidx = reinterpret_cast<int*>(scratch + kTopKBins + kWave);
+      uint32_t n = 0;
+      DSA_TOPK_BLOCKS(
+        bool c[4];
+        uint32_t cnt = 0;
+_Pragma("unroll")
+        for (int t = 0; t < 4; ++t) {
+          c[t] = (!kPartial || 256 * j + t < tail) && topk_bin(v[4 * j + t], lo, scale) == cut_bin;
+          cnt += c[t] ? 1u : 0u;
+        }
+        if (__ballot(cnt != 0) != 0) {
+          const uint32_t incl = wave_incl_scan(cnt);
+          uint32_t pos = n + incl - cnt;
+_Pragma("unroll")
+          for (int t = 0; t < 4; ++t)
+            if (c[t] && pos < (uint32_t)kWave) {
+              cval[pos] = v[4 * j + t];
+              cidx[pos] = topk_key(4 * j + t, lane);
+              ++pos;
+            }
+          n += __builtin_amdgcn_readlane(incl, kWave - 1);
+        })
+      wave_lds_fence();
+      float cv = 0.f;
+      int ci = 0;
+      uint32_t rank = 0;
+      if ((uint32_t)lane < n) {
+        cv = cval[lane];
+        ci = cidx[lane];
+        for (uint32_t m = 0; m < n; ++m) {
+          const float ov = cval[m];
+          const int oi = cidx[m];
+          rank += (ov > cv || (ov == cv && oi < ci)) ? 1u : 0u;
+        }
+      }
+      const uint64_t hit = __ballot((uint32_t)lane < n && rank == loc.rem - 1);
+      const int owner = (int)__builtin_ctzll(hit);
+      tv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv), owner));
+      ti = __builtin_amdgcn_readlane(ci, owner);
+    } else {
+      // Radix over the order keys of the cut bin's keys, most significant
+      // digit first; then the want-th of the keys equal to the cut, by index.
+      uint32_t prefix = 0, pmask = 0, want = loc.rem;
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const int shift = pass < 3 ? 22 - 10 * pass : 0;
+        const uint32_t dmask = pass < 3 ? 1023u : 3u;
+        wave_lds_fence();
+        zero_wave_bins(scratch, lane);
+        wave_lds_fence();
+        DSA_TOPK_BLOCKS(
+_Pragma("unroll")
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t o = float_to_ordered(v[4 * j + t]);
+            if ((!kPartial || 256 * j + t < tail) && topk_bin(v[4 * j + t], lo, scale) == cut_bin &&
+                (o & pmask) == prefix)
+              __hip_atomic_fetch_add(&scratch[(o >> shift) & dmask], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+          })
+        wave_lds_fence();
+        const Locate d = wave_locate<kTopKBins / kWave>(scratch, want, false);
+        prefix |= d.digit << shift;
+        pmask |= dmask << shift;
+        want = d.rem;
+      }
+      uint32_t seen = 0;
+      DSA_TOPK_BLOCKS(
+        bool eq[4];
+        uint32_t cnt = 0;
+_Pragma("unroll")
+        for (int t = 0; t < 4; ++t) {
+          eq[t] = (!kPartial || 256 * j + t < tail) && float_to_ordered(v[4 * j + t]) == prefix;
+          cnt += eq[t] ? 1u : 0u;
+        }
+        const uint32_t incl = wave_incl_scan(cnt);
+        const uint32_t total = __builtin_amdgcn_readlane(incl, kWave - 1);
+        if (ti < 0 && seen + total >= want) {
+          const uint32_t before = seen + incl - cnt;
+          const uint64_t m = __ballot(before < want && want <= seen + incl);
+          const int owner = (int)__builtin_ctzll(m);
+          uint32_t r = want - before;  // meaningful on the owner lane
+          int found = 0;
+_Pragma("unroll")
+          for (int t = 0; t < 4; ++t)
+            if (eq[t] && r != 0) {
+              if (--r == 0) found = topk_key(4 * j + t, lane);
+            }
+          ti = __builtin_amdgcn_readlane(found, owner);
+        }
+        seen += total;)
+      tv = ordered_to_float(prefix);
+    }
+  }
+  uint32_t base = 0;
+  DSA_TOPK_BLOCKS(
+    bool s[4];
+    uint32_t cnt = 0;
+_Pragma("unroll")
+    for (int t = 0; t < 4; ++t) {
+      const int key = topk_key(4 * j + t, lane);
+      const float x = v[4 * j + t];
+      s[t] = (!kPartial || 256 * j + t < tail) && (all || x > tv || (x == tv && key <= ti));
+      cnt += s[t] ? 1u : 0u;
+    }
+    const uint32_t incl = wave_incl_scan(cnt);
+    uint32_t pos = base + incl - cnt;
+_Pragma("unroll")
+    for (int t = 0; t < 4; ++t)
+      if (s[t] && pos < (uint32_t)k) {
+        out_idx[pos] = topk_key(4 * j + t, lane);
+        if (out_val) out_val[pos] = v[4 * j + t];
+        ++pos;
+      }
+    base += __builtin_amdgcn_readlane(incl, kWave - 1);)
+  for (int p = (int)base + lane; p < k; p += kWave) {
+    out_idx[p] = -1;
+    if (out_val) out_val[p] = -__builtin_inff();
+  }
+}
+#undef DSA_TOPK_BLOCKS
+
 // The unit loop is software-pipelined across tiles and units: step t issues
 // the MFMAs of tile t and the ReLU / weight work of tile t - 1 (tile 3 of the
 // previous unit at step 0), interleaved by scheduling groups, while the next
@@ -294,7 +517,7 @@ __device__ __forceinline__ void mfma_valu_interleave() {
   }
 }
 
-template <class Tag>
+template <class Tag, bool kTopK>
 __global__ __launch_bounds__(64 * kPrefillQueries) void prefill_scores_kernel(DenseArgs a, int32_t qblocks,
                                                                             int32_t keysets) {
   constexpr int kThreads = 64 * kPrefillQueries;
@@ -407,6 +630,17 @@ __global__ __launch_bounds__(64 * kPrefillQueries) void prefill_scores_kernel(De
   // Keys past this workgroup's units are invisible to all of its queries.
   if (active)
     for (int key = units * 64 + lane; key < L; key += 64) orow[key] = -__builtin_inff();
+  if constexpr (kTopK) {
+    __shared__ __align__(16) uint32_t topk_scratch[kPrefillQueries][kTopKScratch];
+    if (active) {
+      // The row is read back by the wave that stored it, once its stores
+      // have completed.
+      __builtin_amdgcn_s_waitcnt(0);
+      const int64_t at = seq * a.topk_stride;
+      prefill_topk_row(orsrc, vis, a.topk, a.topk_idx + at, a.topk_val ? a.topk_val + at : nullptr,
+                       topk_scratch[wave], lane);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -659,7 +893,7 @@ int launch_dense(const DenseArgs& a, int64_t sequences, hipStream_t stream) {
       const int64_t keysets = sequences / a.queries_per_keyset;
       const int64_t qblocks = (a.queries_per_keyset + kPrefillQueries - 1) / kPrefillQueries;
       if (keysets * a.queries_per_keyset == sequences && qblocks * keysets <= 0x7fffffffLL) {
-        hipLaunchKernelGGL((prefill_scores_kernel<Tag>), dim3((unsigned)(qblocks * keysets)),
+        hipLaunchKernelGGL((prefill_scores_kernel<Tag, false>), dim3((unsigned)(qblocks * keysets)),
                            dim3(64 * kPrefillQueries), 0, stream, a, (int32_t)qblocks, (int32_t)keysets);
         return check_launch("prefill_scores_kernel");
       }
@@ -764,6 +998,59 @@ extern "C" int dsa_score_queries(const void* queries, int64_t q_stride, const fl
       return fail(DSA_STATUS_INVALID_ARGUMENT, "dsa_score_queries takes fp16/bf16/fp8 keys (got %d)",
                   key_dtype);
   }
+}
+
+extern "C" int dsa_score_queries_topk(const void* queries, int64_t q_stride, const float* weights,
+                                      int64_t w_stride, const void* keys, int64_t key_stride,
+                                      int64_t queries_per_keyset, float* out, int64_t out_stride,
+                                      int64_t sequences, int64_t length, int64_t causal_offset,
+                                      int32_t key_dtype, int32_t k, int64_t* out_indices, float* out_values,
+                                      int64_t topk_stride, void* stream) {
+  DSA_REQUIRE(queries && weights && keys && out && out_indices, "null pointer argument");
+  DSA_REQUIRE(key_dtype == kBF16 || key_dtype == kF16, "dsa_score_queries_topk takes fp16/bf16 keys (got %d)",
+              key_dtype);
+  DSA_REQUIRE(length > 0 && length <= kTopKRowMax, "length %lld outside [1, %d]", (long long)length,
+              kTopKRowMax);
+  DSA_REQUIRE(queries_per_keyset >= kPrefillQueries && queries_per_keyset < (int64_t(1) << 31),
+              "queries_per_keyset %lld outside [%d, 2^31)", (long long)queries_per_keyset, kPrefillQueries);
+  DSA_REQUIRE(sequences > 0 && sequences % queries_per_keyset == 0,
+              "sequences must be a positive multiple of queries_per_keyset");
+  DSA_REQUIRE(k > 0, "k must be positive (got %d)", k);
+  DSA_REQUIRE(topk_stride >= k, "topk_stride < k");
+  DSA_REQUIRE(causal_offset < (int64_t(1) << 30), "causal_offset out of range");
+  DSA_REQUIRE(out_stride >= length, "out_stride < length");
+  DSA_REQUIRE(reinterpret_cast<uintptr_t>(queries) % 16 == 0 && reinterpret_cast<uintptr_t>(keys) % 16 == 0,
+              "queries and keys must be 16-byte aligned");
+  DSA_REQUIRE(q_stride % 8 == 0, "q_stride must keep 16-byte alignment");
+  const int64_t keysets = sequences / queries_per_keyset;
+  const int64_t qblocks = (queries_per_keyset + kPrefillQueries - 1) / kPrefillQueries;
+  DSA_REQUIRE(qblocks * keysets <= 0x7fffffffLL, "problem too large");
+  DenseArgs a = {};
+  a.q = static_cast<const uint16_t*>(queries);
+  a.q_stride = q_stride;
+  a.w = weights;
+  a.w_stride = w_stride;
+  a.head_count = kHeads;
+  a.keys = static_cast<const uint8_t*>(keys);
+  a.key_stride = key_stride;
+  a.queries_per_keyset = (int32_t)queries_per_keyset;
+  a.out = out;
+  a.out_stride = out_stride;
+  a.length = (int32_t)length;
+  a.causal_offset = causal_offset < 0 ? -1 : (int32_t)causal_offset;
+  a.topk = k;
+  a.topk_idx = out_indices;
+  a.topk_val = out_values;
+  a.topk_stride = topk_stride;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(qblocks * keysets));
+  if (key_dtype == kBF16)
+    hipLaunchKernelGGL((prefill_scores_kernel<Bf16Tag, true>), grid, dim3(64 * kPrefillQueries), 0, s, a,
+                       (int32_t)qblocks, (int32_t)keysets);
+  else
+    hipLaunchKernelGGL((prefill_scores_kernel<F16Tag, true>), grid, dim3(64 * kPrefillQueries), 0, s, a,
+                       (int32_t)qblocks, (int32_t)keysets);
+  return check_launch("prefill_scores_kernel");
 }
 
 extern "C" int dsa_full_scores(const void* queries, const float* weights, const void* keys,

@@ -99,6 +99,67 @@ def score_encoded(
     return out
 
 
+def score_encoded_topk(
+    queries: torch.Tensor,
+    weights: torch.Tensor,
+    keys: torch.Tensor,
+    k: int,
+    *,
+    causal: bool = False,
+    causal_offset: int | None = None,
+    return_values: bool = False,
+):
+    """``score_encoded`` (reference sidecar.py:89-107) and every query's exact
+    top-k of its visible keys (``stable_topk``, metrics.py:9-22, in ascending
+    index order) in one launch (``dsa_score_queries_topk``).
+
+    Returns ``(scores [B, Q, K] fp32, indices [B, Q, k] int64)``, plus the
+    selected values ``[B, Q, k]`` with ``return_values``.  A query with fewer
+    than ``k`` visible keys returns all of them, padded with -1 (values -inf).
+    Needs fp16/bf16 queries and keys, at least 8 queries per key set and at
+    most 4096 keys.
+    """
+
+    if queries.ndim != 4 or weights.shape != queries.shape[:-1]:
+        raise ValueError("queries must be [batch,query,heads,dim]")
+    if keys.ndim != 3 or keys.shape[0] != queries.shape[0]:
+        raise ValueError("keys must be [batch,key,dim]")
+    batch, num_queries, heads, dim = queries.shape
+    length = keys.shape[1]
+    if heads != HEADS or dim != HEAD_DIM or keys.shape[2] != HEAD_DIM:
+        raise ValueError("expected 64 heads x 128 dims")
+    if not (queries.is_cuda and weights.is_cuda and keys.is_cuda):
+        raise ValueError("HIP kernels require GPU tensors")
+    if queries.dtype not in (torch.float16, torch.bfloat16) or keys.dtype != queries.dtype:
+        raise ValueError("queries and keys must share FP16/BF16 dtype")
+    if k <= 0:
+        raise ValueError("k must be positive")
+    if not 1 <= length <= 4096:
+        raise ValueError("the fused top-k takes 1..4096 keys per key set")
+    if num_queries < 8:
+        raise ValueError("the fused top-k takes at least 8 queries per key set")
+    offset = -1
+    if causal:
+        offset = length - num_queries if causal_offset is None else int(causal_offset)
+        if offset < 0:
+            raise ValueError("causal_offset must be non-negative")
+    queries = queries.contiguous()
+    keys = keys.contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    scores = torch.empty((batch, num_queries, length), device=keys.device, dtype=torch.float32)
+    indices = torch.empty((batch, num_queries, k), device=keys.device, dtype=torch.int64)
+    values = torch.empty((batch, num_queries, k), device=keys.device, dtype=torch.float32) if return_values else None
+    _lib.call(
+        "dsa_score_queries_topk",
+        _lib.ptr(queries), HEADS * HEAD_DIM, _lib.ptr(weights), HEADS, _lib.ptr(keys), length, num_queries,
+        _lib.ptr(scores), length, batch * num_queries, length, offset, _lib.dtype_code(keys.dtype), int(k),
+        _lib.ptr(indices), _lib.ptr(values), int(k), _lib.stream_of(keys),
+    )
+    if return_values:
+        return scores, indices, values
+    return scores, indices
+
+
 def _row_dtype(t: torch.Tensor) -> int:
     try:
         return _ROW_DTYPES[t.dtype]

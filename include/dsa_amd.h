@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 3
+#define DSA_ABI_VERSION 4
 
 #define DSA_STATUS_OK 0
 #define DSA_STATUS_INVALID_ARGUMENT 1
@@ -89,6 +89,30 @@ int dsa_score_queries(const void* queries, int64_t q_stride, const float* weight
                       int64_t queries_per_keyset, const float* key_scales, int64_t scale_stride,
                       float* out, int64_t out_stride, int64_t sequences, int64_t length,
                       int64_t causal_offset, int32_t key_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Prefill indexer step in one launch: the scores of dsa_score_queries (all
+ * 64 heads, fp16/bf16 keys) and, per query, the exact top-k of its visible
+ * keys with stable_topk's set (metrics.py:9-22), in ascending index order as
+ * dsa_topk with sorted == 0.
+ *
+ * Replaces sidecar.py:89-107 (score_encoded over Q queries per key set)
+ * followed by a per-query stable top-k of the score rows (metrics.py:9-22).
+ *   out            fp32 [sequences, out_stride]: the scores (masked -inf)
+ *   out_indices    int64 [sequences, topk_stride]: row s's top-k key ids;
+ *                  a query with fewer than k visible keys returns all of
+ *                  them, padded with -1
+ *   out_values     fp32, same layout, nullable (padding -inf)
+ * Each workgroup scores eight consecutive queries of one key set; each
+ * query's wave then selects from its own row.  Limits: length <= 4096,
+ * queries_per_keyset >= 8 and sequences a multiple of it, k >= 1,
+ * topk_stride >= k; other arguments as dsa_score_queries.
+ * ------------------------------------------------------------------------ */
+int dsa_score_queries_topk(const void* queries, int64_t q_stride, const float* weights, int64_t w_stride,
+                           const void* keys, int64_t key_stride, int64_t queries_per_keyset, float* out,
+                           int64_t out_stride, int64_t sequences, int64_t length, int64_t causal_offset,
+                           int32_t key_dtype, int32_t k, int64_t* out_indices, float* out_values,
+                           int64_t topk_stride, void* stream);
 
 /* Head routing: per row of weights [rows, heads] (heads <= 64) the `width`
  * head ids with the largest |w| (positive_only == 0) or max(w, 0)
