@@ -123,13 +123,16 @@ __device__ __forceinline__ void dense_compute_unit(const uint4 (&qa)[M][4], cons
 }
 
 // The streaming part of dense_scores_kernel: query block into registers, then
-// the two-buffer unit loop.
-template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists>
+// the two-buffer unit loop.  `after_issue` runs once the query tiles and the
+// first units' loads are in flight (the workgroup's barrier, for the kernels
+// that clear an LDS histogram first), so that its wait overlaps them.
+template <class Tag, class KF, int M, bool kGather, bool kHist, bool kLists, class AfterIssue>
 __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int u_first, int u_stride,
                                              int64_t seq, int valid, int L, int lane, int r, int g,
                                              const uint8_t* key_base, uint32_t key_bytes, BufferRsrc out,
                                              const float* scales,
-                                             uint32_t* hist, float* chunk_scores, int chunk_base) {
+                                             uint32_t* hist, float* chunk_scores, int chunk_base,
+                                             AfterIssue after_issue) {
   uint4 qa[M][4];
   float wr[M][4];
   if constexpr (kGather) {
@@ -153,6 +156,7 @@ __device__ __forceinline__ void dense_stream(const DenseArgs& a, int count, int 
 #pragma unroll
   for (int s = 0; s < NB - 1; ++s)
     dense_load_unit<KF>(ks, min(u_first + u_stride * s, u_last), buf[s], scales, L, scale[s]);
+  after_issue();
   for (int i = 0; i < count; i += NB) {
     const int u = u_first + u_stride * i;
 #pragma unroll
@@ -232,13 +236,20 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
   if constexpr (kHist) {
 #pragma unroll
     for (int j = 0; j < kSelectBins / kThreads; ++j) hist[threadIdx.x + kThreads * j] = 0;
-    __syncthreads();
+    // The cleared histogram is published by one barrier per wave, taken after
+    // the wave's first loads are issued (a wave with no units takes it here).
+    auto publish = [] {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+    };
     const int chunk_keys = a.units_per_wg * 64;
     const int chunk_base = chunk * chunk_keys;
     if (count > 0)
       dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g,
                                                        key_base, key_bytes, out, scales, hist, chunk_scores,
-                                                       chunk_base);
+                                                       chunk_base, publish);
+    else
+      publish();
     __syncthreads();
     if constexpr (kLists) {
       // The chunk's list: every valid key whose bin is at least the bin of
@@ -266,7 +277,7 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
   }
   if (count == 0) return;
   dense_stream<Tag, KF, M, kGather, kHist, kLists>(a, count, u_first, u_stride, seq, valid, L, lane, r, g, key_base,
-                                                   key_bytes, out, scales, hist, chunk_scores, 0);
+                                                   key_bytes, out, scales, hist, chunk_scores, 0, [] {});
 }
 
 
