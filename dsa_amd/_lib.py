@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libdsa_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -45,6 +45,10 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _i64, _p,
     ],
     "dsa_route_heads": [_p, _i64, _i64, _i64, _i32, _p, _p, _p],
+    "dsa_pair_moments": [_p, _p, _i32, _i64, _p, _p, _p],
+    "dsa_average_ranks": [_p, _i32, _p, _i64, _p, _p],
+    "dsa_index_overlap": [_p, _p, _i64, _p, _p],
+    "dsa_block_streaks": [_p, _p, _i64, _p, _p, _p, _p, _p],
     "dsa_score_topk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _i64, _p],
     "dsa_score_topk_noalloc": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p],
     "dsa_score_hist": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p],

@@ -5,9 +5,10 @@ cli.py:42-103): it finds ``.npz`` traces under ``--trace-roots``, replays each
 with the sweep of the ``replay`` section of a YAML config (``k_values``,
 ``block_sizes``, ``gamma_sigma``, ``key_bytes``, ``metadata_bytes_per_block``,
 optional ``calibrated_margins`` per layer, or a ``--margin-file``), and writes
-``replay_rows.csv`` and the aggregated ``replay_summary.csv`` to
-``--output``.  The replay runs in the HIP temporal kernels
-(:mod:`dsa_amd.replay`).  The reference's statistics tables, graphs, hardware
+``temporal_stats.csv``, ``block_stats.csv`` (reference cli.py:17-20,55-58,
+replay.py:403-474), ``replay_rows.csv`` and the aggregated
+``replay_summary.csv`` to ``--output``.  The replay and the statistics run in
+the HIP kernels (:mod:`dsa_amd.replay`).  The reference's graphs, hardware
 extrapolation and verdict report are analysis presentation and stay with the
 reference's tools, which read the traces and CSVs written here.
 
@@ -41,7 +42,7 @@ def _trace_paths(roots: list[Path]) -> list[Path]:
 def analyze(args: argparse.Namespace) -> None:
     import pandas as pd
 
-    from .replay import aggregate_rows, replay_trace_rows
+    from .replay import aggregate_rows, block_temporal_stats, replay_trace_rows, temporal_stats
     from .trace import load_trace
 
     config = yaml.safe_load(args.config.read_text(encoding="utf-8")) if args.config else {}
@@ -56,8 +57,11 @@ def analyze(args: argparse.Namespace) -> None:
     block_sizes = replay.get("block_sizes", [16, 32, 64, 128])
     gammas = replay.get("gamma_sigma", [0.0, 0.25, 0.5, 1.0])
     rows: list[dict] = []
+    temporal_frames, block_frames = [], []
     for path in _trace_paths(args.trace_roots):
         trace = load_trace(path)
+        temporal_frames.append(temporal_stats(trace, k_values))
+        block_frames.append(block_temporal_stats(trace, block_sizes, k_values))
         margins = replay.get("calibrated_margins", {}).get(str(trace.layer))
         if margins:
             margins = {int(b): float(v) for b, v in margins.items()}
@@ -68,6 +72,8 @@ def analyze(args: argparse.Namespace) -> None:
         ))
         print(f"replayed {path} ({trace.scores.shape[0] - 1} transitions)", flush=True)
     args.output.mkdir(parents=True, exist_ok=True)
+    pd.concat(temporal_frames, ignore_index=True).to_csv(args.output / "temporal_stats.csv", index=False)
+    pd.concat(block_frames, ignore_index=True).to_csv(args.output / "block_stats.csv", index=False)
     frame = pd.DataFrame(rows)
     frame.to_csv(args.output / "replay_rows.csv", index=False)
     aggregate_rows(frame).to_csv(args.output / "replay_summary.csv", index=False)

@@ -321,3 +321,170 @@ def aggregate_rows(frame):
         metadata_bytes=("metadata_bytes", "median"),
         net_byte_reduction=("net_byte_reduction", "median"),
     )
+
+
+# ---------------------------------------------------------------------------
+# Statistics tables of consecutive rows (reference replay.py:403-474).
+# ---------------------------------------------------------------------------
+def _moments(x: torch.Tensor, y: torch.Tensor, abs_delta: torch.Tensor | None = None) -> list[float]:
+    """dsa_pair_moments: [mean x, mean y, Sxx, Syy, Sxy, mean d, Sdd]."""
+
+    out = torch.empty(7, device=x.device, dtype=torch.float64)
+    code = _lib.DTYPE_F64 if x.dtype == torch.float64 else _lib.DTYPE_F32
+    _lib.call("dsa_pair_moments", _lib.ptr(x), _lib.ptr(y), code, x.numel(), _lib.ptr(out), _lib.ptr(abs_delta),
+              _lib.stream_of(x))
+    return out.tolist()
+
+
+def _pearson(m: list[float], n: int) -> float:
+    """Pearson's r from the moments (reference metrics.py:40-47: NaN for
+    fewer than two values or a constant row)."""
+
+    sxx, syy, sxy = m[2], m[3], m[4]
+    if n < 2 or sxx == 0.0 or syy == 0.0:
+        return math.nan
+    return float(min(1.0, max(-1.0, sxy / math.sqrt(sxx * syy))))
+
+
+def _sorted_desc(row: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The row sorted by (value desc, index asc) with its keys, on the GPU."""
+
+    from .metrics import _exact_topk
+
+    order, values = _exact_topk(row.reshape(1, -1), row.numel(), sorted=True, return_values=True)
+    return order[0], values[0]
+
+
+def _ranks(row: torch.Tensor) -> torch.Tensor:
+    order, values = _sorted_desc(row)
+    ranks = torch.empty(row.numel(), device=row.device, dtype=torch.float64)
+    code = _lib.DTYPE_F64 if values.dtype == torch.float64 else _lib.DTYPE_F32
+    _lib.call("dsa_average_ranks", _lib.ptr(values), code, _lib.ptr(order), row.numel(), _lib.ptr(ranks),
+              _lib.stream_of(row))
+    return ranks
+
+
+def _percentiles(sorted_desc: torch.Tensor, qs) -> list[float]:
+    """numpy's linear percentiles of a row sorted descending, with numpy's
+    arithmetic: the quantile q / 100, the virtual index (n - 1) q, its
+    fraction and the two-sided lerp are all in the row's own precision
+    (float32 rows give float32 percentiles).  Only the two neighbours of each
+    virtual index are read back."""
+
+    dt = np.float32 if sorted_desc.dtype == torch.float32 else np.float64
+    n = sorted_desc.numel()
+    plan = []
+    for q in qs:
+        qf = dt(q) / dt(100)
+        virtual = dt(n - 1) * qf
+        if virtual >= n - 1:
+            lo = hi = n - 1
+        elif virtual < 0:
+            lo = hi = 0
+        else:
+            lo = int(np.floor(virtual))
+            hi = lo + 1
+        plan.append((lo, hi, dt(virtual - dt(np.floor(virtual)))))
+    picks = torch.tensor([n - 1 - i for lo, hi, _ in plan for i in (lo, hi)], device=sorted_desc.device)
+    vals = sorted_desc.index_select(0, picks).cpu().numpy().astype(dt)
+    out = []
+    for j, (_, _, t) in enumerate(plan):
+        a, b = vals[2 * j], vals[2 * j + 1]
+        diff = dt(b - a)
+        out.append(float(dt(b - diff * (dt(1) - t)) if t >= 0.5 else dt(a + diff * t)))
+    return out
+
+
+def temporal_stats(trace: ScoreTrace, k_values):
+    """The reference's ``temporal_stats`` (replay.py:403-428) on the GPU: per
+    transition and k, the Pearson and Spearman correlations of consecutive
+    rows, the drift's mean, std and 99th percentile of |drift|, and the top-k
+    overlap.  Returns a pandas DataFrame with the reference's columns."""
+
+    import pandas as pd
+
+    _lib.load()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    records = []
+    for step in range(1, trace.scores.shape[0]):
+        prev_h, cur_h = trace.row(step - 1), trace.row(step)
+        n = min(prev_h.size, cur_h.size)
+        prev = torch.from_numpy(prev_h[:n]).to(dev)
+        cur = torch.from_numpy(cur_h[:n]).to(dev)
+        abs_delta = torch.empty(n, device=dev, dtype=torch.float32)
+        m = _moments(prev, cur, abs_delta)
+        rank_m = _moments(_ranks(prev), _ranks(cur))
+        p99 = _percentiles(_sorted_desc(abs_delta)[1], [99])[0]
+        base = {
+            "step": step, "layer": trace.layer, "workload": trace.workload, "prompt_id": trace.prompt_id,
+            "context_length": int(cur_h.size),
+            "score_pearson": _pearson(m, n),
+            "score_spearman": _pearson(rank_m, n),
+            "delta_mean": m[5],
+            "delta_std": math.sqrt(m[6] / n),
+            "delta_p99_abs": p99,
+        }
+        for k in k_values:
+            if k > n:
+                continue
+            a = device_topk(prev.reshape(1, -1), k, sorted=False)[0]
+            b = device_topk(cur.reshape(1, -1), k, sorted=False)[0]
+            hits = torch.zeros(1, device=dev, dtype=torch.int32)
+            _lib.call("dsa_index_overlap", _lib.ptr(a), _lib.ptr(b), k, _lib.ptr(hits), _lib.stream_of(a))
+            records.append({**base, "k": k, "topk_overlap": int(hits.item()) / k})
+    return pd.DataFrame(records)
+
+
+def block_temporal_stats(trace: ScoreTrace, block_sizes, k_values):
+    """The reference's ``block_temporal_stats`` (replay.py:431-474) on the
+    GPU: per transition, block size and k, the drift of the block maxima
+    (mean, 5th / 50th / 95th percentiles) and the fraction of blocks whose
+    maximum stayed below the current k-th largest score for at least 1, 2, 4
+    and 8 consecutive steps.  Returns a pandas DataFrame with the reference's
+    columns."""
+
+    import pandas as pd
+
+    _lib.load()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    capacity = int(trace.scores.shape[1])
+    streaks: dict[tuple[int, int], torch.Tensor] = {}
+    records = []
+    for step in range(1, trace.scores.shape[0]):
+        prev_h, cur_h = trace.row(step - 1), trace.row(step)
+        n = min(prev_h.size, cur_h.size)
+        prev = torch.from_numpy(prev_h[:n]).to(dev).reshape(1, -1)
+        cur = torch.from_numpy(cur_h[:n]).to(dev).reshape(1, -1)
+        kth = {k: device_topk(cur, k, sorted=True, return_values=True)[1][0] for k in k_values if k <= n}
+        for bs in block_sizes:
+            pm = block_max(prev, bs)[0]
+            cm = block_max(cur, bs)[0]
+            nb = cm.numel()
+            for k in k_values:
+                if k > n:
+                    continue
+                state = streaks.setdefault((bs, k), torch.zeros(-(-capacity // bs), device=dev, dtype=torch.int32))
+                delta = torch.empty(nb, device=dev, dtype=torch.float64)
+                counts = torch.zeros(4, device=dev, dtype=torch.int32)
+                _lib.call("dsa_block_streaks", _lib.ptr(pm), _lib.ptr(cm), nb, kth[k].data_ptr() + 4 * (k - 1),
+                          _lib.ptr(state), _lib.ptr(delta), _lib.ptr(counts), _lib.stream_of(cm))
+                dm = _moments(delta, delta)
+                sorted_delta = _sorted_desc(delta)[1]
+                p5, p95 = _percentiles(sorted_delta, [5, 95])
+                mid = sorted_delta.index_select(0, torch.tensor(sorted({(nb - 1) // 2, nb // 2}), device=dev))
+                median = float(mid.double().mean().item()) if mid.numel() == 2 else float(mid[0].item())
+                c = counts.tolist()
+                records.append({
+                    "step": step, "layer": trace.layer, "workload": trace.workload, "prompt_id": trace.prompt_id,
+                    "context_length": int(cur_h.size), "k": k, "block_size": bs,
+                    "topk_threshold": float(kth[k][k - 1].item()),
+                    "delta_max_mean": dm[0],
+                    "delta_max_p5": p5,
+                    "delta_max_median": median,
+                    "delta_max_p95": p95,
+                    "cold_fraction_1": c[0] / nb,
+                    "cold_fraction_2": c[1] / nb,
+                    "cold_fraction_4": c[2] / nb,
+                    "cold_fraction_8": c[3] / nb,
+                })
+    return pd.DataFrame(records)

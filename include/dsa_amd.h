@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 4
+#define DSA_ABI_VERSION 5
 
 #define DSA_STATUS_OK 0
 #define DSA_STATUS_INVALID_ARGUMENT 1
@@ -113,6 +113,39 @@ int dsa_score_queries_topk(const void* queries, int64_t q_stride, const float* w
                            int64_t out_stride, int64_t sequences, int64_t length, int64_t causal_offset,
                            int32_t key_dtype, int32_t k, int64_t* out_indices, float* out_values,
                            int64_t topk_stride, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Statistics of consecutive score rows, for the replay analysis tables
+ * (replay.py:403-474, temporal_stats / block_temporal_stats).  dtype codes:
+ * DSA_DTYPE_F32 or DSA_DTYPE_F64.
+ * ------------------------------------------------------------------------ */
+
+/* x, y [n]: out[7] float64 = mean x, mean y, sum (x-mx)^2, sum (y-my)^2,
+ * sum (x-mx)(y-my), mean d, sum (d-md)^2 with d = y - x (subtracted in the
+ * rows' precision, as numpy subtracts float32 rows); abs_delta [n] in the
+ * rows' dtype receives |d| (nullable).  Pearson's r (metrics.py:40-47) and
+ * the drift's mean and std (replay.py:417-419) follow from out. */
+int dsa_pair_moments(const void* x, const void* y, int32_t dtype, int64_t n, double* out, void* abs_delta,
+                     void* stream);
+
+/* 0-based ascending ranks of a row, ties sharing the mean of their positions
+ * (metrics.py:50-61, the input of spearman), from the row sorted descending
+ * (sorted [n] in dtype, e.g. dsa_topk_exact with k = n) and the key of each
+ * sorted position (order [n]); ranks [n] float64 indexed by key. */
+int dsa_average_ranks(const void* sorted, int32_t dtype, const int64_t* order, int64_t n, double* ranks,
+                      void* stream);
+
+/* *out += |{b[i]} ∩ {a[j]}| for two ascending key lists of length k (entries
+ * -1 are padding at the end and match nothing): the top-k overlap of
+ * replay.py:425-426 from the two rows' top-k in index order. */
+int dsa_index_overlap(const int64_t* a, const int64_t* b, int64_t k, uint32_t* out, void* stream);
+
+/* Per block b < blocks: streak[b] = cur_max[b] < *threshold ? streak[b] + 1
+ * : 0, delta[b] = cur_max[b] - prev_max[b] (float64), and counts[0..3] +=
+ * the blocks whose streak is at least 1, 2, 4, 8 (replay.py:448-472; the
+ * threshold is the row's k-th largest score, a device value). */
+int dsa_block_streaks(const float* prev_max, const float* cur_max, int64_t blocks, const float* threshold,
+                      int32_t* streak, double* delta, uint32_t* counts, void* stream);
 
 /* Head routing: per row of weights [rows, heads] (heads <= 64) the `width`
  * head ids with the largest |w| (positive_only == 0) or max(w, 0)

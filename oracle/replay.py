@@ -381,3 +381,115 @@ def aggregate_rows(rows: list[dict]):
         metadata_bytes=("metadata_bytes", "median"),
         net_byte_reduction=("net_byte_reduction", "median"),
     )
+
+
+# ---------------------------------------------------------------------------
+# Per-transition statistics tables (reference replay.py:403-474, the inputs of
+# the analyze command's temporal_stats.csv and block_stats.csv).
+# ---------------------------------------------------------------------------
+def pearson(x, y) -> float:
+    """Reference metrics.py:40-47: float64 correlation, NaN for fewer than two
+    values or a constant vector."""
+
+    x = np.asarray(x, dtype=np.float64)
+    y = np.asarray(y, dtype=np.float64)
+    if x.size != y.size or x.size < 2 or np.std(x) == 0 or np.std(y) == 0:
+        return math.nan
+    xc = x - x.mean()
+    yc = y - y.mean()
+    return float(np.clip(np.dot(xc, yc) / math.sqrt(np.dot(xc, xc) * np.dot(yc, yc)), -1.0, 1.0))
+
+
+def average_ranks(x) -> np.ndarray:
+    """0-based ascending ranks, tied values sharing the mean of their
+    positions (reference metrics.py:50-61)."""
+
+    x = np.asarray(x)
+    order = np.argsort(x, kind="stable")
+    ranks = np.empty(x.size, dtype=np.float64)
+    sx = x[order]
+    # run boundaries of equal values in ascending order
+    cuts = np.flatnonzero(np.concatenate(([True], sx[1:] != sx[:-1], [True])))
+    for start, end in zip(cuts[:-1], cuts[1:]):
+        ranks[order[start:end]] = 0.5 * (start + end - 1)
+    return ranks
+
+
+def spearman(x, y) -> float:
+    """Reference metrics.py:64-69."""
+
+    return pearson(average_ranks(x), average_ranks(y))
+
+
+def temporal_stats_rows(rows: list[np.ndarray], k_values, *, layer=0, workload="", prompt_id="") -> list[dict]:
+    """One record per (transition, k <= common length): score correlations,
+    the score drift and the top-k overlap of consecutive rows (reference
+    replay.py:403-428)."""
+
+    out = []
+    for step in range(1, len(rows)):
+        prev = np.asarray(rows[step - 1], dtype=np.float32)
+        cur = np.asarray(rows[step], dtype=np.float32)
+        n = min(prev.size, cur.size)
+        p, c = prev[:n], cur[:n]
+        delta = c - p  # float32, as the reference subtracts float32 rows
+        base = {
+            "step": step, "layer": layer, "workload": workload, "prompt_id": prompt_id,
+            "context_length": cur.size,
+            "score_pearson": pearson(p, c),
+            "score_spearman": spearman(p, c),
+            "delta_mean": float(np.mean(delta)),
+            "delta_std": float(np.std(delta)),
+            "delta_p99_abs": float(np.percentile(np.abs(delta), 99)),
+        }
+        for k in k_values:
+            if k > n:
+                continue
+            a = set(stable_topk(p, k).tolist())
+            b = stable_topk(c, k)
+            overlap = sum(1 for i in b.tolist() if i in a) / b.size
+            out.append({**base, "k": k, "topk_overlap": overlap})
+    return out
+
+
+def block_temporal_stats_rows(rows: list[np.ndarray], block_sizes, k_values, *, layer=0, workload="",
+                              prompt_id="") -> list[dict]:
+    """One record per (transition, block size, k <= common length): the
+    drift of the block maxima and the fraction of blocks cold (block maximum
+    below the current k-th largest score) for at least 1, 2, 4 and 8
+    consecutive steps (reference replay.py:431-474)."""
+
+    out = []
+    streak: dict[tuple[int, int], np.ndarray] = {}
+    for step in range(1, len(rows)):
+        prev = np.asarray(rows[step - 1], dtype=np.float32)
+        cur = np.asarray(rows[step], dtype=np.float32)
+        n = min(prev.size, cur.size)
+        for bs in block_sizes:
+            pm = block_maxima(prev[:n], bs)
+            cm = block_maxima(cur[:n], bs)
+            for k in k_values:
+                if k > n:
+                    continue
+                threshold = float(np.sort(cur[:n])[n - k])
+                state = streak.setdefault((bs, k), np.zeros(0, dtype=np.int32))
+                if state.size < cm.size:
+                    state = np.concatenate((state, np.zeros(cm.size - state.size, dtype=np.int32)))
+                cold = cm < threshold
+                state[: cm.size] = np.where(cold, state[: cm.size] + 1, 0)
+                streak[(bs, k)] = state
+                s = state[: cm.size]
+                delta = cm - pm
+                out.append({
+                    "step": step, "layer": layer, "workload": workload, "prompt_id": prompt_id,
+                    "context_length": cur.size, "k": k, "block_size": bs, "topk_threshold": threshold,
+                    "delta_max_mean": float(np.mean(delta)),
+                    "delta_max_p5": float(np.percentile(delta, 5)),
+                    "delta_max_median": float(np.median(delta)),
+                    "delta_max_p95": float(np.percentile(delta, 95)),
+                    "cold_fraction_1": float(np.mean(s >= 1)),
+                    "cold_fraction_2": float(np.mean(s >= 2)),
+                    "cold_fraction_4": float(np.mean(s >= 4)),
+                    "cold_fraction_8": float(np.mean(s >= 8)),
+                })
+    return out

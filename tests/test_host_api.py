@@ -150,3 +150,25 @@ def test_exact_order_keeps_integers_within_float64() -> None:
     for values, dtype in (([2**53, 7], np.uint64), ([-(2**53), 7], np.int64), ([3, 1], np.uint32)):
         got = metrics._exact_dtype(torch.from_numpy(np.array(values, dtype=dtype)))
         assert got.dtype == torch.float64 and [int(v) for v in got.tolist()] == values
+
+
+def test_replay_percentiles_follow_numpy() -> None:
+    # The statistics tables read two neighbours of each virtual index from a
+    # descending GPU sort and interpolate on the host with numpy's arithmetic
+    # in the row's precision (reference replay.py:420, 461-463 np.percentile);
+    # checked here on CPU tensors against numpy itself.
+    import numpy as np
+    import torch
+
+    from dsa_amd import replay
+
+    rng = np.random.default_rng(0)
+    for trial in range(400):
+        n = int(rng.integers(1, 3000))
+        dt = np.float32 if trial % 2 else np.float64
+        x = (rng.standard_normal(n) * rng.uniform(0.1, 10)).astype(dt)
+        if trial % 5 == 0:
+            x = np.round(x)
+        desc = torch.from_numpy(np.sort(x)[::-1].copy())
+        got = replay._percentiles(desc, [1, 5, 50, 95, 99, 100])
+        assert got == [float(np.percentile(x, q)) for q in (1, 5, 50, 95, 99, 100)]
