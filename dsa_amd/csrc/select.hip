@@ -44,18 +44,32 @@ struct SelectArgs {
 
 __device__ __forceinline__ uint64_t composite(uint32_t key, int pos) { return select_composite(key, (uint32_t)pos); }
 
+#ifdef DSA_PHASE_TRACE
+// The list select, per workgroup (by blockIdx.x): 0 start, 1 entries counted
+// and the cut's bin located, 2 cut resolved, 3 earlier lists' chosen counted,
+// 4 written; 5, 6, 7: the radix cut's passes 0, 1, 2 counted.
+__device__ uint64_t g_trace_select[kTraceWgs * kTraceMarks];
+#endif
+
 // Radix select of the want-th largest composite among the n entries at(i)
-// whose top 12 bits equal `bin`: 11-bit digits of bits 51..8, then bits
-// 7..0.  All waves count a digit, wave 0 locates the digit holding the cut
+// whose top 12 bits equal `bin`: 11-bit digits of bits 51..41, then the
+// score key's last 9 bits (40..32); then the position part, 11, 11 and 10
+// bits.  All waves count a digit, wave 0 locates the digit holding the cut
 // while the other waves clear the other counter buffer, and a digit with a
 // single entry ends the search (that entry was recorded while counting).
+// With kOrdered (the entries at(0..n) in ascending position order), once the
+// score key is fixed the cut is the rem-th entry carrying it in that order,
+// found by one counting pass and a block scan instead of three position
+// digits: tied scores are common where scores are quantised.
 // digits[0] must be zero on entry; both buffers are left dirty.
 struct RadixShared {
   uint64_t last[kDigitBins];  // an entry of each digit (the only one when its count is 1)
+  __align__(16) uint32_t wsum[kSelWaves];  // the tie scan's wave sums (read as uint4)
   uint32_t digit, rem, count;
+  uint64_t tie;
 };
 
-template <class At>
+template <bool kOrdered, class At>
 __device__ __forceinline__ uint64_t radix_cut(uint32_t bin, uint32_t want, uint32_t n, At at,
                                               uint32_t (*digits)[kDigitBins], RadixShared& rs) {
   const uint32_t tid = threadIdx.x;
@@ -66,18 +80,51 @@ __device__ __forceinline__ uint64_t radix_cut(uint32_t bin, uint32_t want, uint3
   uint32_t rem = want;
 #pragma unroll 1
   for (int pass = 0; pass < 5; ++pass) {
-    const int shift = pass < 4 ? 41 - 11 * pass : 0;
-    const uint32_t dmask = pass < 4 ? 0x7ffu : 0xffu;
+    if (kOrdered && pass == 2) {
+      // The score key is fixed: the rem-th entry carrying it, by position.
+      const uint32_t per = (n + kSelThreads - 1) / kSelThreads;
+      const uint32_t i0 = min(n, tid * per);
+      const uint32_t i1 = min(n, i0 + per);
+      uint32_t ties = 0;
+      for (uint32_t i = i0; i < i1; ++i) ties += (at(i) & mask) == prefix ? 1u : 0u;
+      uint32_t total;
+      uint32_t before = block_excl_scan<kSelWaves>(ties, rs.wsum, total);
+      if (before < rem && rem <= before + ties) {
+        for (uint32_t i = i0; i < i1; ++i) {
+          const uint64_t x = at(i);
+          if ((x & mask) == prefix && ++before == rem) rs.tie = x;
+        }
+      }
+      __syncthreads();
+      return rs.tie;
+    }
+    // Digits: bits 51..41, 40..32, 31..21, 20..10, 9..0 (selects, not a
+    // table: a table would be a scalar load at every pass).
+    const int shift = pass == 0 ? 41 : pass == 1 ? 32 : pass == 2 ? 21 : pass == 3 ? 10 : 0;
+    const uint32_t dmask = pass == 1 ? 0x1ffu : pass == 4 ? 0x3ffu : 0x7ffu;
     uint32_t* dig = digits[pass & 1];
-    for (uint32_t i = tid; i < n; i += kSelThreads) {
-      const uint64_t x = at(i);
-      if ((x & mask) == prefix) {
-        const uint32_t d = (uint32_t)(x >> shift) & dmask;
-        __hip_atomic_fetch_add(&dig[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        rs.last[d] = x;
+    // Eight entries per thread are read before any is counted, so that the
+    // reads are in flight together (the counts and the recorded entries
+    // would otherwise order every read behind the previous entry's writes).
+    constexpr int kBatch = 8;
+    for (uint32_t i0 = tid; i0 < n; i0 += kBatch * kSelThreads) {
+      uint64_t x[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const uint32_t i = i0 + u * kSelThreads;
+        x[u] = i < n ? at(i) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (i0 + u * kSelThreads < n && (x[u] & mask) == prefix) {
+          const uint32_t d = (uint32_t)(x[u] >> shift) & dmask;
+          __hip_atomic_fetch_add(&dig[d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          rs.last[d] = x[u];
+        }
       }
     }
     __syncthreads();
+    if (pass < 3) DSA_TRACE_MARK(g_trace_select, blockIdx.x, 5 + pass);
     if (wave == 0) {
       const Locate t = wave_locate<kDigitBins / kWave>(dig, rem, false);
       if (lane == 0) {
@@ -309,7 +356,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs 
       }
       __syncthreads();
     }
-    cstar = radix_cut(bin, want, crowd, cand_at, sh.digits, sh.radix);
+    cstar = radix_cut<false>(bin, want, crowd, cand_at, sh.digits, sh.radix);
   }
 
   // This chunk's chosen scores in index order, after the chosen scores of the
@@ -436,6 +483,7 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
   const uint32_t kk = (uint32_t)a.k;
   const float* srow = a.scores + (size_t)row * n;
   const uint64_t* lrow = a.lists + (size_t)row * n;
+  DSA_TRACE_MARK(g_trace_select, blockIdx.x, 0);
   if (a.count_parts && c == 0 && wave == 0) {
     uint32_t sum = 0;
     uint32_t flags = 0;
@@ -532,6 +580,7 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
     __syncthreads();  // every thread has read sh.miss before the next round clears it
   }
 
+  DSA_TRACE_MARK(g_trace_select, blockIdx.x, 1);
   const uint32_t bin = sh.bin;
   auto raw_of = [&](uint32_t list) { return sh.raw[list] != 0u; };
   auto entry_of = [&](uint32_t s) -> uint64_t {  // entry s of this thread's source
@@ -550,7 +599,8 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
     uint32_t (*digits)[kDigitBins] = reinterpret_cast<uint32_t (*)[kDigitBins]>(sh.hist);
     for (uint32_t i = tid; i < (uint32_t)kDigitBins; i += kSelThreads) digits[0][i] = 0;
     __syncthreads();
-    cstar = radix_cut(bin, sh.want, entries, [&](uint32_t i) { return sh.stage[i]; }, digits, sh.radix);
+    cstar = radix_cut<true>(bin, sh.want, entries, [&](uint32_t i) { return sh.stage[i]; }, digits, sh.radix);
+    DSA_TRACE_MARK(g_trace_select, blockIdx.x, 2);
     before = 0;
     for (uint32_t i = tid; i < sh.base[c]; i += kSelThreads) before += sh.stage[i] >= cstar ? 1u : 0u;
   } else if (bin != kNoBin) {
@@ -599,7 +649,7 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
     __syncthreads();
     const uint32_t crowd = sh.crowd;
     if (crowd <= (uint32_t)kCandCapacity) {
-      cstar = radix_cut(bin, sh.want, crowd, [&](uint32_t i) { return sh.cands[i]; }, digits, sh.radix);
+      cstar = radix_cut<false>(bin, sh.want, crowd, [&](uint32_t i) { return sh.cands[i]; }, digits, sh.radix);
       // The chosen entries of the cut's bin in the lists before this chunk's.
       for (uint32_t i = tid; i < crowd; i += kSelThreads) {
         const uint64_t x = sh.cands[i];
@@ -619,12 +669,13 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
         const uint32_t pos = lo * ck + (i - sh.base[lo]);
         return raw_of(lo) ? select_composite(float_to_ordered(srow[pos]), pos) : lrow[pos];
       };
-      cstar = radix_cut(bin, sh.want, entries, entry_at, digits, sh.radix);
+      cstar = radix_cut<true>(bin, sh.want, entries, entry_at, digits, sh.radix);
       before = 0;
       for (uint32_t i = tid; i < sh.base[c]; i += kSelThreads) before += entry_at(i) >= cstar ? 1u : 0u;
     }
   }
 
+  DSA_TRACE_MARK(g_trace_select, blockIdx.x, 3);
   // This chunk's own source, a contiguous run per thread, in index order.
   const uint32_t own0 = sh.base[c];
   const uint32_t own_n = sh.base[c + 1] - own0;
@@ -668,6 +719,7 @@ __global__ __launch_bounds__(kSelThreads) void select_lists_kernel(ListArgs a) {
       if (oval) oval[i] = -__builtin_inff();
     }
   }
+  DSA_TRACE_MARK(g_trace_select, blockIdx.x, 4);
 }
 
 // ---------------------------------------------------------------------------
@@ -852,3 +904,18 @@ extern "C" int dsa_select_topk_timed(const float* scores, int64_t batch, int64_t
   return select_topk(scores, batch, length, k, out_indices, out_values, workspace, workspace_bytes, stream,
                      static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
 }
+
+#ifdef DSA_PHASE_TRACE
+// The list select's phase log (trace builds only).
+extern "C" int dsa_trace_select_lists(uint64_t* host, int64_t n, int32_t clear) {
+  using namespace dsa;
+  DSA_REQUIRE(host && n >= 0 && n <= int64_t(kTraceWgs) * kTraceMarks, "bad trace read");
+  if (int st = check_hip(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace_select), (size_t)n * 8), "trace read"))
+    return st;
+  if (clear) {
+    static const uint64_t zeros[kTraceWgs * kTraceMarks] = {};
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_select), zeros, sizeof(zeros)), "trace clear");
+  }
+  return DSA_STATUS_OK;
+}
+#endif

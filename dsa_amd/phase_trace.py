@@ -13,9 +13,10 @@ earliest workgroup start, as percentiles over workgroups and per XCD
 
 Configurations: ``c2`` (B=16, L=32768 bf16, K=2048 decode step), ``c5``
 (B=4, L=131072 fp8, K=2048), ``c3-static`` (B=4, 16384 -> 16385 keys,
-K=2048, block 64 static temporal step) and ``c4-topk`` (the prefill top-512
+K=2048, block 64 static temporal step), ``c4-topk`` (the prefill top-512
 of 4096 causal rows of 1..4096 scores; in this one the row-loaded mark waits
-for the row, so the trace build's timing of that kernel differs slightly).
+for the row, so the trace build's timing of that kernel differs slightly),
+and ``c2-select`` / ``c5-select`` (the decode step's list select).
 """
 
 from __future__ import annotations
@@ -39,8 +40,11 @@ MARKS = {
     "static": ["start", "seeds listed", "seeds scored", "threshold exchanged", "blocks decided", "units scored",
                "list written"],
     "topk": ["start", "row loaded", "range known", "cut located", "cut resolved", "slots scanned", "written"],
+    "select": ["start", "entries counted, cut bin located", "cut resolved", "earlier lists counted", "written",
+               "radix pass 0 counted", "radix pass 1 counted", "radix pass 2 counted"],
 }
-KERNEL_SYMBOL = {"dense": "dsa_trace_dense_scores", "static": "dsa_trace_temporal_static", "topk": "dsa_trace_topk"}
+KERNEL_SYMBOL = {"dense": "dsa_trace_dense_scores", "static": "dsa_trace_temporal_static", "topk": "dsa_trace_topk",
+                 "select": "dsa_trace_select_lists"}
 
 
 def _c2(device):
@@ -97,7 +101,15 @@ def _c4_topk(device):
                                     idx.data_ptr(), None, stream)
 
 
-CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static, "c4-topk": _c4_topk}
+def _select_of(config):
+    # The same decode step, timed by the list select's marks.
+    def make(device):
+        return "select", config(device)[1]
+    return make
+
+
+CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static, "c4-topk": _c4_topk,
+           "c2-select": _select_of(_c2), "c5-select": _select_of(_c5)}
 
 
 def timeline(config: str, runs: int = 8) -> dict:
@@ -125,13 +137,18 @@ def timeline(config: str, runs: int = 8) -> dict:
     log = np.frombuffer(host, dtype=np.uint64).reshape(4096, 8).astype(np.int64)
     wgs = np.flatnonzero(log[:, 0] > 0)
     names = MARKS[kernel]
-    t = (log[wgs][:, : len(names)] - log[wgs, 0].min()) / WALL_CLOCK_MHZ  # microseconds
+    raw = log[wgs][:, : len(names)].astype(np.float64)
+    raw[raw == 0] = np.nan  # a mark the workgroup did not reach (an early exit)
+    t = (raw - log[wgs, 0].min()) / WALL_CLOCK_MHZ  # microseconds
     out = {"config": config, "kernel": kernel, "workgroups": int(wgs.size), "unit": "us from the earliest start",
            "marks": {}}
     for i, name in enumerate(names):
-        col = t[:, i]
+        col = t[:, i][~np.isnan(t[:, i])]
+        if col.size == 0:
+            continue
         out["marks"][name] = {q: round(float(np.percentile(col, p)), 2)
                               for q, p in (("min", 0), ("p10", 10), ("median", 50), ("p90", 90), ("max", 100))}
+        out["marks"][name]["workgroups"] = int(col.size)
     last = len(names) - 1
     xcd = wgs % 8
     out["per_xcd_end"] = {int(x): {"median": round(float(np.median(t[xcd == x, last])), 2),
