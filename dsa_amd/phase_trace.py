@@ -149,10 +149,10 @@ def timeline(config: str, runs: int = 8) -> dict:
         out["marks"][name] = {q: round(float(np.percentile(col, p)), 2)
                               for q, p in (("min", 0), ("p10", 10), ("median", 50), ("p90", 90), ("max", 100))}
         out["marks"][name]["workgroups"] = int(col.size)
-    last = len(names) - 1
+    end = np.nanmax(t, axis=1)  # each workgroup's latest mark
     xcd = wgs % 8
-    out["per_xcd_end"] = {int(x): {"median": round(float(np.median(t[xcd == x, last])), 2),
-                                   "max": round(float(t[xcd == x, last].max()), 2)} for x in range(8)}
+    out["per_xcd_end"] = {int(x): {"median": round(float(np.median(end[xcd == x])), 2),
+                                   "max": round(float(end[xcd == x].max()), 2)} for x in range(8)}
     return out
 
 
