@@ -285,13 +285,16 @@ __global__ __launch_bounds__(64 * kWaves, kWaves == 4 ? 2 : 1) void dense_scores
 // Multi-query (prefill) scoring: many query blocks against one shared key set.
 // A workgroup owns kPrefillQueries consecutive queries of one key set, one
 // per wave, and streams the key units they see through LDS: each 64-key unit
-// is loaded from memory once and scored for all eight queries, instead of
+// is loaded from memory once and scored for all four queries, instead of
 // once per query.  Rows are padded to kPrefillRow bytes so the 16 rows a lane
 // group reads fall on different banks.  With a causal limit the heaviest
 // query blocks are dispatched first.  One query per wave needs about half the
-// registers of two, so two waves share each SIMD.
+// registers of two; a workgroup holds one wave per SIMD and two or three
+// workgroups share a CU, so one workgroup's barrier waits and its top-k
+// epilogue run under another's MFMAs (eight queries per workgroup, one
+// workgroup per CU, measured 5 us slower per C4 layer; two, 60 us slower).
 // ---------------------------------------------------------------------------
-constexpr int kPrefillQueries = 8;
+constexpr int kPrefillQueries = 4;
 constexpr int kPrefillRow = 272;
 
 // ---------------------------------------------------------------------------
@@ -529,7 +532,7 @@ __device__ __forceinline__ void mfma_valu_interleave() {
 }
 
 template <class Tag, bool kTopK>
-__global__ __launch_bounds__(64 * kPrefillQueries) void prefill_scores_kernel(DenseArgs a, int32_t qblocks,
+__global__ __launch_bounds__(64 * kPrefillQueries, 2) void prefill_scores_kernel(DenseArgs a, int32_t qblocks,
                                                                             int32_t keysets) {
   constexpr int kThreads = 64 * kPrefillQueries;
   constexpr int kRowSplit = kThreads / 64;

@@ -116,7 +116,7 @@ def score_encoded_topk(
     Returns ``(scores [B, Q, K] fp32, indices [B, Q, k] int64)``, plus the
     selected values ``[B, Q, k]`` with ``return_values``.  A query with fewer
     than ``k`` visible keys returns all of them, padded with -1 (values -inf).
-    Needs fp16/bf16 queries and keys, at least 8 queries per key set and at
+    Needs fp16/bf16 queries and keys, at least 4 queries per key set and at
     most 4096 keys.
     """
 
@@ -136,8 +136,8 @@ def score_encoded_topk(
         raise ValueError("k must be positive")
     if not 1 <= length <= 4096:
         raise ValueError("the fused top-k takes 1..4096 keys per key set")
-    if num_queries < 8:
-        raise ValueError("the fused top-k takes at least 8 queries per key set")
+    if num_queries < 4:
+        raise ValueError("the fused top-k takes at least 4 queries per key set")
     offset = -1
     if causal:
         offset = length - num_queries if causal_offset is None else int(causal_offset)

@@ -103,9 +103,9 @@ int dsa_score_queries(const void* queries, int64_t q_stride, const float* weight
  *                  a query with fewer than k visible keys returns all of
  *                  them, padded with -1
  *   out_values     fp32, same layout, nullable (padding -inf)
- * Each workgroup scores eight consecutive queries of one key set; each
+ * Each workgroup scores four consecutive queries of one key set; each
  * query's wave then selects from its own row.  Limits: length <= 4096,
- * queries_per_keyset >= 8 and sequences a multiple of it, k >= 1,
+ * queries_per_keyset >= 4 and sequences a multiple of it, k >= 1,
  * topk_stride >= k; other arguments as dsa_score_queries.
  * ------------------------------------------------------------------------ */
 int dsa_score_queries_topk(const void* queries, int64_t q_stride, const float* weights, int64_t w_stride,
