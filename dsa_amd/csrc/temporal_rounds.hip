@@ -17,7 +17,10 @@
 //     group: the group's decisions against the exact threshold, then the
 //     listed keys of its kept blocks join the running k largest; scored
 //     blocks that the replay prunes get -inf back, seeds excepted
-//     (temporal_resolve_kernel).
+//     (temporal_resolve_kernel).  No threshold of the round exceeds the k-th
+//     largest of all the round's keys, and none falls below the one in force,
+//     so a run of groups whose every bound lies outside that interval is
+//     decided, and joined, in one step of the replay.
 //
 // The decisions, the evaluated keys and their scores are those of the
 // sequential scan (the persistent and per-wave paths of temporal.hip) bit for
@@ -51,7 +54,8 @@ static_assert(kRoundWaves * kRoundWaveKeys == kRoundKeys, "two 64-key units per 
 // Per row (trace builds only): wall-clock ticks of the replay's phases and
 // event counts: 0 group loop, 1 decisions, 2 exact selects, 3 select count
 // (low half) and cut move count (high half), 4 joins, 5 cut moves, 6 listed
-// keys (low 48 bits) and rounds that sorted in the workspace (high 16), 7 setup
+// keys (bits 0-23), loop steps (bits 24-47) and rounds that sorted in the
+// workspace (high 16), 7 setup
 // (kernel start to the group loop).  Accumulated in registers by wave 0 and added to memory once per
 // launch, so that the timing itself adds no memory round trip to the loop.
 __device__ uint64_t g_trace_resolve[kTraceWgs * kTraceMarks];
@@ -287,9 +291,14 @@ struct ResolveShared {
   uint16_t blk[kMaxTemporalBlocks];   // block at each
   uint8_t kept[kMaxTemporalBlocks];   // by block id
   uint16_t resets[kMaxTemporalBlocks];
+  // Positions whose bound is at or below the upper edge of the bin holding
+  // the k-th largest of every key of the round (the only ones a threshold of
+  // the round can prune), in position order, with their bound keys.
+  uint32_t risky_uk[kMaxTemporalBlocks];
+  uint16_t risky_pos[kMaxTemporalBlocks];
   uint32_t digits[kCutDigits];
   uint32_t wsum[kResolveWaves];
-  uint32_t above, max_key, nreset, tau, cut_bin, n_out;
+  uint32_t above, max_key, nreset, tau, cut_bin, n_out, bin_hi, n_risky;
 };
 
 // The j-th largest (1-based) of the joined keys in slots [s0, s1) of bin `bin`
@@ -385,7 +394,10 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     sh.E[i] = 0;
   }
   for (int i = tid; i < n_groups; i += kResolveThreads) sh.gend[i] = 0;
-  if (tid == 0) sh.above = 0;
+  if (tid == 0) {
+    sh.above = 0;
+    sh.bin_hi = kBins - 1;
+  }
   __syncthreads();
   uint32_t above = 0;
   each_run([&](uint32_t v) {
@@ -417,26 +429,44 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     uint32_t before = block_excl_scan<kResolveWaves>(sum, sh.wsum, total);
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
+      // The bin of the k-th largest of all keys (total - before keys sit in
+      // bins at or above this one): no threshold of the round lies above it.
+      if (c[j] && total - before >= (uint32_t)k && total - before - c[j] < (uint32_t)k) sh.bin_hi = tid * kPer + j;
       sh.end[tid * kPer + j] = before;
       before += c[j];
     }
     __syncthreads();
+    // Group starts, and the positions a threshold of the round could prune
+    // (bound key at or below the upper edge of the k-th largest's bin),
+    // compacted in position order: both counts scanned in one word (listed
+    // keys below 2^18 in the low bits, positions below 2^12 from bit 19).
+    const uint64_t hi_edge = (uint64_t)floor_key + ((uint64_t)(sh.bin_hi + 1) << shift) - 1ull;
     constexpr int kGPer = kMaxTemporalBlocks / kResolveThreads;
     uint32_t gc[kGPer];
+    bool risky[kGPer];
     uint32_t gsum = 0;
 #pragma unroll
     for (int j = 0; j < kGPer; ++j) {
       const int gi = tid * kGPer + j;
       gc[j] = gi < n_groups ? sh.gend[gi] : 0u;
-      gsum += gc[j];
+      risky[j] = gi < n_pos && (uint64_t)sh.uk[gi] <= hi_edge;
+      gsum += gc[j] + (risky[j] ? 1u << 19 : 0u);
     }
     uint32_t gbefore = block_excl_scan<kResolveWaves>(gsum, sh.wsum, total);
+    uint32_t rbefore = gbefore >> 19;
+    gbefore &= (1u << 19) - 1u;
 #pragma unroll
     for (int j = 0; j < kGPer; ++j) {
       const int gi = tid * kGPer + j;
       if (gi < n_groups) sh.gend[gi] = gbefore;
       gbefore += gc[j];
+      if (risky[j]) {
+        sh.risky_pos[rbefore] = (uint16_t)gi;
+        sh.risky_uk[rbefore] = sh.uk[gi];
+        ++rbefore;
+      }
     }
+    if (tid == 0) sh.n_risky = total >> 19;
   }
   __syncthreads();
   // Scatter: run's keys joined, listed keys not yet; listed keys' items by group.
@@ -493,7 +523,7 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     int pf_blk = 0;
     auto prefetch = [&](int gi) {
       const int q = gi * W + lane;
-      const bool ok = gi < n_groups && q < min(gi * W + W, n_pos);
+      const bool ok = gi < n_groups && q < n_pos;
       pf_uk = ok ? sh.uk[q] : 0u;
       pf_blk = ok ? (int)sh.blk[q] : 0;
     };
@@ -511,13 +541,48 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     prefetch(0);
     prefetch_items(0u);
     uint32_t i0 = 0u;  // the group's first item
-    for (int gi = 0; gi < n_groups; ++gi) {
-      const uint32_t i1 = sh.gend[gi];
+    // Positions whose decision is the same under every threshold between the
+    // cut bin's lower edge (no later threshold is below it) and hi_edge (none
+    // is above it): bound above hi_edge, kept; below the lower edge, pruned
+    // (when neither edge admits a NaN threshold).  Only risky positions can
+    // be open; rc is the first risky one that may still be.
+    const uint64_t hi_edge = (uint64_t)floor_key + ((uint64_t)(sh.bin_hi + 1) << shift) - 1ull;
+    const uint32_t n_risky = sh.n_risky;
+    uint32_t rc = 0u;
+    for (int gi = 0, g_end = 1; gi < n_groups; gi = g_end) {
+      // The step covers group gi and every following group with no open
+      // position: their decisions, and then their joins, need no threshold
+      // beyond the one group gi is decided by.
+      g_end = gi + 1;
+      if (!(rp.first_round && gi == 0)) {
+        const uint64_t lo_edge = (uint64_t)floor_key + ((uint64_t)bin << shift);
+        const bool can_prune = lo_edge >= 0x007fffffull && hi_edge <= 0xff800000ull;
+        const uint32_t q_first = (uint32_t)(gi * W);
+        int g_open = n_groups;
+        while (rc < n_risky) {
+          const uint32_t i = rc + (uint32_t)lane;
+          uint32_t pos = 0u;
+          bool open = false;
+          if (i < n_risky) {
+            pos = sh.risky_pos[i];
+            open = pos >= q_first && !(can_prune && (uint64_t)sh.risky_uk[i] < lo_edge);
+          }
+          const uint64_t m = __ballot(open);
+          if (m) {
+            g_open = __builtin_amdgcn_readlane((int)pos, (int)__builtin_ctzll(m)) / W;
+            break;
+          }
+          rc += kWave;  // every entry is decided already or pruned at every later threshold
+        }
+        g_end = max(g_open, gi + 1);
+      }
+      RESOLVE_COUNT(6, 1ull << 24);
+      const uint32_t i1 = sh.gend[g_end - 1];
       uint32_t pf_v[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) pf_v[h] = val[pf_it[h] & 0x3ffffu];
       const int q0 = gi * W;
-      const int q1 = min(q0 + W, n_pos);
+      const int q1 = min(g_end * W, n_pos);
       const bool seed_group = rp.first_round && gi == 0;
       // The cut bin's keys, and whether NaN keys can fall in it (then every
       // decision takes the exact threshold).
@@ -554,7 +619,7 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
         nreset += (uint32_t)__builtin_popcountll(m);
       }
       wave_sync();
-      prefetch(gi + 1);
+      prefetch(g_end);
       RESOLVE_ADD(1, t_dec);
       // The kept blocks' listed keys join, 128 at a time: the first 128 from
       // the values read ahead, the rest (long groups) read here, items and
