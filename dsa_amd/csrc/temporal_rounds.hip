@@ -514,10 +514,10 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       }
       return tau;
     };
-    // Read ahead of each group: its first 64 decision inputs, and the items
-    // of its first 128 listed keys (items are stored by group, so the next
-    // group's start slot is this group's end), whose values are then read
-    // while the group's decisions are made.  Reads past a group's end are
+    // Read ahead of each step: its first 64 decision inputs, and the items
+    // of its first 256 listed keys (items are stored by group, so the next
+    // step's start slot is this step's end), whose values are then read
+    // while the step's decisions are made.  Reads past a step's end are
     // harmless (items of later groups, or the last item again) and unused.
     uint32_t pf_uk = 0u;
     int pf_blk = 0;
@@ -530,10 +530,11 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     // (With no listed keys the read of item 0 is stale, so its slot and block
     // are replaced by 0: slot 0 holds a run key, block 0 exists.)
     const uint32_t item_last = n_listed ? n_listed - 1u : 0u;
-    uint32_t pf_it[2];
+    constexpr int kJoinHalves = 4;  // listed keys per lane per join pass
+    uint32_t pf_it[kJoinHalves];
     auto prefetch_items = [&](uint32_t start) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kJoinHalves; ++h) {
         const uint32_t it = item[min(start + (uint32_t)(h * kWave + lane), item_last)];
         pf_it[h] = n_listed ? it : 0u;
       }
@@ -578,9 +579,9 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       }
       RESOLVE_COUNT(6, 1ull << 24);
       const uint32_t i1 = sh.gend[g_end - 1];
-      uint32_t pf_v[2];
+      uint32_t pf_v[kJoinHalves];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) pf_v[h] = val[pf_it[h] & 0x3ffffu];
+      for (int h = 0; h < kJoinHalves; ++h) pf_v[h] = val[pf_it[h] & 0x3ffffu];
       const int q0 = gi * W;
       const int q1 = min(g_end * W, n_pos);
       const bool seed_group = rp.first_round && gi == 0;
@@ -621,35 +622,37 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       wave_sync();
       prefetch(g_end);
       RESOLVE_ADD(1, t_dec);
-      // The kept blocks' listed keys join, 128 at a time: the first 128 from
-      // the values read ahead, the rest (long groups) read here, items and
-      // values of both halves issued before any is used.
+      // The kept blocks' listed keys join, 256 at a time: the first 256 from
+      // the values read ahead, the rest (long steps) read here, items and
+      // values of all four quarters issued before any is used.
       RESOLVE_T0(t_join);
-      auto join_keys = [&](uint32_t c0, const uint32_t (&it)[2], const uint32_t (&v)[2]) {
-        uint32_t b[2];
-        bool in[2];
+      auto join_keys = [&](uint32_t c0, const uint32_t (&it)[kJoinHalves], const uint32_t (&v)[kJoinHalves]) {
+        uint32_t b[kJoinHalves];
+        bool in[kJoinHalves];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < kJoinHalves; ++h) {
           b[h] = (v[h] - floor_key) >> shift;
           in[h] = c0 + (uint32_t)(h * kWave + lane) < i1 && sh.kept[it[h] >> 18];
         }
+        bool reaches = false;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < kJoinHalves; ++h) {
           if (in[h]) {
             join[it[h] & 0x3ffffu] = 1;
             __hip_atomic_fetch_add(&sh.E[b[h]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
-        cut_above += (uint32_t)__builtin_popcountll(__ballot(in[0] && b[0] > bin)) +
-                     (uint32_t)__builtin_popcountll(__ballot(in[1] && b[1] > bin));
-        if (__ballot((in[0] && b[0] >= bin) || (in[1] && b[1] >= bin))) tau_ok = false;
+          cut_above += (uint32_t)__builtin_popcountll(__ballot(in[h] && b[h] > bin));
+          reaches = reaches || (in[h] && b[h] >= bin);
+        }
+        if (__ballot(reaches)) tau_ok = false;
       };
       if (i0 < i1) join_keys(i0, pf_it, pf_v);
-      for (uint32_t c0 = i0 + 2 * kWave; c0 < i1; c0 += 2 * kWave) {
-        uint32_t it[2], v[2];
+      for (uint32_t c0 = i0 + kJoinHalves * kWave; c0 < i1; c0 += kJoinHalves * kWave) {
+        uint32_t it[kJoinHalves], v[kJoinHalves];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) it[h] = item[min(c0 + (uint32_t)(h * kWave + lane), item_last)];
+        for (int h = 0; h < kJoinHalves; ++h) it[h] = item[min(c0 + (uint32_t)(h * kWave + lane), item_last)];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) v[h] = val[it[h] & 0x3ffffu];
+        for (int h = 0; h < kJoinHalves; ++h) v[h] = val[it[h] & 0x3ffffu];
         join_keys(c0, it, v);
       }
       prefetch_items(i1);
