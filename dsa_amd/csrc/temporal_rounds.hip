@@ -522,10 +522,9 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     uint32_t pf_uk = 0u;
     int pf_blk = 0;
     auto prefetch = [&](int gi) {
-      const int q = gi * W + lane;
-      const bool ok = gi < n_groups && q < n_pos;
-      pf_uk = ok ? sh.uk[q] : 0u;
-      pf_blk = ok ? (int)sh.blk[q] : 0;
+      const int qc = max(min(gi * W + lane, n_pos - 1), 0);
+      pf_uk = sh.uk[qc];
+      pf_blk = (int)sh.blk[qc];
     };
     // (With no listed keys the read of item 0 is stale, so its slot and block
     // are replaced by 0: slot 0 holds a run key, block 0 exists.)
@@ -596,9 +595,10 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
         const bool active = q < q1;
         uint32_t uk = pf_uk;
         int blk = pf_blk;
-        if (c0 != q0) {
-          uk = active ? sh.uk[q] : 0u;
-          blk = active ? (int)sh.blk[q] : 0;
+        if (c0 != q0) {  // (read for every lane, clamped: no branch around the reads)
+          const int qc = min(q, n_pos - 1);
+          uk = sh.uk[qc];
+          blk = (int)sh.blk[qc];
         }
         int verdict = 2;  // 0 pruned, 1 kept, 2 needs the exact threshold
         if (seed_group) {
@@ -627,12 +627,16 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       // values of all four quarters issued before any is used.
       RESOLVE_T0(t_join);
       auto join_keys = [&](uint32_t c0, const uint32_t (&it)[kJoinHalves], const uint32_t (&v)[kJoinHalves]) {
-        uint32_t b[kJoinHalves];
+        // (Every item read is a valid one, so the flags are read for all
+        // lanes at once, with no branch between the reads.)
+        uint32_t b[kJoinHalves], kb[kJoinHalves];
         bool in[kJoinHalves];
+#pragma unroll
+        for (int h = 0; h < kJoinHalves; ++h) kb[h] = sh.kept[it[h] >> 18];
 #pragma unroll
         for (int h = 0; h < kJoinHalves; ++h) {
           b[h] = (v[h] - floor_key) >> shift;
-          in[h] = c0 + (uint32_t)(h * kWave + lane) < i1 && sh.kept[it[h] >> 18];
+          in[h] = (c0 + (uint32_t)(h * kWave + lane) < i1) & (kb[h] != 0u);
         }
         bool reaches = false;
 #pragma unroll
