@@ -40,6 +40,7 @@ struct SelectArgs {
   SelectWorkspace ws;
   int64_t* out_idx;  // [rows, k]
   float* out_val;    // [rows, k] or null
+  const uint32_t* skip;  // [rows] or null: rows with a nonzero flag are not selected
 };
 
 __device__ __forceinline__ uint64_t composite(uint32_t key, int pos) { return select_composite(key, (uint32_t)pos); }
@@ -162,6 +163,7 @@ __global__ __launch_bounds__(kSelThreads) void select_gather_kernel(SelectArgs a
   const uint32_t logical = logical_block();
   const uint32_t row = logical / chunks;
   const uint32_t c = logical % chunks;
+  if (a.skip && a.skip[row]) return;
   const uint32_t n = (uint32_t)a.length;
   const uint32_t kk = (uint32_t)a.k;
   const uint32_t p0 = c * kSelectChunk + tid * kSelEpt;
@@ -250,6 +252,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_kernel(SelectArgs 
   const uint32_t logical = logical_block();
   const uint32_t row = logical / chunks;
   const uint32_t c = logical % chunks;
+  if (a.skip && a.skip[row]) return;
   const uint32_t n = (uint32_t)a.length;
   const uint32_t kk = (uint32_t)a.k;
   const uint32_t p0 = c * kSelectChunk + tid * kSelEpt;
@@ -789,8 +792,9 @@ SelectWorkspace select_workspace_layout(void* base, int64_t rows, int64_t length
 
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,
-                  hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+                  hipStream_t stream, hipEvent_t start, hipEvent_t stop, const uint32_t* skip) {
   SelectArgs a;
+  a.skip = skip;
   a.scores = scores;
   a.rows = (int32_t)rows;
   a.length = (int32_t)length;
@@ -834,6 +838,7 @@ int launch_select_lists(const float* scores, int64_t rows, int64_t length, int64
 int launch_select_scores(const float* scores, int64_t rows, int64_t length, int64_t k,
                          const SelectWorkspace& ws, int64_t* out_idx, float* out_val, hipStream_t stream) {
   SelectArgs a;
+  a.skip = nullptr;
   a.scores = scores;
   a.rows = (int32_t)rows;
   a.length = (int32_t)length;

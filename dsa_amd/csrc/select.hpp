@@ -98,7 +98,8 @@ int launch_select_scores(const float* scores, int64_t rows, int64_t length, int6
 // their own start and end (hipExtLaunchKernel).
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,
-                  hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+                  hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr,
+                  const uint32_t* skip = nullptr);  // skip[row] != 0: the row is left as it is
 
 // Selects the top-k of scores [rows, length] from the candidate lists that
 // the scoring kernel wrote to ws under `plan`.

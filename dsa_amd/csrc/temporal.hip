@@ -67,6 +67,7 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   if (tid == 0) {
     a.ws.tau[row] = 0xffffffffu;
     a.ws.floor[row] = 0xffffffffu;
+    a.ws.done[row] = 0u;
     a.ws.loaded[row] = 0;
     a.qk_scored[row] = 0;
     if (a.waits_given_up) a.waits_given_up[row] = 0;  // only the fused static step waits
@@ -281,6 +282,7 @@ __device__ __forceinline__ void score_seeds(const TemporalArgs& a, int block) {
     const int64_t key = seeds[i];
     if (key < 0 || key >= a.length) {
       a.ws.run[(size_t)row * a.k + i] = 0;  // below every score
+      a.ws.run_idx[(size_t)row * a.k + i] = 0xffffffffu;
       lowest = 0;
     } else {
       if constexpr (KF::kScaled)
@@ -292,6 +294,7 @@ __device__ __forceinline__ void score_seeds(const TemporalArgs& a, int block) {
       least = float_to_ordered(v);
       lowest = least;
       a.ws.run[(size_t)row * a.k + i] = least;
+      a.ws.run_idx[(size_t)row * a.k + i] = (uint32_t)key;
     }
   }
   // One atomic per wave and value: the minimum of its 64 seeds.
@@ -629,6 +632,7 @@ __global__ __launch_bounds__(256) void temporal_hist_kernel(TemporalArgs a) {
   const int chunks = (L + kSelectChunk - 1) / kSelectChunk;
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
+  if (a.ws.done[row]) return;  // finished by the dynamic rounds' last replay
   for (int i = tid; i < kSelectBins; i += 256) hist[i] = 0;
   __syncthreads();
   const float* srow = a.scores + (size_t)row * L;
@@ -836,6 +840,7 @@ int run_step(TemporalArgs& a, int32_t wave, int32_t key_dtype, int64_t* out_topk
     if (int st = temporal_static_fused(a, key_dtype, out_topk, s, ran)) return st;
     if (ran) return DSA_STATUS_OK;
   }
+  a.replay_topk = out_topk;  // the rounds' last replay may finish rows itself
   if (int st = temporal_scan(a, wave, key_dtype, s)) return st;
   return temporal_finish(a, out_topk, nullptr, s);
 }
@@ -859,7 +864,11 @@ int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, 
   const int chunks = (a.length + kSelectChunk - 1) / kSelectChunk;
   hipLaunchKernelGGL(temporal_hist_kernel, dim3(a.rows * chunks), dim3(256), 0, stream, a);
   if (int st = check_launch("temporal_hist_kernel")) return st;
-  if (int st = launch_select(a.scores, a.rows, a.length, a.k, a.ws.select, out_topk, nullptr, stream)) return st;
+  // Rows the dynamic rounds' last replay finished (ws.done, cleared by the
+  // prep) are skipped by the histogram and the select.
+  if (int st = launch_select(a.scores, a.rows, a.length, a.k, a.ws.select, out_topk, nullptr, stream, nullptr,
+                             nullptr, a.ws.done))
+    return st;
   if (a.policy_mode == 0) return DSA_STATUS_OK;
   StateArgs s = {};
   s.scores = a.scores;

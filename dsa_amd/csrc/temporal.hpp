@@ -32,6 +32,8 @@ struct TemporalWorkspace {
   uint32_t* floor;      // [rows] least of run (the k-th largest evaluated score), dynamic rounds
   uint32_t* loaded;     // [rows] key rows a dynamic step loaded (seeds + every key of its rounds' scored blocks)
   uint32_t* run;        // [rows][k] ordered keys of the k largest evaluated scores
+  uint32_t* run_idx;    // [rows][k] dynamic rounds: the key of each run entry (0xffffffff: a copy of the threshold)
+  uint32_t* done;       // [rows] dynamic rounds: the last replay wrote the row's top-k and keys scored
   uint32_t* order;      // [rows][blocks] block ids in scan order
   double* upper;        // [rows][blocks] U_b, in double like the float64 reference
   double* upper_pos;    // [rows][blocks] the same, by scan position
@@ -71,7 +73,9 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   const int64_t floor_off = tau_off + round(rows * 4);
   const int64_t loaded_off = floor_off + round(rows * 4);
   const int64_t run_off = loaded_off + round(rows * 4);
-  const int64_t order_off = run_off + round(rows * k * 4);
+  const int64_t run_idx_off = run_off + round(rows * k * 4);
+  const int64_t done_off = run_idx_off + round(rows * k * 4);
+  const int64_t order_off = done_off + round(rows * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
   const int64_t upos_off = upper_off + round(rows * blocks * 8);
   const int64_t shi_off = upos_off + round(rows * blocks * 8);
@@ -95,6 +99,8 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   ws.floor = base ? reinterpret_cast<uint32_t*>(p + floor_off) : nullptr;
   ws.loaded = base ? reinterpret_cast<uint32_t*>(p + loaded_off) : nullptr;
   ws.run = base ? reinterpret_cast<uint32_t*>(p + run_off) : nullptr;
+  ws.run_idx = base ? reinterpret_cast<uint32_t*>(p + run_idx_off) : nullptr;
+  ws.done = base ? reinterpret_cast<uint32_t*>(p + done_off) : nullptr;
   ws.order = base ? reinterpret_cast<uint32_t*>(p + order_off) : nullptr;
   ws.upper = base ? reinterpret_cast<double*>(p + upper_off) : nullptr;
   ws.upper_pos = base ? reinterpret_cast<double*>(p + upos_off) : nullptr;
@@ -139,6 +145,8 @@ struct TemporalArgs {
   float* scores;          // [rows][length]
   uint8_t* evaluated;     // [rows][blocks]
   int32_t* qk_scored;     // [rows]
+  int64_t* replay_topk;   // [rows][k] or null: the dynamic rounds' last replay writes the top-k and keys scored
+                          // where it can (then ws.done[row] is set and the finishing select skips the row)
   int32_t* waits_given_up;  // [rows] or null: fused static workgroups whose wait for the row's seed minima ran out
   int32_t rows, length, k, block_size, blocks, prev_length, prev_blocks;
   int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper, 3 order_key

@@ -722,35 +722,123 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       sh.cut_bin = bin;
       sh.n_out = 0;
     }
-    if (!rp.last_round) {
+    if (!rp.last_round || a.replay_topk) {
       const uint32_t t = exact_tau();
       if (lane == 0) sh.tau = t;
     }
   }
   __syncthreads();
+  // After the loop the LDS key arrays are free: sh.item and sh.val serve as
+  // staging (in the spill case they were never used).
+  const int bs = a.block_size;
+  const int L = a.length;
+  const uint32_t t = sh.tau;
+  const uint32_t* run_in = a.ws.run + (size_t)row * k;
+  const uint32_t* idx_in = a.ws.run_idx + (size_t)row * k;
+  // A listed key joined iff its block was kept (every listed key's block was
+  // decided by this round).
+  auto listed_joined = [&](uint64_t x) { return sh.kept[((uint32_t)(x >> 32) & 0x1ffffu) / (uint32_t)bs] != 0; };
   if (!rp.last_round) {
-    // The next round starts from the exact k largest: the joined keys above
-    // the threshold, then copies of it.
-    const uint32_t t = sh.tau;
-    const uint32_t s0 = sh.cut_bin ? sh.end[sh.cut_bin - 1] : 0u;
-    const uint32_t s1 = sh.end[kBins - 1];
-    for (uint32_t i = s0 + (uint32_t)tid; i < s1; i += kResolveThreads) {
-      const uint32_t v = val[i];
-      if (join[i] && v > t)
-        a.ws.run[(size_t)row * k +
-                 __hip_atomic_fetch_add(&sh.n_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)] = v;
+    // The next round starts from the exact k largest, each with its key: the
+    // joined keys above the threshold (the run's and the listed ones), then
+    // copies of it.  The run is staged in LDS first, as it is rewritten.
+    for (int i = tid; i < k; i += kResolveThreads) {
+      sh.item[i] = run_in[i];
+      sh.val[i] = idx_in[i];
     }
     __syncthreads();
-    for (uint32_t c = sh.n_out + (uint32_t)tid; c < (uint32_t)k; c += kResolveThreads)
-      a.ws.run[(size_t)row * k + c] = t;
+    uint32_t* run_out = a.ws.run + (size_t)row * k;
+    uint32_t* idx_out = a.ws.run_idx + (size_t)row * k;
+    auto emit = [&](uint32_t v, uint32_t key) {
+      const uint32_t j = __hip_atomic_fetch_add(&sh.n_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      run_out[j] = v;
+      idx_out[j] = key;
+    };
+    for (int i = tid; i < k; i += kResolveThreads)
+      if (sh.item[i] > t) emit(sh.item[i], sh.val[i]);
+    for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
+      const uint64_t x = list[e];
+      if ((uint32_t)x > t && listed_joined(x)) emit((uint32_t)x, (uint32_t)(x >> 32) & 0x1ffffu);
+    }
+    __syncthreads();
+    for (uint32_t c = sh.n_out + (uint32_t)tid; c < (uint32_t)k; c += kResolveThreads) {
+      run_out[c] = t;
+      idx_out[c] = 0xffffffffu;
+    }
     if (tid == 0) {
       a.ws.tau[row] = t;
       a.ws.floor[row] = t;
     }
+  } else if (a.replay_topk && t > floor_key && t > 0x007fffffu && t <= 0xff800000u) {
+    // The step's top-k, when the last threshold lies above this round's floor
+    // and is a number above -inf: every evaluated key at or above it is then
+    // a joined key with a known index (evaluated keys left out of the joined
+    // set are at or below the floor, and so are the run's copies), and when
+    // exactly k of them are, they are the k largest of the scores row, -inf
+    // elsewhere, with no tie to break.  Otherwise (ties across the cut,
+    // repeated seeds) the histogram select does it.  The chosen keys are
+    // marked in a bitmap over the row (sh.item) and written in index order.
+    const uint32_t words = (uint32_t)(L + 31) / 32u;  // at most 4096 (L <= 2^17)
+    for (uint32_t w = (uint32_t)tid; w < words; w += kResolveThreads) sh.item[w] = 0u;
+    __syncthreads();
+    uint32_t chosen = 0u;
+    auto mark = [&](uint32_t key) {
+      ++chosen;
+      if (key < (uint32_t)L) __hip_atomic_fetch_or(&sh.item[key >> 5], 1u << (key & 31u), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+      else chosen += 1u << 20;  // no index: not this path
+    };
+    for (int i = tid; i < k; i += kResolveThreads)
+      if (run_in[i] >= t) mark(idx_in[i]);
+    for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
+      const uint64_t x = list[e];
+      if ((uint32_t)x >= t && listed_joined(x)) mark((uint32_t)(x >> 32) & 0x1ffffu);
+    }
+    uint32_t total;
+    block_excl_scan<kResolveWaves>(chosen, sh.wsum, total);  // its barrier also ends the marking
+    if (total == (uint32_t)k) {
+      constexpr int kWordsPer = (1 << 17) / 32 / kResolveThreads;
+      const uint32_t w0 = (uint32_t)tid * kWordsPer;
+      uint32_t bits[kWordsPer];
+      uint32_t n_bits = 0u;
+#pragma unroll
+      for (int j = 0; j < kWordsPer; ++j) {
+        bits[j] = w0 + j < words ? sh.item[w0 + j] : 0u;
+        n_bits += (uint32_t)__builtin_popcount(bits[j]);
+      }
+      __syncthreads();  // the previous scan's sums are read
+      uint32_t marked;
+      uint32_t at = block_excl_scan<kResolveWaves>(n_bits, sh.wsum, marked);
+      if (marked == (uint32_t)k) {  // (repeated seeds would mark fewer)
+        int64_t* out = a.replay_topk + (size_t)row * k;
+#pragma unroll
+        for (int j = 0; j < kWordsPer; ++j)
+          for (uint32_t b = bits[j]; b; b &= b - 1u) out[at++] = (int64_t)((w0 + j) * 32u + (uint32_t)__builtin_ctz(b));
+        // Keys scored: the seeds and every key of a kept block, each once.
+        const int nb = a.blocks;
+        const uint32_t* mask = a.ws.seed_mask + (size_t)row * words;
+        uint32_t scored = 0u;
+        for (uint32_t w = (uint32_t)tid; w < words; w += kResolveThreads) {
+          uint32_t m = mask[w];
+          for (uint32_t sub = 0; sub < 32u; sub += 16u) {  // blocks are multiples of 16 keys
+            const int blk = (int)((w * 32u + sub) / (uint32_t)bs);
+            if (blk < nb && a.evaluated[(size_t)row * nb + blk]) m |= 0xffffu << sub;
+          }
+          const uint32_t valid = min(32u, (uint32_t)L - w * 32u);
+          if (valid < 32u) m &= (1u << valid) - 1u;
+          scored += (uint32_t)__builtin_popcount(m);
+        }
+        __syncthreads();
+        uint32_t qk;
+        block_excl_scan<kResolveWaves>(scored, sh.wsum, qk);
+        if (tid == 0) {
+          a.qk_scored[row] = (int32_t)qk;
+          a.ws.done[row] = 1u;
+        }
+      }
+    }
   }
   // Scored blocks the replay pruned: their keys back to -inf, seeds excepted.
-  const int bs = a.block_size;
-  const int L = a.length;
   int bs_shift = 4;
   while ((1 << bs_shift) < bs) ++bs_shift;
   const uint32_t nreset = sh.nreset;
@@ -803,15 +891,15 @@ __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(Tempo
 
 // Round splits, as fractions of the scan's groups: DSA_AMD_TEMPORAL_ROUNDS, a
 // comma-separated increasing list in (0, 1), or "1" for a single round (read
-// at every step).  By default one split at a quarter of the scan, and two
-// (a tenth, three tenths) for rows of 64K keys or more, whose later rounds
-// gain more from a floor raised early (C3 at 16K keys: 124-148 us per step
-// with one split, 139-162 with two; C5 at 128K: 296-342 us with one,
-// 196-246 with two).
-std::vector<double> round_splits(int length) {
+// at every step).  By default one split at a tenth of the scan: the first
+// round raises the floor early, and the replay's multi-group steps make a
+// long second round cheap (in one A/B run, C3 at 16K keys: 95-117 us per
+// step against 98-120 with a split at a quarter and 117-144 with none; C5 at
+// 128K: 184-268 us against 197-268 with splits at a tenth and three tenths).
+std::vector<double> round_splits(int) {
   std::vector<double> splits;
   const char* v = std::getenv("DSA_AMD_TEMPORAL_ROUNDS");
-  const char* s = v ? v : (length >= 65536 ? "0.1,0.3" : "0.25");
+  const char* s = v ? v : "0.1";
   double last = 0.0;
   while (*s) {
     char* end = nullptr;
