@@ -192,29 +192,37 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
     return v;
   };
 
+  // The wave's first unit is loaded now, before the threshold is known, with
+  // every tile but the seeds' rows: its latency then overlaps the seed phase
+  // and the exchange, and the tiles the decisions prune are discarded (a
+  // static step so loads at most one unit per wave of pruned keys).
+  constexpr int NB = KF::kBuffers;
+  uint4 buf[NB][4][KF::kRaw];
+  if (units > wave) load_unit(wave, 0xfu, buf[0]);
+
   // 1. The chunk's seeds, gathered 64 per wave-tile so that every wave's
   // loads are in flight together: only their key rows are loaded.
   uint32_t least = 0xffffffffu;
   {
     const uint32_t n_seeds = s_nseeds;
     const BufferRsrc row_rsrc = make_buffer(row_keys, (uint32_t)valid_bytes);
-    constexpr int kPerWave = 2;  // gathered tiles a wave loads before scoring them
+    constexpr int kPerWave = 1;  // gathered tiles a wave loads before scoring them (one: the first unit is held)
     for (uint32_t e0 = 64u * kPerWave * wave; e0 < n_seeds; e0 += 64u * kPerWave * kFusedWaves) {
-      uint4 buf[kPerWave][4][KF::kRaw];
+      uint4 sbuf[kPerWave][4][KF::kRaw];
 #pragma unroll
       for (int q = 0; q < kPerWave; ++q)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const uint32_t e = e0 + 64u * q + 16u * t + (uint32_t)r;
           const int key = e < n_seeds ? base + (int)seed_list[e] : (int)kFarKey;
-          KF::load_buf(row_rsrc, key, g, buf[q][t]);
+          KF::load_buf(row_rsrc, key, g, sbuf[q][t]);
         }
 #pragma unroll
       for (int q = 0; q < kPerWave; ++q) {
         const uint32_t e = e0 + 64u * q + (uint32_t)lane;  // lane l holds entry e0 + 64q + l
         float sc[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[q][t]);
+        for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, sbuf[q][t]);
         float v = unit_reduce(sc, g);
         if (e < n_seeds) {
           const int local = seed_list[e];
@@ -320,11 +328,9 @@ __global__ __launch_bounds__(kFusedThreads, 2) void temporal_static_kernel(Tempo
       __hip_atomic_fetch_add(&hist[float_to_ordered(s) >> 20], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   };
   if (count_units > 0) {
-    constexpr int NB = KF::kBuffers;
     const int last = wave + kFusedWaves * (count_units - 1);
-    uint4 buf[NB][4][KF::kRaw];
 #pragma unroll
-    for (int s = 0; s < NB - 1; ++s) {
+    for (int s = 1; s < NB - 1; ++s) {  // (unit 0, the wave's first, is in flight already)
       const int ul = min(wave + kFusedWaves * s, last);
       load_unit(ul, tiles_of(ul), buf[s]);
     }
