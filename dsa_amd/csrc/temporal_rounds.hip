@@ -891,15 +891,19 @@ __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(Tempo
 
 // Round splits, as fractions of the scan's groups: DSA_AMD_TEMPORAL_ROUNDS, a
 // comma-separated increasing list in (0, 1), or "1" for a single round (read
-// at every step).  By default one split at a tenth of the scan: the first
-// round raises the floor early, and the replay's multi-group steps make a
-// long second round cheap (in one A/B run, C3 at 16K keys: 95-117 us per
-// step against 98-120 with a split at a quarter and 117-144 with none; C5 at
-// 128K: 184-268 us against 197-268 with splits at a tenth and three tenths).
-std::vector<double> round_splits(int) {
+// at every step).  By default one split at a quarter of the scan, and two
+// (a tenth, three tenths) for rows of 64K keys or more.  Each later round
+// starts from a higher floor, so fewer of its blocks are scored and then
+// pruned: fewer splits are faster but load more key bytes (C5 with a single
+// split at a tenth: from as fast to 18 us faster per step, but 0.21 instead
+// of 0.38 of the dense key bytes not loaded at gamma_sigma -0.25, and 0.017
+// instead of 0.061 at 1.0; C3 with a split at a tenth: 2-3 us faster, 0
+// instead of 0.0019 not loaded for the block-16 address scan at gamma_sigma
+// 1.0).
+std::vector<double> round_splits(int length) {
   std::vector<double> splits;
   const char* v = std::getenv("DSA_AMD_TEMPORAL_ROUNDS");
-  const char* s = v ? v : "0.1";
+  const char* s = v ? v : (length >= 65536 ? "0.1,0.3" : "0.25");
   double last = 0.0;
   while (*s) {
     char* end = nullptr;
