@@ -279,6 +279,7 @@ constexpr int kResolveWaves = kResolveThreads / kWave;
 constexpr int kSortCap = 8192;  // keys the replay sorts in LDS (more: in the workspace)
 constexpr int kBins = 4096;
 constexpr int kCutDigits = 1024;  // 10-bit digits of the select inside the cut bin
+constexpr int kKeyBatch = 8;      // key values per thread in flight in the replay's first read
 
 struct ResolveShared {
   uint32_t val[kSortCap];   // ordered keys, by bin
@@ -298,7 +299,7 @@ struct ResolveShared {
   uint16_t risky_pos[kMaxTemporalBlocks];
   uint32_t digits[kCutDigits];
   uint32_t wsum[kResolveWaves];
-  uint32_t above, max_key, nreset, tau, cut_bin, n_out, bin_hi, n_risky;
+  uint32_t above, nreset, tau, cut_bin, n_out, bin_hi, n_risky;
 };
 
 // The j-th largest (1-based) of the joined keys in slots [s0, s1) of bin `bin`
@@ -358,7 +359,7 @@ __device__ __forceinline__ uint32_t cut_select(P32 val, P8 join, uint32_t s0, ui
 
 template <bool kSpill>
 __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPlan& rp, ResolveShared& sh,
-                                            uint32_t n_listed, uint64_t t_start) {
+                                            uint32_t n_listed, uint32_t max_key, uint64_t t_start) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -370,7 +371,6 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
   const int n_groups = (rp.pos_end + W - 1) / W - g_begin;
   const int n_pos = rp.pos_end - rp.pos_begin;
   const uint32_t floor_key = a.ws.floor[row];
-  const uint32_t max_key = sh.max_key;
   const uint32_t span = max_key - floor_key;
   const uint32_t shift = span < (uint32_t)kBins ? 0u : 32u - (uint32_t)__builtin_clz(span) - 12u;
   const size_t spill_at = (size_t)row * a.ws.spill_capacity;
@@ -863,30 +863,67 @@ __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(Tempo
   const int nb = a.blocks;
   const int k = a.k;
   const int n_pos = rp.pos_end - rp.pos_begin;
-  const auto* order = a.ws.order + (size_t)row * nb + rp.pos_begin;
+  const int wave = tid >> 6;
+  const uint32_t* order = a.ws.order + (size_t)row * nb + rp.pos_begin;
   const double* upper = a.ws.upper_pos + (size_t)row * nb + rp.pos_begin;
-  batched<4>((uint32_t)tid, (uint32_t)n_pos, kResolveThreads, [&](uint32_t i) { return order[i]; },
-             [&](uint32_t i, auto b) { sh.blk[i] = (uint16_t)b; });
-  batched<4>((uint32_t)tid, (uint32_t)n_pos, kResolveThreads, [&](uint32_t i) { return upper[i]; },
-             [&](uint32_t i, double u) { sh.uk[i] = upper_key(u); });
-  if (tid == 0) sh.max_key = 0;
-  __syncthreads();
-  // Keys to sort and their largest (the span of the bins).
   const uint32_t* run = a.ws.run + (size_t)row * k;
   const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
+  // The setup's inputs are read in one round trip: the positions' blocks and
+  // bounds (at most four per thread), the list's length, and the first
+  // kKeyBatch key values per thread, each from the running k largest or the
+  // list (one dword: an entry's value is its low word), list reads clamped
+  // to its capacity until its length is known.
   const uint32_t n_listed = a.ws.list_total[(size_t)row * kMaxRounds + rp.round];
+  constexpr int kPosPer = kMaxTemporalBlocks / kResolveThreads;
+  uint32_t pb[kPosPer];
+  double pu[kPosPer];
+#pragma unroll
+  for (int j = 0; j < kPosPer; ++j) {
+    const int i = max(min(tid + j * kResolveThreads, n_pos - 1), 0);
+    pb[j] = order[i];
+    pu[j] = upper[i];
+  }
+  const uint32_t cap_last = (uint32_t)a.ws.list_capacity - 1u;
+  auto key_value = [&](uint32_t i, uint32_t last) {
+    const uint32_t e = min(i - (uint32_t)k, last);  // (wraps below k: clamped, unused)
+    const uint32_t* p = i < (uint32_t)k ? run + i : reinterpret_cast<const uint32_t*>(list + e);
+    return *p;
+  };
+  uint32_t kv[kKeyBatch];
+#pragma unroll
+  for (int j = 0; j < kKeyBatch; ++j) kv[j] = key_value((uint32_t)(tid + j * kResolveThreads), cap_last);
+#pragma unroll
+  for (int j = 0; j < kPosPer; ++j) {
+    const int i = tid + j * kResolveThreads;
+    if (i < n_pos) {
+      sh.blk[i] = (uint16_t)pb[j];
+      sh.uk[i] = upper_key(pu[j]);
+    }
+  }
+  // The largest key (the span of the bins): per wave, then over the waves.
+  const uint32_t n_keys = (uint32_t)k + n_listed;
   uint32_t mx = 0;
-  batched<4>((uint32_t)tid, (uint32_t)k, kResolveThreads, [&](uint32_t i) { return run[i]; },
-             [&](uint32_t, uint32_t v) { mx = max(mx, v); });
-  batched<4>((uint32_t)tid, n_listed, kResolveThreads, [&](uint32_t e) { return list[e]; },
-             [&](uint32_t, uint64_t x) { mx = max(mx, (uint32_t)x); });
+#pragma unroll
+  for (int j = 0; j < kKeyBatch; ++j)
+    if ((uint32_t)(tid + j * kResolveThreads) < n_keys) mx = max(mx, kv[j]);
+  const uint32_t list_last = n_listed ? n_listed - 1u : 0u;
+  for (uint32_t i0 = (uint32_t)tid + kKeyBatch * kResolveThreads; i0 < n_keys; i0 += kKeyBatch * kResolveThreads) {
+#pragma unroll
+    for (int j = 0; j < kKeyBatch; ++j) kv[j] = key_value(i0 + (uint32_t)(j * kResolveThreads), list_last);
+#pragma unroll
+    for (int j = 0; j < kKeyBatch; ++j)
+      if (i0 + (uint32_t)(j * kResolveThreads) < n_keys) mx = max(mx, kv[j]);
+  }
   for (int off = 32; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, kWave));
-  if (lane == 0) __hip_atomic_fetch_max(&sh.max_key, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (lane == 0) sh.wsum[wave] = mx;
   __syncthreads();
-  if ((uint32_t)k + n_listed <= (uint32_t)kSortCap)
-    resolve_row<false>(a, rp, sh, n_listed, t_start);
+  uint32_t max_key = 0;
+#pragma unroll
+  for (int w = 0; w < kResolveWaves; ++w) max_key = max(max_key, sh.wsum[w]);
+  if (n_keys <= (uint32_t)kSortCap)
+    resolve_row<false>(a, rp, sh, n_listed, max_key, t_start);
   else
-    resolve_row<true>(a, rp, sh, n_listed, t_start);
+    resolve_row<true>(a, rp, sh, n_listed, max_key, t_start);
 }
 
 // Round splits, as fractions of the scan's groups: DSA_AMD_TEMPORAL_ROUNDS, a
