@@ -96,6 +96,13 @@ int launch_select_scores(const float* scores, int64_t rows, int64_t length, int6
 // Selects the top-k of scores [rows, length] whose histogram is in ws.
 // start/stop, when not null, are recorded by the first and last kernel at
 // their own start and end (hipExtLaunchKernel).
+// The exact top-k (stable ties, index order) of each row of at most
+// kTopkRowsMaxLength scores, one workgroup per row; rows with skip[row] != 0
+// (skip nullable) are left as they are.
+constexpr int64_t kTopkRowsMaxLength = 32768;
+int launch_topk_rows(const float* scores, int64_t rows, int64_t length, int64_t k, int64_t* out_idx,
+                     const uint32_t* skip, hipStream_t stream);
+
 int launch_select(const float* scores, int64_t rows, int64_t length, int64_t k,
                   const SelectWorkspace& ws, int64_t* out_idx, float* out_val,
                   hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr,

@@ -840,8 +840,17 @@ int run_step(TemporalArgs& a, int32_t wave, int32_t key_dtype, int64_t* out_topk
     if (int st = temporal_static_fused(a, key_dtype, out_topk, s, ran)) return st;
     if (ran) return DSA_STATUS_OK;
   }
-  a.replay_topk = out_topk;  // the rounds' last replay may finish rows itself
+  // Dynamic rounds: the last replay writes the top-k of the rows it can and,
+  // for rows a one-workgroup top-k holds, every row's keys scored, so that
+  // only that top-k runs after it (on the rows the replay left).
+  const bool rounds = wave > 0 && !legacy_paths_forced();
+  a.replay_topk = rounds ? out_topk : nullptr;
+  a.replay_qk = rounds && a.length <= kTopkRowsMaxLength;
   if (int st = temporal_scan(a, wave, key_dtype, s)) return st;
+  if (a.replay_qk) {
+    if (int st = launch_topk_rows(a.scores, a.rows, a.length, a.k, out_topk, a.ws.done, s)) return st;
+    return policy_state(a, out_topk, nullptr, s);
+  }
   return temporal_finish(a, out_topk, nullptr, s);
 }
 
@@ -869,6 +878,10 @@ int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, 
   if (int st = launch_select(a.scores, a.rows, a.length, a.k, a.ws.select, out_topk, nullptr, stream, nullptr,
                              nullptr, a.ws.done))
     return st;
+  return policy_state(a, out_topk, rescued, stream);
+}
+
+int policy_state(TemporalArgs& a, const int64_t* out_topk, const uint8_t* rescued, hipStream_t stream) {
   if (a.policy_mode == 0) return DSA_STATUS_OK;
   StateArgs s = {};
   s.scores = a.scores;

@@ -147,6 +147,7 @@ struct TemporalArgs {
   int32_t* qk_scored;     // [rows]
   int64_t* replay_topk;   // [rows][k] or null: the dynamic rounds' last replay writes the top-k and keys scored
                           // where it can (then ws.done[row] is set and the finishing select skips the row)
+  int32_t replay_qk;      // with replay_topk: the last replay writes the keys scored of every row
   int32_t* waits_given_up;  // [rows] or null: fused static workgroups whose wait for the row's seed minima ran out
   int32_t rows, length, k, block_size, blocks, prev_length, prev_blocks;
   int32_t scan_order;     // 0 address, 1 previous-hot, 2 upper, 3 order_key
@@ -339,6 +340,10 @@ int temporal_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t 
 // top-k of the scores row into out_topk, and (policy mode) the state update
 // of every block refreshed by the scan or flagged in `rescued` (may be null).
 int temporal_finish(TemporalArgs& a, int64_t* out_topk, const uint8_t* rescued, hipStream_t stream);
+
+// The policy-mode state update alone (nothing in replay-filter mode), after
+// the top-k is in out_topk.
+int policy_state(TemporalArgs& a, const int64_t* out_topk, const uint8_t* rescued, hipStream_t stream);
 
 // The static replay-filter step (wave 0, no policy, live keys) as one
 // scoring launch plus the candidate-list select.  Returns

@@ -769,72 +769,80 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       a.ws.tau[row] = t;
       a.ws.floor[row] = t;
     }
-  } else if (a.replay_topk && t > floor_key && t > 0x007fffffu && t <= 0xff800000u) {
+  } else if (a.replay_topk) {
     // The step's top-k, when the last threshold lies above this round's floor
     // and is a number above -inf: every evaluated key at or above it is then
     // a joined key with a known index (evaluated keys left out of the joined
     // set are at or below the floor, and so are the run's copies), and when
     // exactly k of them are, they are the k largest of the scores row, -inf
     // elsewhere, with no tie to break.  Otherwise (ties across the cut,
-    // repeated seeds) the histogram select does it.  The chosen keys are
-    // marked in a bitmap over the row (sh.item) and written in index order.
+    // repeated seeds) the top-k launched after the rounds does it.  The chosen
+    // keys are marked in a bitmap over the row (sh.item) and written in index
+    // order.
     const uint32_t words = (uint32_t)(L + 31) / 32u;  // at most 4096 (L <= 2^17)
-    for (uint32_t w = (uint32_t)tid; w < words; w += kResolveThreads) sh.item[w] = 0u;
-    __syncthreads();
-    uint32_t chosen = 0u;
-    auto mark = [&](uint32_t key) {
-      ++chosen;
-      if (key < (uint32_t)L) __hip_atomic_fetch_or(&sh.item[key >> 5], 1u << (key & 31u), __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-      else chosen += 1u << 20;  // no index: not this path
-    };
-    for (int i = tid; i < k; i += kResolveThreads)
-      if (run_in[i] >= t) mark(idx_in[i]);
-    for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
-      const uint64_t x = list[e];
-      if ((uint32_t)x >= t && listed_joined(x)) mark((uint32_t)(x >> 32) & 0x1ffffu);
-    }
-    uint32_t total;
-    block_excl_scan<kResolveWaves>(chosen, sh.wsum, total);  // its barrier also ends the marking
-    if (total == (uint32_t)k) {
-      constexpr int kWordsPer = (1 << 17) / 32 / kResolveThreads;
-      const uint32_t w0 = (uint32_t)tid * kWordsPer;
-      uint32_t bits[kWordsPer];
-      uint32_t n_bits = 0u;
+    bool finished = false;  // uniform over the workgroup
+    if (t > floor_key && t > 0x007fffffu && t <= 0xff800000u) {
+      for (uint32_t w = (uint32_t)tid; w < words; w += kResolveThreads) sh.item[w] = 0u;
+      __syncthreads();
+      uint32_t chosen = 0u;
+      auto mark = [&](uint32_t key) {
+        ++chosen;
+        if (key < (uint32_t)L) __hip_atomic_fetch_or(&sh.item[key >> 5], 1u << (key & 31u), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+        else chosen += 1u << 20;  // no index: not this path
+      };
+      for (int i = tid; i < k; i += kResolveThreads)
+        if (run_in[i] >= t) mark(idx_in[i]);
+      for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
+        const uint64_t x = list[e];
+        if ((uint32_t)x >= t && listed_joined(x)) mark((uint32_t)(x >> 32) & 0x1ffffu);
+      }
+      uint32_t total;
+      block_excl_scan<kResolveWaves>(chosen, sh.wsum, total);  // its barrier also ends the marking
+      if (total == (uint32_t)k) {
+        constexpr int kWordsPer = (1 << 17) / 32 / kResolveThreads;
+        const uint32_t w0 = (uint32_t)tid * kWordsPer;
+        uint32_t bits[kWordsPer];
+        uint32_t n_bits = 0u;
 #pragma unroll
-      for (int j = 0; j < kWordsPer; ++j) {
-        bits[j] = w0 + j < words ? sh.item[w0 + j] : 0u;
-        n_bits += (uint32_t)__builtin_popcount(bits[j]);
+        for (int j = 0; j < kWordsPer; ++j) {
+          bits[j] = w0 + j < words ? sh.item[w0 + j] : 0u;
+          n_bits += (uint32_t)__builtin_popcount(bits[j]);
+        }
+        __syncthreads();  // the previous scan's sums are read
+        uint32_t marked;
+        uint32_t at = block_excl_scan<kResolveWaves>(n_bits, sh.wsum, marked);
+        if (marked == (uint32_t)k) {  // (repeated seeds would mark fewer)
+          int64_t* out = a.replay_topk + (size_t)row * k;
+#pragma unroll
+          for (int j = 0; j < kWordsPer; ++j)
+            for (uint32_t b = bits[j]; b; b &= b - 1u)
+              out[at++] = (int64_t)((w0 + j) * 32u + (uint32_t)__builtin_ctz(b));
+          finished = true;
+        }
+      }
+    }
+    if (finished || a.replay_qk) {
+      // Keys scored: the seeds and every key of a kept block, each once.
+      const int nb = a.blocks;
+      const uint32_t* mask = a.ws.seed_mask + (size_t)row * words;
+      uint32_t scored = 0u;
+      for (uint32_t w = (uint32_t)tid; w < words; w += kResolveThreads) {
+        uint32_t m = mask[w];
+        for (uint32_t sub = 0; sub < 32u; sub += 16u) {  // blocks are multiples of 16 keys
+          const int blk = (int)((w * 32u + sub) / (uint32_t)bs);
+          if (blk < nb && a.evaluated[(size_t)row * nb + blk]) m |= 0xffffu << sub;
+        }
+        const uint32_t valid = min(32u, (uint32_t)L - w * 32u);
+        if (valid < 32u) m &= (1u << valid) - 1u;
+        scored += (uint32_t)__builtin_popcount(m);
       }
       __syncthreads();  // the previous scan's sums are read
-      uint32_t marked;
-      uint32_t at = block_excl_scan<kResolveWaves>(n_bits, sh.wsum, marked);
-      if (marked == (uint32_t)k) {  // (repeated seeds would mark fewer)
-        int64_t* out = a.replay_topk + (size_t)row * k;
-#pragma unroll
-        for (int j = 0; j < kWordsPer; ++j)
-          for (uint32_t b = bits[j]; b; b &= b - 1u) out[at++] = (int64_t)((w0 + j) * 32u + (uint32_t)__builtin_ctz(b));
-        // Keys scored: the seeds and every key of a kept block, each once.
-        const int nb = a.blocks;
-        const uint32_t* mask = a.ws.seed_mask + (size_t)row * words;
-        uint32_t scored = 0u;
-        for (uint32_t w = (uint32_t)tid; w < words; w += kResolveThreads) {
-          uint32_t m = mask[w];
-          for (uint32_t sub = 0; sub < 32u; sub += 16u) {  // blocks are multiples of 16 keys
-            const int blk = (int)((w * 32u + sub) / (uint32_t)bs);
-            if (blk < nb && a.evaluated[(size_t)row * nb + blk]) m |= 0xffffu << sub;
-          }
-          const uint32_t valid = min(32u, (uint32_t)L - w * 32u);
-          if (valid < 32u) m &= (1u << valid) - 1u;
-          scored += (uint32_t)__builtin_popcount(m);
-        }
-        __syncthreads();
-        uint32_t qk;
-        block_excl_scan<kResolveWaves>(scored, sh.wsum, qk);
-        if (tid == 0) {
-          a.qk_scored[row] = (int32_t)qk;
-          a.ws.done[row] = 1u;
-        }
+      uint32_t qk;
+      block_excl_scan<kResolveWaves>(scored, sh.wsum, qk);
+      if (tid == 0) {
+        a.qk_scored[row] = (int32_t)qk;
+        if (finished) a.ws.done[row] = 1u;
       }
     }
   }

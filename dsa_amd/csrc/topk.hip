@@ -11,6 +11,7 @@
 // chosen elements are written in index order, or bitonic-sorted in LDS by
 // (value desc, index asc) when a sorted result is requested.
 #include "common.hpp"
+#include "select.hpp"
 #include "status.hpp"
 
 namespace dsa {
@@ -39,6 +40,7 @@ struct TopkArgs {
   int32_t sorted;
   int64_t* out_idx;
   float* out_val;
+  const uint32_t* skip;  // [rows] or null: rows with a nonzero flag are left as they are
 };
 
 template <int THREADS, int CAP>
@@ -173,6 +175,7 @@ __global__ __launch_bounds__(THREADS) void topk_kernel(TopkArgs a) {
   const int64_t v = (int64_t)gridDim.x - 1 - blockIdx.x;
   const int64_t row = v / a.chunks;
   const int chunk = (int)(v % a.chunks);
+  if (a.skip && a.skip[row]) return;
   int row_len = a.length;
   if (a.row_lengths) row_len = min(row_len, max(0, a.row_lengths[row]));
   const int start = chunk * a.chunk_len;
@@ -443,8 +446,30 @@ int launch_topk(const TopkArgs& a, int64_t virtual_rows, hipStream_t stream) {
 
 constexpr int64_t kMaxRowLen = int64_t(kTopkThreads) * 32;
 constexpr int64_t kLongChunk = 32768;
+static_assert(kMaxRowLen == kTopkRowsMaxLength, "one-workgroup rows");
 
 }  // namespace
+
+int launch_topk_rows(const float* scores, int64_t rows, int64_t length, int64_t k, int64_t* out_idx,
+                     const uint32_t* skip, hipStream_t stream) {
+  DSA_REQUIRE(length > 0 && length <= kMaxRowLen && k > 0 && k <= kMaxK, "rows of %lld for k=%lld",
+              (long long)length, (long long)k);
+  TopkArgs a;
+  a.scores = scores;
+  a.in_idx = nullptr;
+  a.row_stride = length;
+  a.row_lengths = nullptr;
+  a.length = (int32_t)length;
+  a.chunks = 1;
+  a.chunk_len = (int32_t)length;
+  a.k = (int32_t)k;
+  a.sorted = 0;
+  a.out_idx = out_idx;
+  a.out_val = nullptr;
+  a.skip = skip;
+  return launch_topk(a, rows, stream);
+}
+
 }  // namespace dsa
 
 using namespace dsa;
@@ -471,6 +496,7 @@ extern "C" int dsa_topk(const float* scores, const int64_t* in_indices, int64_t 
   a.sorted = sorted ? 1 : 0;
   a.out_idx = out_indices;
   a.out_val = out_values;
+  a.skip = nullptr;
   return launch_topk(a, rows, static_cast<hipStream_t>(stream));
 }
 
@@ -513,6 +539,7 @@ extern "C" int dsa_topk_long(const float* scores, int64_t rows, int64_t length, 
   a.sorted = 0;
   a.out_idx = cand_idx;
   a.out_val = cand_val;
+  a.skip = nullptr;
   if (int st = launch_topk(a, rows * chunks, s)) return st;
   // Stage 2: exact merge of the candidates (ties break on the global index).
   return dsa_topk(cand_val, cand_idx, rows, chunks * k, chunks * k, nullptr, k, sorted,
