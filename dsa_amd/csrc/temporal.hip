@@ -40,6 +40,8 @@ __host__ __device__ inline bool ranked_order(const TemporalArgs& a) {
   return sorted && !(policy && a.ap.p.order == DSA_ORDER_BUCKET);
 }
 
+constexpr int kPrepClearKeys = 16384;  // scores each clearing workgroup of the prep sets to -inf
+
 // Bounds, scan order and a clean slate for one row (one workgroup per row).
 // Replay filter: U_b = prev max + gamma, +inf for blocks with new keys, order
 // (previous-hot first,) larger U, lower address.  Policy: U_b = risk, or +inf
@@ -53,12 +55,20 @@ __global__ __launch_bounds__(1024) void temporal_prep_kernel(TemporalArgs a) {
   __shared__ double s_rank[kMaxTemporalBlocks];
   __shared__ uint32_t s_exact;
   const int tid = threadIdx.x;
-  const int row = blockIdx.x;
   const int L = a.length;
+  if ((int)blockIdx.x >= a.rows) {
+    // The workgroups past the rows clear the scores rows, kPrepClearKeys keys
+    // each, beside the row workgroups' work.
+    const int c = (int)blockIdx.x - a.rows;
+    const int parts = (L + kPrepClearKeys - 1) / kPrepClearKeys;
+    float* srow = a.scores + (size_t)(c / parts) * L;
+    const int k1 = min(L, (c % parts + 1) * kPrepClearKeys);
+    for (int i = (c % parts) * kPrepClearKeys + tid; i < k1; i += 1024) srow[i] = -__builtin_inff();
+    return;
+  }
+  const int row = blockIdx.x;
   const int nb = a.blocks;
   const int bs = a.block_size;
-  float* srow = a.scores + (size_t)row * L;
-  for (int i = tid; i < L; i += 1024) srow[i] = -__builtin_inff();
   const int words = (L + 31) / 32;
   for (int i = tid; i < words; i += 1024) a.ws.seed_mask[(size_t)row * words + i] = 0;
   for (int i = tid; i < nb; i += 1024) a.evaluated[(size_t)row * nb + i] = 0;
@@ -796,7 +806,8 @@ __global__ __launch_bounds__(1024) void approx_state_kernel(StateArgs s) {
 
 template <class Tag, class KF>
 int launch_scan(TemporalArgs& a, int32_t wave, int32_t key_dtype, hipStream_t stream) {
-  hipLaunchKernelGGL(temporal_prep_kernel, dim3(a.rows), dim3(1024), 0, stream, a);
+  const int clear_parts = (a.length + kPrepClearKeys - 1) / kPrepClearKeys;
+  hipLaunchKernelGGL(temporal_prep_kernel, dim3(a.rows * (1 + clear_parts)), dim3(1024), 0, stream, a);
   if (int st = check_launch("temporal_prep_kernel")) return st;
   const int seed_wgs = a.rows * ((a.k + 255) / 256);
   if (ranked_order(a)) {

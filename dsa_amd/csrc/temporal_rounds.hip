@@ -173,13 +173,32 @@ __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalA
     const double up = a.ws.upper_pos[(size_t)row * nb + p];
     if (!prunes(upper_key(up), floor_key)) my_tiles = (uint32_t)((min(L, (blk + 1) * bs) - blk * bs + 15) >> 4);
   }
-  const uint32_t* mask = a.ws.seed_mask + (size_t)row * ((L + 31) / 32);
+  // The seed-mask words of the block's first eight tiles, read before the
+  // scan so that their latency overlaps it (one round trip, not one per tile).
+  const uint32_t words = (uint32_t)(L + 31) / 32u;
+  const uint32_t* mask = a.ws.seed_mask + (size_t)row * words;
+  const uint32_t key_first = (uint32_t)(blk * bs);
+  const uint32_t wbase = key_first >> 5;
+  const bool odd = (key_first & 16u) != 0u;  // the block starts in a word's upper half
+  uint32_t mw[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) mw[i] = my_tiles ? mask[min(wbase + (uint32_t)i, words - 1u)] : 0u;
   uint32_t total = 0;
   const uint32_t first = block_excl_scan<kRoundWaves>(my_tiles, s_wsum, total);
-  for (uint32_t j = 0; j < my_tiles; ++j) {
-    const uint32_t key0 = (uint32_t)(blk * bs) + 16u * j;  // tiles are 16-key aligned
+  const uint16_t group = (uint16_t)(p / rp.group);
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; ++j) {
+    if (j >= my_tiles) break;
+    const uint32_t key0 = key_first + 16u * j;  // tiles are 16-key aligned
+    const uint32_t word = odd ? mw[(j + 1u) >> 1] : mw[j >> 1];
     s_tile_key[first + j] = key0;
-    s_tile_group[first + j] = (uint16_t)(p / rp.group);
+    s_tile_group[first + j] = group;
+    s_tile_seeds[first + j] = (uint16_t)(word >> (key0 & 16u));
+  }
+  for (uint32_t j = 8u; j < my_tiles; ++j) {  // blocks of more than 128 keys
+    const uint32_t key0 = key_first + 16u * j;
+    s_tile_key[first + j] = key0;
+    s_tile_group[first + j] = group;
     s_tile_seeds[first + j] = (uint16_t)(mask[key0 >> 5] >> (key0 & 16u));
   }
   __syncthreads();
