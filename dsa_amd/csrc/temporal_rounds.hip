@@ -47,7 +47,8 @@ namespace {
 
 constexpr int kRoundThreads = 256;
 constexpr int kRoundWaves = kRoundThreads / kWave;
-constexpr int kRoundTiles = kRoundKeys / 16;
+constexpr int kRoundParts = 2;            // kRoundKeys spans of positions per wide workgroup
+constexpr int64_t kRoundWideSpans = 192;  // spans in a round from which its workgroups are wide
 static_assert(kRoundWaves * kRoundWaveKeys == kRoundKeys, "two 64-key units per scoring wave");
 
 #ifdef DSA_PHASE_TRACE
@@ -131,15 +132,18 @@ __device__ __forceinline__ void batched(uint32_t first, uint32_t n, uint32_t str
 
 // ---------------------------------------------------------------------------
 // 1. Scoring.  Workgroup (row, part) covers scan positions
-// [pos_begin + part * per_wg, + per_wg) of the round (kRoundKeys keys): the
-// blocks there whose bound clears the row's floor are cut into 16-key tiles,
-// which the four waves score four at a time (one MFMA unit, two units per
-// wave) with the dense kernel's tile code.  Every scored key's score goes to
-// the scores row; a non-seed key above the floor is listed, with its group,
-// in the row's list of the round (one atomic reservation per wave).
+// [pos_begin + part * per_wg, + per_wg) of the round (kParts x kRoundKeys
+// keys): the blocks there whose bound clears the row's floor are
+// cut into 16-key tiles, which the four waves score four at a time (one MFMA
+// unit) with the dense kernel's tile code, each wave's units streamed through
+// two register buffers.  Every scored key's score goes to the scores row; a
+// non-seed key above the floor is listed, with its group, in the row's list
+// of the round (one atomic reservation per wave).
 // ---------------------------------------------------------------------------
-template <class Tag, class KF>
+template <class Tag, class KF, int kParts>
 __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalArgs a, RoundPlan rp) {
+  constexpr int kRoundTiles = kParts * kRoundKeys / 16;           // 16-key tiles a workgroup scores at most
+  constexpr int kRoundWaveUnits = kRoundTiles / 4 / kRoundWaves;  // 64-key units per wave at most
   __shared__ uint32_t s_tile_key[kRoundTiles];
   __shared__ uint16_t s_tile_group[kRoundTiles];
   __shared__ uint16_t s_tile_seeds[kRoundTiles];  // the tile's seeds (scored by the seed pass: not loaded again)
@@ -207,72 +211,151 @@ __global__ __launch_bounds__(kRoundThreads) void temporal_round_kernel(TemporalA
   const BufferRsrc keys = make_buffer(a.source ? nullptr : a.keys + (size_t)row * a.key_stride * KF::kRowBytes,
                                       a.source ? 0u : (uint32_t)L * KF::kRowBytes);
   const BufferRsrc out = make_buffer(a.scores + (size_t)row * L, (uint32_t)L * 4u);
-  const int units = (int)(total + 3) >> 2;
-  const int t_res = lane >> 4;  // the tile of this lane's result
-  // Two units per wave, all loads first.  A seed's row is not loaded (its
-  // score is the seed pass's, already in the scores row).
-  uint4 buf[2][4][KF::kRaw];
-  float scale[2] = {1.f, 1.f};
-  int key_res[2];
-  bool valid[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int u = wave + kRoundWaves * h;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int ti = 4 * u + t;
-      int key = (int)kFarKey;
-      if (ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u)) key = (int)s_tile_key[ti] + r;
-      KF::load_buf(keys, key < L ? key : (int)kFarKey, g, buf[h][t]);
+  if constexpr (kParts == 1) {
+    // Two units per wave at most: both loaded before either is scored.
+    const int units = (int)(total + 3) >> 2;
+    const int t_res = lane >> 4;  // the tile of this lane's result
+    // A seed's row is not loaded (its score is the seed pass's, already in
+    // the scores row).
+    uint4 buf[2][4][KF::kRaw];
+    float scale[2] = {1.f, 1.f};
+    int key_res[2];
+    bool valid[2];
+  #pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int u = wave + kRoundWaves * h;
+  #pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int ti = 4 * u + t;
+        int key = (int)kFarKey;
+        if (ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u)) key = (int)s_tile_key[ti] + r;
+        KF::load_buf(keys, key < L ? key : (int)kFarKey, g, buf[h][t]);
+      }
+      const int ti = 4 * u + t_res;
+      valid[h] = ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u);
+      key_res[h] = valid[h] ? (int)s_tile_key[ti] + r : 0;
+      valid[h] = valid[h] && key_res[h] < L;
+      if constexpr (KF::kScaled)
+        if (valid[h] && !a.source) scale[h] = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key_res[h] >> 7)];
     }
-    const int ti = 4 * u + t_res;
-    valid[h] = ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u);
-    key_res[h] = valid[h] ? (int)s_tile_key[ti] + r : 0;
-    valid[h] = valid[h] && key_res[h] < L;
-    if constexpr (KF::kScaled)
-      if (valid[h] && !a.source) scale[h] = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (key_res[h] >> 7)];
-  }
-  uint32_t listed = 0;
-  uint64_t entry[2] = {0ull, 0ull};
-  uint32_t at[2] = {0u, 0u};
-  bool take[2] = {false, false};
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int u = wave + kRoundWaves * h;
-    if (u >= units) break;  // uniform over the wave
-    float v;
-    if (a.source) {
-      v = valid[h] ? a.source[(size_t)row * a.source_stride + key_res[h]] : 0.f;
-    } else {
-      float sc[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[h][t]);
-      v = unit_reduce(sc, g) * scale[h];
+    uint32_t listed = 0;
+    uint64_t entry[2] = {0ull, 0ull};
+    uint32_t at[2] = {0u, 0u};
+    bool take[2] = {false, false};
+  #pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int u = wave + kRoundWaves * h;
+      if (u >= units) break;  // uniform over the wave
+      float v;
+      if (a.source) {
+        v = valid[h] ? a.source[(size_t)row * a.source_stride + key_res[h]] : 0.f;
+      } else {
+        float sc[4];
+  #pragma unroll
+        for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[h][t]);
+        v = unit_reduce(sc, g) * scale[h];
+      }
+      const int key = key_res[h];
+      if (valid[h]) buffer_store_f32(out, (uint32_t)key * 4u, v);
+      const uint32_t o = float_to_ordered(v);
+      take[h] = valid[h] && o > floor_key;
+      const uint64_t m = __ballot(take[h]);
+      if (take[h]) entry[h] = ((uint64_t)s_tile_group[4 * u + t_res] << 49) | ((uint64_t)key << 32) | o;
+      at[h] = listed + lanes_below(m);
+      listed += (uint32_t)__builtin_popcountll(m);
     }
-    const int key = key_res[h];
-    if (valid[h]) buffer_store_f32(out, (uint32_t)key * 4u, v);
-    const uint32_t o = float_to_ordered(v);
-    take[h] = valid[h] && o > floor_key;
-    const uint64_t m = __ballot(take[h]);
-    if (take[h]) entry[h] = ((uint64_t)s_tile_group[4 * u + t_res] << 49) | ((uint64_t)key << 32) | o;
-    at[h] = listed + lanes_below(m);
-    listed += (uint32_t)__builtin_popcountll(m);
+    // One reservation per wave in the row's list of this round, and the key
+    // rows the wave loaded.
+    uint32_t base = 0;
+    if (lane == 0 && listed)
+      base = __hip_atomic_fetch_add(&a.ws.list_total[(size_t)row * kMaxRounds + rp.round], listed, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t rows_loaded = (uint32_t)__builtin_popcountll(__ballot(valid[0])) +
+                                 (uint32_t)__builtin_popcountll(__ballot(valid[1]));
+    if (lane == 0 && rows_loaded && !a.source)
+      __hip_atomic_fetch_add(a.ws.loaded + row, rows_loaded, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity + base;
+  #pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (take[h]) list[at[h]] = entry[h];
+  } else {
+    const int units = (int)(total + 3) >> 2;
+    const int t_res = lane >> 4;  // the tile of this lane's result
+    // The wave's units (u = wave, wave + kRoundWaves, ...) stream through two
+    // register buffers: the next unit's loads are issued before the current one
+    // is scored.  A seed's row is not loaded (its score is the seed pass's,
+    // already in the scores row).
+    const int count = units > wave ? (units - wave + kRoundWaves - 1) / kRoundWaves : 0;
+    auto load_unit = [&](int u, uint4 (&b)[4][KF::kRaw], float& scale) {
+  #pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int ti = 4 * u + t;
+        int key = (int)kFarKey;
+        if (ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u)) key = (int)s_tile_key[ti] + r;
+        KF::load_buf(keys, key < L ? key : (int)kFarKey, g, b[t]);
+      }
+      scale = 1.f;
+      if constexpr (KF::kScaled) {
+        const int ti = 4 * u + t_res;
+        if (ti < (int)total && !a.source) {
+          const int key = (int)s_tile_key[ti] + r;
+          scale = a.scales[(size_t)row * ((a.key_stride + 127) / 128) + (min(key, L - 1) >> 7)];
+        }
+      }
+    };
+    uint4 buf[2][4][KF::kRaw];
+    float scale[2] = {1.f, 1.f};
+    if (count > 0) load_unit(wave, buf[0], scale[0]);
+    uint32_t listed = 0, rows_loaded = 0, take_bits = 0;
+    uint64_t entry[kRoundWaveUnits];
+    uint32_t at[kRoundWaveUnits];
+  #pragma unroll
+    for (int i = 0; i < kRoundWaveUnits; ++i) {
+      entry[i] = 0ull;
+      at[i] = 0u;
+      if (i < count) {  // uniform over the wave
+        const int u = wave + kRoundWaves * i;
+        if (i + 1 < count) load_unit(u + kRoundWaves, buf[(i + 1) & 1], scale[(i + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const int ti = 4 * u + t_res;
+        bool valid = ti < (int)total && !((s_tile_seeds[ti] >> r) & 1u);
+        const int key = valid ? (int)s_tile_key[ti] + r : 0;
+        valid = valid && key < L;
+        float v;
+        if (a.source) {
+          v = valid ? a.source[(size_t)row * a.source_stride + key] : 0.f;
+        } else {
+          float sc[4];
+  #pragma unroll
+          for (int t = 0; t < 4; ++t) sc[t] = tile_contrib<Tag, 4, KF>(qa, wr, buf[i & 1][t]);
+          v = unit_reduce(sc, g) * scale[i & 1];
+        }
+        if (valid) buffer_store_f32(out, (uint32_t)key * 4u, v);
+        const uint32_t o = float_to_ordered(v);
+        const bool take = valid && o > floor_key;
+        const uint64_t m = __ballot(take);
+        if (take) entry[i] = ((uint64_t)s_tile_group[ti] << 49) | ((uint64_t)key << 32) | o;
+        at[i] = listed + lanes_below(m);
+        take_bits |= take ? 1u << i : 0u;
+        listed += (uint32_t)__builtin_popcountll(m);
+        rows_loaded += (uint32_t)__builtin_popcountll(__ballot(valid));
+      }
+    }
+    // One reservation per wave in the row's list of this round, and the key
+    // rows the wave loaded.
+    uint32_t base = 0;
+    if (lane == 0 && listed)
+      base = __hip_atomic_fetch_add(&a.ws.list_total[(size_t)row * kMaxRounds + rp.round], listed, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0 && rows_loaded && !a.source)
+      __hip_atomic_fetch_add(a.ws.loaded + row, rows_loaded, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity + base;
+  #pragma unroll
+    for (int i = 0; i < kRoundWaveUnits; ++i)
+      if ((take_bits >> i) & 1u) list[at[i]] = entry[i];
   }
-  // One reservation per wave in the row's list of this round, and the key
-  // rows the wave loaded.
-  uint32_t base = 0;
-  if (lane == 0 && listed)
-    base = __hip_atomic_fetch_add(&a.ws.list_total[(size_t)row * kMaxRounds + rp.round], listed, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t rows_loaded = (uint32_t)__builtin_popcountll(__ballot(valid[0])) +
-                               (uint32_t)__builtin_popcountll(__ballot(valid[1]));
-  if (lane == 0 && rows_loaded && !a.source)
-    __hip_atomic_fetch_add(a.ws.loaded + row, rows_loaded, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-  uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity + base;
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    if (take[h]) list[at[h]] = entry[h];
 }
 
 // ---------------------------------------------------------------------------
@@ -999,19 +1082,29 @@ int launch_rounds(TemporalArgs& a, int32_t wave, hipStream_t stream) {
     if (c > cuts.back() && c < groups && (int)cuts.size() < kMaxRounds) cuts.push_back(c);
   }
   cuts.push_back(groups);
-  const int per_wg = kRoundKeys / a.block_size;
+  const int span = kRoundKeys / a.block_size;  // scan positions of kRoundKeys keys
   for (size_t r = 0; r + 1 < cuts.size(); ++r) {
     RoundPlan rp;
     rp.pos_begin = cuts[r] * W;
     rp.pos_end = min(cuts[r + 1] * W, nb);
+    // Wide rounds give each workgroup kRoundParts spans (fewer, longer
+    // workgroups, each wave's units streamed); narrow ones one span, so that
+    // the round still spreads over the whole GPU.
+    const int64_t spans = (int64_t)a.rows * ((rp.pos_end - rp.pos_begin + span - 1) / span);
+    const bool wide = spans >= kRoundWideSpans;
+    const int per_wg = (wide ? kRoundParts : 1) * span;  // at most 64 positions: one per thread
     rp.per_wg = per_wg;
     rp.wgs_per_row = (rp.pos_end - rp.pos_begin + per_wg - 1) / per_wg;
     rp.group = W;
     rp.first_round = r == 0;
     rp.last_round = r + 2 == cuts.size();
     rp.round = (int32_t)r;
-    hipLaunchKernelGGL((temporal_round_kernel<Tag, KF>), dim3((unsigned)(a.rows * rp.wgs_per_row)),
-                       dim3(kRoundThreads), 0, stream, a, rp);
+    if (wide)
+      hipLaunchKernelGGL((temporal_round_kernel<Tag, KF, kRoundParts>), dim3((unsigned)(a.rows * rp.wgs_per_row)),
+                         dim3(kRoundThreads), 0, stream, a, rp);
+    else
+      hipLaunchKernelGGL((temporal_round_kernel<Tag, KF, 1>), dim3((unsigned)(a.rows * rp.wgs_per_row)),
+                         dim3(kRoundThreads), 0, stream, a, rp);
     if (int st = check_launch("temporal_round_kernel")) return st;
     hipLaunchKernelGGL(temporal_resolve_kernel, dim3((unsigned)a.rows), dim3(kResolveThreads), 0, stream, a, rp);
     if (int st = check_launch("temporal_resolve_kernel")) return st;
