@@ -31,8 +31,9 @@ struct TemporalWorkspace {
   uint32_t* tau;        // [rows] ordered key of the threshold in force
   uint32_t* floor;      // [rows] least of run (the k-th largest evaluated score), dynamic rounds
   uint32_t* loaded;     // [rows] key rows a dynamic step loaded (seeds + every key of its rounds' scored blocks)
-  uint32_t* run;        // [rows][k] ordered keys of the k largest evaluated scores
-  uint32_t* run_idx;    // [rows][k] dynamic rounds: the key of each run entry (0xffffffff: a copy of the threshold)
+  uint32_t* run;        // [2][rows][k] ordered keys of the k largest evaluated scores (the dynamic rounds
+                        // alternate between the two buffers; every other path uses the first)
+  uint32_t* run_idx;    // [2][rows][k] dynamic rounds: the key of each run entry (0xffffffff: a copy of the threshold)
   uint32_t* done;       // [rows] dynamic rounds: the last replay wrote the row's top-k and keys scored
   uint32_t* order;      // [rows][blocks] block ids in scan order
   double* upper;        // [rows][blocks] U_b, in double like the float64 reference
@@ -73,8 +74,8 @@ inline TemporalWorkspace temporal_layout(void* base, int64_t rows, int64_t lengt
   const int64_t floor_off = tau_off + round(rows * 4);
   const int64_t loaded_off = floor_off + round(rows * 4);
   const int64_t run_off = loaded_off + round(rows * 4);
-  const int64_t run_idx_off = run_off + round(rows * k * 4);
-  const int64_t done_off = run_idx_off + round(rows * k * 4);
+  const int64_t run_idx_off = run_off + round(2 * rows * k * 4);
+  const int64_t done_off = run_idx_off + round(2 * rows * k * 4);
   const int64_t order_off = done_off + round(rows * 4);
   const int64_t upper_off = order_off + round(rows * blocks * 4);
   const int64_t upos_off = upper_off + round(rows * blocks * 8);

@@ -104,6 +104,12 @@ __device__ __forceinline__ uint32_t upper_key(double bound) {
 __device__ __forceinline__ bool nan_key(uint32_t t) { return t > 0xff800000u || t < 0x007fffffu; }
 __device__ __forceinline__ bool prunes(uint32_t bound_key, uint32_t t) { return !nan_key(t) && bound_key < t; }
 
+// The running k largest that round r reads (and round r - 1 wrote): two
+// buffers of [rows][k], used alternately; the seed pass writes the first.
+__device__ __forceinline__ size_t run_offset(const TemporalArgs& a, int round, int row) {
+  return ((size_t)(round & 1) * a.rows + row) * a.k;
+}
+
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -479,7 +485,7 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
   uint32_t* val = kSpill ? a.ws.spill_val + spill_at : sh.val;
   uint32_t* item = kSpill ? a.ws.spill_item + spill_at : sh.item;
   uint8_t* join = kSpill ? a.ws.spill_join + spill_at : sh.join;
-  const uint32_t* run = a.ws.run + (size_t)row * k;
+  const uint32_t* run = a.ws.run + run_offset(a, rp.round, row);
   const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
   auto each_run = [&](auto f) {
     batched<4>((uint32_t)tid, (uint32_t)k, kResolveThreads, [&](uint32_t i) { return run[i]; },
@@ -830,34 +836,34 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     }
   }
   __syncthreads();
+#ifdef DSA_PHASE_TRACE
+  const uint64_t t_tail0 = wall_clock64();
+#endif
   // After the loop the LDS key arrays are free: sh.item and sh.val serve as
   // staging (in the spill case they were never used).
   const int bs = a.block_size;
   const int L = a.length;
   const uint32_t t = sh.tau;
-  const uint32_t* run_in = a.ws.run + (size_t)row * k;
-  const uint32_t* idx_in = a.ws.run_idx + (size_t)row * k;
+  const size_t run_at = run_offset(a, rp.round, row);
+  const uint32_t* run_in = a.ws.run + run_at;
+  const uint32_t* idx_in = a.ws.run_idx + run_at;
   // A listed key joined iff its block was kept (every listed key's block was
   // decided by this round).
   auto listed_joined = [&](uint64_t x) { return sh.kept[((uint32_t)(x >> 32) & 0x1ffffu) / (uint32_t)bs] != 0; };
   if (!rp.last_round) {
     // The next round starts from the exact k largest, each with its key: the
     // joined keys above the threshold (the run's and the listed ones), then
-    // copies of it.  The run is staged in LDS first, as it is rewritten.
-    for (int i = tid; i < k; i += kResolveThreads) {
-      sh.item[i] = run_in[i];
-      sh.val[i] = idx_in[i];
-    }
-    __syncthreads();
-    uint32_t* run_out = a.ws.run + (size_t)row * k;
-    uint32_t* idx_out = a.ws.run_idx + (size_t)row * k;
+    // copies of it, in the other of the two run buffers.
+    const size_t out_at = run_offset(a, rp.round + 1, row);
+    uint32_t* run_out = a.ws.run + out_at;
+    uint32_t* idx_out = a.ws.run_idx + out_at;
     auto emit = [&](uint32_t v, uint32_t key) {
       const uint32_t j = __hip_atomic_fetch_add(&sh.n_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       run_out[j] = v;
       idx_out[j] = key;
     };
     for (int i = tid; i < k; i += kResolveThreads)
-      if (sh.item[i] > t) emit(sh.item[i], sh.val[i]);
+      if (run_in[i] > t) emit(run_in[i], idx_in[i]);
     for (uint32_t e = (uint32_t)tid; e < n_listed; e += kResolveThreads) {
       const uint64_t x = list[e];
       if ((uint32_t)x > t && listed_joined(x)) emit((uint32_t)x, (uint32_t)(x >> 32) & 0x1ffffu);
@@ -948,16 +954,42 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
       }
     }
   }
+#ifdef DSA_PHASE_TRACE
+  const uint64_t t_tail1 = wall_clock64();
+#endif
   // Scored blocks the replay pruned: their keys back to -inf, seeds excepted.
   int bs_shift = 4;
   while ((1 << bs_shift) < bs) ++bs_shift;
   const uint32_t nreset = sh.nreset;
   const uint32_t* mask = a.ws.seed_mask + (size_t)row * ((L + 31) / 32);
   float* srow = a.scores + (size_t)row * L;
-  for (uint32_t i = (uint32_t)tid; i < nreset * (uint32_t)bs; i += kResolveThreads) {
-    const int key = (int)sh.resets[i >> bs_shift] * bs + (int)(i & (uint32_t)(bs - 1));
-    if (key < L && !((mask[key >> 5] >> (key & 31)) & 1u)) srow[key] = -__builtin_inff();
+  // (Block sizes divide kRoundKeys: powers of two.)  Eight keys per thread
+  // per pass, their seed-mask words read before any is written.
+  const uint32_t n_reset_keys = nreset * (uint32_t)bs;
+  for (uint32_t i0 = (uint32_t)tid; i0 < n_reset_keys; i0 += 8u * kResolveThreads) {
+    int key[8];
+    uint32_t word[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t i = min(i0 + (uint32_t)j * kResolveThreads, n_reset_keys - 1u);
+      key[j] = (int)sh.resets[i >> bs_shift] * bs + (int)(i & (uint32_t)(bs - 1));
+      word[j] = mask[min(key[j], L - 1) >> 5];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i0 + (uint32_t)j * kResolveThreads < n_reset_keys && key[j] < L && !((word[j] >> (key[j] & 31)) & 1u))
+        srow[key[j]] = -__builtin_inff();
   }
+#ifdef DSA_PHASE_TRACE
+  // Rows 1024 + row of the log (trace builds only): the tail after the group
+  // loop, its write-back or top-k part, and the -inf resets.
+  if (tid == 0 && row < 1024) {
+    const uint64_t t_end = wall_clock64();
+    g_trace_resolve[(size_t)(1024 + row) * kTraceMarks + 0] += t_end - t_tail0;
+    g_trace_resolve[(size_t)(1024 + row) * kTraceMarks + 1] += t_tail1 - t_tail0;
+    g_trace_resolve[(size_t)(1024 + row) * kTraceMarks + 2] += t_end - t_tail1;
+  }
+#endif
 }
 
 __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(TemporalArgs a, RoundPlan rp) {
@@ -976,7 +1008,7 @@ __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(Tempo
   const int wave = tid >> 6;
   const uint32_t* order = a.ws.order + (size_t)row * nb + rp.pos_begin;
   const double* upper = a.ws.upper_pos + (size_t)row * nb + rp.pos_begin;
-  const uint32_t* run = a.ws.run + (size_t)row * k;
+  const uint32_t* run = a.ws.run + run_offset(a, rp.round, row);
   const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
   // The setup's inputs are read in one round trip: the positions' blocks and
   // bounds (at most four per thread), the list's length, and the first
