@@ -17,6 +17,15 @@ K=2048, block 64 static temporal step), ``c4-topk`` (the prefill top-512
 of 4096 causal rows of 1..4096 scores; in this one the row-loaded mark waits
 for the row, so the trace build's timing of that kernel differs slightly),
 and ``c2-select`` / ``c5-select`` (the decode step's list select).
+
+``c3-replay`` and ``c5-replay`` report instead, per row, the phase totals of
+the dynamic temporal step's replay (temporal_resolve_kernel) over all of the
+step's rounds: setup (kernel start to the group loop), the group loop and its
+decisions, exact selects, joins and cut moves, the loop's steps, the listed
+keys, and the tail after the loop (the running k largest written back with
+its keys, or the step's top-k and keys scored; the -inf resets).  C3: block 16,
+address order, 33-block groups, gamma = sigma of the score drift; C5: fp8,
+block 64, previous-hot order, 96-block groups, gamma = 0.25 sigma.
 """
 
 from __future__ import annotations
@@ -101,6 +110,56 @@ def _c4_topk(device):
                                     idx.data_ptr(), None, stream)
 
 
+def _transition(device, fp8: bool):
+    """One decode transition L - 1 -> L with AR(1) queries (rho 0.95): the
+    keys, scales, weights, both queries, and the previous step's top-k and
+    scores."""
+
+    from . import decode
+
+    gen = torch.Generator().manual_seed(1582)
+    rows, length = 4, (131072 if fp8 else 16385)
+    w = (torch.randn(rows, 64, generator=gen) / 8).to(device)
+    raw = torch.randn(rows, length, 128, generator=gen)
+    scales = None
+    if fp8:
+        scales = raw.reshape(rows, length // 128, 128 * 128).abs().amax(dim=2) / 448
+        keys = (raw / scales.repeat_interleave(128, dim=1)[..., None]).to(torch.float8_e4m3fn).to(device)
+        scales = scales.to(device).contiguous()
+    else:
+        keys = raw.to(torch.bfloat16).to(device)
+    del raw
+    q0 = torch.randn(rows, 64, 128, generator=gen) / math.sqrt(128)
+    q1 = 0.95 * q0 + math.sqrt(1 - 0.95**2) * torch.randn(rows, 64, 128, generator=gen) / math.sqrt(128)
+    q0, q1 = q0.to(torch.bfloat16).to(device), q1.to(torch.bfloat16).to(device)
+    prev_top, prev_scores = decode.indexer_topk(q0, w, keys[:, : length - 1].contiguous(), 2048, key_scales=scales,
+                                                return_scores=True)
+    dense = decode.indexer_topk(q1, w, keys, 2048, key_scales=scales, return_scores=True)[1]
+    sigma = (dense[:, : length - 1] - prev_scores).std(dim=1, unbiased=False)
+    return keys, scales, w, q1, prev_top, prev_scores, sigma, length
+
+
+def _c3_replay(device):
+    from . import temporal
+
+    keys, _, w, q1, prev_top, prev_scores, sigma, length = _transition(device, fp8=False)
+    prev_max = temporal.block_max(prev_scores, 16)
+    gamma = sigma.contiguous()
+    return "replay", lambda: temporal.temporal_step(q1, w, keys, prev_max, length - 1, prev_top, gamma, block_size=16,
+                                                    method="dynamic", scan_order="address", wave=33)
+
+
+def _c5_replay(device):
+    from . import temporal
+
+    keys, scales, w, q1, prev_top, prev_scores, sigma, length = _transition(device, fp8=True)
+    prev_max = temporal.block_max(prev_scores, 64)
+    gamma = (0.25 * sigma).contiguous()
+    return "replay", lambda: temporal.temporal_step(q1, w, keys, prev_max, length - 1, prev_top, gamma, block_size=64,
+                                                    method="dynamic", scan_order="previous_hot", wave=96,
+                                                    key_scales=scales)
+
+
 def _select_of(config):
     # The same decode step, timed by the list select's marks.
     def make(device):
@@ -109,7 +168,23 @@ def _select_of(config):
 
 
 CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static, "c4-topk": _c4_topk,
-           "c2-select": _select_of(_c2), "c5-select": _select_of(_c5)}
+           "c2-select": _select_of(_c2), "c5-select": _select_of(_c5), "c3-replay": _c3_replay, "c5-replay": _c5_replay}
+KERNEL_SYMBOL["replay"] = "dsa_trace_temporal_resolve"
+
+
+def replay_phases(log: np.ndarray, rows: int) -> dict:
+    """Per-row totals of the replay's phases (rows r and 1024 + r of its log)."""
+
+    us = lambda ticks: round(float(ticks) / WALL_CLOCK_MHZ, 2)  # noqa: E731
+    out = {}
+    for r in range(rows):
+        a, tail = log[r], log[1024 + r]
+        out[r] = {"setup_us": us(a[7]), "loop_us": us(a[0]), "decisions_us": us(a[1]), "exact_selects_us": us(a[2]),
+                  "joins_us": us(a[4]), "cut_moves_us": us(a[5]), "exact_selects": int(a[3]) & 0xFFFFFFFF,
+                  "cut_moves": int(a[3]) >> 32, "loop_steps": (int(a[6]) >> 24) & 0xFFFFFF,
+                  "listed_keys": int(a[6]) & 0xFFFFFF, "tail_us": us(tail[0]), "tail_writeback_topk_us": us(tail[1]),
+                  "tail_resets_us": us(tail[2])}
+    return out
 
 
 def timeline(config: str, runs: int = 8) -> dict:
@@ -135,6 +210,8 @@ def timeline(config: str, runs: int = 8) -> dict:
     if reader(host, n, 0) != 0:
         raise RuntimeError(lib.dsa_last_error().decode(errors="replace"))
     log = np.frombuffer(host, dtype=np.uint64).reshape(4096, 8).astype(np.int64)
+    if kernel == "replay":
+        return {"config": config, "kernel": "replay", "rows": replay_phases(log, 4)}
     wgs = np.flatnonzero(log[:, 0] > 0)
     names = MARKS[kernel]
     raw = log[wgs][:, : len(names)].astype(np.float64)
