@@ -385,7 +385,7 @@ extern "C" int dsa_project_gemm(const void* hidden, int32_t hidden_dtype, int64_
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (weight_dtype == kF32) {
     DSA_REQUIRE(!positions, "the fused RoPE takes bf16 weights");
-    DSA_REQUIRE(kdim % 4 == 0 && hidden_stride % 4 == 0, "fp32 projections need kdim and hidden_stride % 4 == 0");
+    DSA_REQUIRE(kdim % 4 == 0 && hidden_stride % 4 == 0, "fp32 projections need kdim and hidden_stride divisible by 4");
     const int64_t grid = ((features + kF32Feat - 1) / kF32Feat) * ((tokens + kF32Tok - 1) / kF32Tok);
     DSA_REQUIRE(grid <= 0x7fffffffLL, "problem too large");
     hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)grid), dim3(256), 0, s, a);

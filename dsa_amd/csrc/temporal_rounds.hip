@@ -467,7 +467,8 @@ __device__ __forceinline__ uint32_t cut_select(P32 val, P8 join, uint32_t s0, ui
 
 template <bool kSpill>
 __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPlan& rp, ResolveShared& sh,
-                                            uint32_t n_listed, uint32_t max_key, uint64_t t_start) {
+                                            uint32_t n_listed, uint32_t max_key, uint32_t floor_key,
+                                            uint32_t seed_tau, uint64_t t_start) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -478,7 +479,6 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
   const int g_begin = rp.pos_begin / W;
   const int n_groups = (rp.pos_end + W - 1) / W - g_begin;
   const int n_pos = rp.pos_end - rp.pos_begin;
-  const uint32_t floor_key = a.ws.floor[row];
   const uint32_t span = max_key - floor_key;
   const uint32_t shift = span < (uint32_t)kBins ? 0u : 32u - (uint32_t)__builtin_clz(span) - 12u;
   const size_t spill_at = (size_t)row * a.ws.spill_capacity;
@@ -608,7 +608,6 @@ __device__ __forceinline__ void resolve_row(const TemporalArgs& a, const RoundPl
     uint32_t tau = floor_key;
     bool tau_ok = true;
     uint32_t nreset = 0;
-    const uint32_t seed_tau = a.ws.tau[row];
     RESOLVE_T0(t_all);
     auto bin_start = [&](uint32_t b) { return b ? sh.end[b - 1] : 0u; };
     auto exact_tau = [&]() {
@@ -1011,11 +1010,14 @@ __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(Tempo
   const uint32_t* run = a.ws.run + run_offset(a, rp.round, row);
   const uint64_t* list = a.ws.entries + (size_t)row * a.ws.list_capacity;
   // The setup's inputs are read in one round trip: the positions' blocks and
-  // bounds (at most four per thread), the list's length, and the first
-  // kKeyBatch key values per thread, each from the running k largest or the
-  // list (one dword: an entry's value is its low word), list reads clamped
-  // to its capacity until its length is known.
+  // bounds (at most four per thread), the list's length, the floor, the
+  // seeds' threshold, and the first kKeyBatch key values per thread, each
+  // from the running k largest or the list (one dword: an entry's value is
+  // its low word), list reads clamped to its capacity until its length is
+  // known.
   const uint32_t n_listed = a.ws.list_total[(size_t)row * kMaxRounds + rp.round];
+  const uint32_t floor_key = a.ws.floor[row];
+  const uint32_t seed_tau = a.ws.tau[row];
   constexpr int kPosPer = kMaxTemporalBlocks / kResolveThreads;
   uint32_t pb[kPosPer];
   double pu[kPosPer];
@@ -1063,9 +1065,9 @@ __global__ __launch_bounds__(kResolveThreads) void temporal_resolve_kernel(Tempo
 #pragma unroll
   for (int w = 0; w < kResolveWaves; ++w) max_key = max(max_key, sh.wsum[w]);
   if (n_keys <= (uint32_t)kSortCap)
-    resolve_row<false>(a, rp, sh, n_listed, max_key, t_start);
+    resolve_row<false>(a, rp, sh, n_listed, max_key, floor_key, seed_tau, t_start);
   else
-    resolve_row<true>(a, rp, sh, n_listed, max_key, t_start);
+    resolve_row<true>(a, rp, sh, n_listed, max_key, floor_key, seed_tau, t_start);
 }
 
 // Round splits, as fractions of the scan's groups: DSA_AMD_TEMPORAL_ROUNDS, a
