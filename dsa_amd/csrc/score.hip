@@ -330,8 +330,14 @@ __device__ __forceinline__ void zero_wave_bins(uint32_t* bins, int lane) {
 // Key of register slot e of a lane in the read-back row, and the linear bin
 // of a value.
 __device__ __forceinline__ int topk_key(int e, int lane) { return 256 * (e >> 2) + 4 * lane + (e & 3); }
-__device__ __forceinline__ int topk_bin(float x, float lo, float scale) {
-  return min(kTopKBins - 1, (int)((x - lo) * scale));
+// x * scale + nlo, nlo = -lo * scale, is monotone in x.  v_cvt_i32_f32
+// saturates (-inf to INT_MIN) and converts NaN to 0, so -inf (a key past the
+// visible ones, or any key when scale is 0) lands in bin 0; it is issued
+// directly because the C++ conversion leaves those inputs undefined.
+__device__ __forceinline__ int topk_bin(float x, float /*lo*/, float scale, float nlo) {
+  int b;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(b) : "v"(fmaf(x, scale, nlo)));
+  return min(max(b, 0), kTopKBins - 1);
 }
 
 // Every pass below walks the row in blocks of 256 keys (one float4 per lane):
@@ -340,13 +346,13 @@ __device__ __forceinline__ int topk_bin(float x, float lo, float scale) {
 #define DSA_TOPK_BLOCKS(BODY)                                  \
   _Pragma("unroll") for (int j = 0; j < 16; ++j) {             \
     if (256 * j < vis) {                                       \
-      constexpr bool kPartial = true;                          \
+      [[maybe_unused]] constexpr bool kPartial = true;         \
       BODY                                                     \
     }                                                          \
   }
 
-__device__ __forceinline__ void prefill_topk_row(BufferRsrc row, int vis, int k, int64_t* out_idx, float* out_val,
-                                                 uint32_t* scratch, int lane) {
+__device__ __forceinline__ void prefill_topk_row(BufferRsrc row, int vis, int length, int k, int64_t* out_idx,
+                                                 float* out_val, uint32_t* scratch, int lane) {
   float v[64];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -357,37 +363,48 @@ __device__ __forceinline__ void prefill_topk_row(BufferRsrc row, int vis, int k,
     v[4 * j + 2] = __uint_as_float(q.z);
     v[4 * j + 3] = __uint_as_float(q.w);
   }
+  // The kernel stored -inf at the row's keys past the visible ones; keys past
+  // the row's length (in its last block) read 0 from the buffer and become
+  // -inf here, so that every key past the visible ones is -inf below.
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    if (256 * j < vis && 256 * j + 256 > length)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[4 * j + t] = 256 * j + 4 * lane + t < length ? v[4 * j + t] : -__builtin_inff();
   // key 256 j + 4 lane + t of the last block is visible iff t < tail
   const int tail = vis - 4 * lane;
   const bool all = vis <= k;
-  float tv = 0.f;  // the cut: key i with value x is kept iff x > tv or (x == tv and i <= ti)
+  // The cut: key i with value x is kept iff x > tv or (x == tv and i <= ti).
+  // With at most k visible keys it keeps every finite score, and no -inf
+  // (the keys past the visible ones).
+  float tv = -__builtin_inff();
   int ti = -1;
   if (!all) {
+    // The kernel stored -inf past the visible keys, and a visible score is
+    // finite: the range needs no visibility test.
     float lo = __builtin_inff(), hi = -__builtin_inff();
     DSA_TOPK_BLOCKS(
+      const float* x = &v[4 * j];
+      hi = fmaxf(fmaxf(hi, x[0]), fmaxf(x[1], fmaxf(x[2], x[3])));
 _Pragma("unroll")
-      for (int t = 0; t < 4; ++t) {
-        const float x = v[4 * j + t];
-        const bool ok = !kPartial || 256 * j + t < tail;
-        lo = ok && x < lo ? x : lo;
-        hi = ok && x > hi ? x : hi;
-      })
+      for (int t = 0; t < 4; ++t) lo = fminf(lo, x[t] == -__builtin_inff() ? __builtin_inff() : x[t]);)
     lo = wave_min(lo);
     hi = wave_max(hi);
     // Monotone binning: bin(x) > bin(y) implies x > y.  A single value, or a
     // span that overflows, puts every key in bin 0 (the radix below resolves it).
     float scale = (float)kTopKBins / (hi - lo);
-    if (!(scale <= 3.0e38f)) scale = 0.f;
+    float nlo = -lo * scale;
+    if (!(scale <= 3.0e38f) || !(fabsf(nlo) <= 3.0e38f)) scale = nlo = 0.f;
     zero_wave_bins(scratch, lane);
     wave_lds_fence();
-    // Keys past the visible ones count into a spare word after the candidates.
+    // Keys past the visible ones (-inf) count into bin 0: the counts above
+    // the cut bin, and so the rank wanted inside it, are exact; only bin 0's
+    // own count may exceed its visible keys, which the passes below test.
     DSA_TOPK_BLOCKS(
 _Pragma("unroll")
-      for (int t = 0; t < 4; ++t) {
-        int at = topk_bin(v[4 * j + t], lo, scale);
-        if (kPartial) at = 256 * j + t < tail ? at : kTopKScratch - 1;
-        __hip_atomic_fetch_add(&scratch[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      })
+      for (int t = 0; t < 4; ++t)
+        __hip_atomic_fetch_add(&scratch[topk_bin(v[4 * j + t], lo, scale, nlo)], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);)
     wave_lds_fence();
     const Locate loc = wave_locate<kTopKBins / kWave>(scratch, (uint32_t)k, false);
     const int cut_bin = (int)loc.digit;
@@ -401,7 +418,7 @@ _Pragma("unroll")
         uint32_t cnt = 0;
 _Pragma("unroll")
         for (int t = 0; t < 4; ++t) {
-          c[t] = (!kPartial || 256 * j + t < tail) && topk_bin(v[4 * j + t], lo, scale) == cut_bin;
+          c[t] = topk_bin(v[4 * j + t], lo, scale, nlo) == cut_bin && v[4 * j + t] != -__builtin_inff();
           cnt += c[t] ? 1u : 0u;
         }
         if (__ballot(cnt != 0) != 0) {
@@ -448,7 +465,7 @@ _Pragma("unroll")
 _Pragma("unroll")
           for (int t = 0; t < 4; ++t) {
             const uint32_t o = float_to_ordered(v[4 * j + t]);
-            if ((!kPartial || 256 * j + t < tail) && topk_bin(v[4 * j + t], lo, scale) == cut_bin &&
+            if ((!kPartial || 256 * j + t < tail) && topk_bin(v[4 * j + t], lo, scale, nlo) == cut_bin &&
                 (o & pmask) == prefix)
               __hip_atomic_fetch_add(&scratch[(o >> shift) & dmask], 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -495,7 +512,7 @@ _Pragma("unroll")
     for (int t = 0; t < 4; ++t) {
       const int key = topk_key(4 * j + t, lane);
       const float x = v[4 * j + t];
-      s[t] = (!kPartial || 256 * j + t < tail) && (all || x > tv || (x == tv && key <= ti));
+      s[t] = x > tv || (x == tv && key <= ti);
       cnt += s[t] ? 1u : 0u;
     }
     const uint32_t incl = wave_incl_scan(cnt);
@@ -651,7 +668,7 @@ __global__ __launch_bounds__(64 * kPrefillQueries, 2) void prefill_scores_kernel
       // have completed.
       __builtin_amdgcn_s_waitcnt(0);
       const int64_t at = seq * a.topk_stride;
-      prefill_topk_row(orsrc, vis, a.topk, a.topk_idx + at, a.topk_val ? a.topk_val + at : nullptr,
+      prefill_topk_row(orsrc, vis, L, a.topk, a.topk_idx + at, a.topk_val ? a.topk_val + at : nullptr,
                        topk_scratch[wave], lane);
     }
   }
