@@ -1,7 +1,8 @@
 """Randomised parity sweep of the dynamic temporal step (the rounds path)
 against the oracle's replay filter (reference replay.py:172-222).
 
-Eighteen configurations drawn from a fixed seed: block sizes 16-128, the live
+Eighteen configurations drawn from a fixed seed, and eight with rows of 8K to
+40K keys and k up to 2048 from another: block sizes 16-128, the live
 step's three scan orders (oracle_current needs recorded scores: the replay
 tests cover it), refresh waves from one block to a whole-row's worth, margins from
 -sigma to +sigma, lengths that do and do not grow, k from 8 to 1000, bf16 and
@@ -45,6 +46,32 @@ def draw_cases(n: int, seed: int) -> list:
 
 
 CASES = draw_cases(18, seed=1582)
+
+
+def draw_long_cases(n: int, seed: int) -> list:
+    """Longer rows (to 40K keys, past the one-workgroup top-k's 32K), k to
+    2048, waves of one or two blocks or up to half the row, within the step's
+    limits (at most 2048 blocks, k + wave * block_size <= 8192)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        k = int(rng.choice([256, 1000, 2048]))
+        prev_length = int(rng.integers(8192, 40000))
+        length = prev_length + int(rng.choice([0, 1, 200]))
+        block = int(rng.choice([b for b in (16, 32, 64, 128) if math.ceil(length / b) <= 2048]))
+        order = str(rng.choice(["address", "previous_hot", "upper_hot"]))
+        blocks = math.ceil(length / block)
+        wave = int(rng.choice([1, 2, int(rng.integers(1, max(2, blocks // 2)))]))
+        wave = max(1, min(wave, (8192 - k) // block))
+        gamma_sigma = float(rng.choice([-1.0, -0.25, 0.0, 0.5, 1.0, 2.0]))
+        dtype = str(rng.choice(["bf16", "f16"]))
+        distinct = int(rng.choice([0, 0, 40, 500]))
+        splits = str(rng.choice(["1", "0.25", "0.1,0.3", "0.05,0.15,0.4,0.8"]))
+        cases.append((100 + i, block, order, k, prev_length, length, wave, gamma_sigma, dtype, distinct, splits))
+    return cases
+
+
+CASES += draw_long_cases(8, seed=2026)
 
 
 def transition(batch, prev_length, length, seed, rho=0.95):
