@@ -7,9 +7,11 @@ semantics).  One step = dense scores of all 16 x 32768 keys + the top-K of
 every sequence, inputs resident in HBM.  Four distinct key sets (4 x 128 MiB)
 are rotated so that the 256 MB last-level cache cannot hold the step's keys.
 
-The timed region replays a HIP graph of 4 consecutive steps (one per key
-set): the step is three kernel launches and Python issues them slower than the
-GPU runs them.  Prints one JSON line (see the driver contract) with a
+The timed region replays a HIP graph of up to 40 consecutive steps (the four
+key sets in turn), sized to divide the number of timed steps: the step is two
+kernel launches and Python issues them slower than the GPU runs them, and each
+graph launch costs about as much as one step's gap between kernels, so a
+longer graph leaves less of it per step.  Prints one JSON line (see the driver contract) with a
 `roofline` object for the dominant kernel (the scoring kernel, timed by HIP
 events that the kernel records at its own start and end, on the stream it
 runs on; its bytes are the step's algorithmic bytes, keys + queries +
@@ -221,9 +223,14 @@ def main() -> None:
         select()
     torch.cuda.synchronize()
 
-    # The step is launch-bound from Python (three kernels, ~40 us of GPU work),
-    # so the timed region replays a HIP graph of ROTATIONS consecutive steps
-    # (one per key set); every launch in it is one of the library's kernels.
+    # The step is launch-bound from Python (two kernels, ~40 us of GPU work),
+    # so the timed region replays a HIP graph of consecutive steps (the key
+    # sets in turn); every launch in it is one of the library's kernels.  The
+    # graph holds the largest of 40, 20, 12, 8 steps that divides the timed
+    # steps (else 4, and the timed steps round up to a multiple of 4): a
+    # graph launch costs about one step's kernel gap, about 1 us per step
+    # over a graph of 4 steps against 40.
+    per_graph = next((n for n in (40, 20, 12, 8, 4) if args.steps % n == 0), ROTATIONS)
     graph = torch.cuda.CUDAGraph()
     capture = torch.cuda.Stream(device)
     capture.wait_stream(torch.cuda.current_stream(device))
@@ -234,11 +241,11 @@ def main() -> None:
     torch.cuda.current_stream(device).wait_stream(capture)
     torch.cuda.synchronize()
     with torch.cuda.graph(graph):
-        for r in range(ROTATIONS):
-            score(key_sets[r])
+        for i in range(per_graph):
+            score(key_sets[i % ROTATIONS])
             select()
-    replays = max(1, -(-args.steps // ROTATIONS))
-    steps = replays * ROTATIONS
+    replays = max(1, -(-args.steps // per_graph))
+    steps = replays * per_graph
     graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
@@ -376,7 +383,8 @@ def main() -> None:
             "algorithmic_bytes": step_bytes,
             "hbm_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "wall_s": round(wall, 3),
-            "timing": f"value: HIP events around {replays} replays of a graph of {ROTATIONS} steps; "
+            "timing": f"value: HIP events around {replays} replays of a graph of {per_graph} steps "
+                      f"(the {ROTATIONS} key sets in turn); "
             f"score_us/topk_us: HIP events recorded by the kernels themselves (hipExtLaunchKernel) over {timed} eager steps "
             "queued behind a hold on the stream, so they run back to back",
             "launch_gap_us": round(gap_us, 3),
