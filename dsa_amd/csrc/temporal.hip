@@ -932,7 +932,10 @@ int check_step(const void* queries, const void* keys, int64_t key_stride, const 
   DSA_REQUIRE(k > 0 && k <= kMaxRun && k <= prev_length, "k=%lld must be in [1, min(4096, prev_length)]",
               (long long)k);
   DSA_REQUIRE(wave >= 0, "wave must be >= 0");
-  DSA_REQUIRE(k + int64_t(wave) * block_size <= kMaxMerge, "k + wave * block_size exceeds %d", kMaxMerge);
+  // The sequential path merges the running k largest with a wave's keys in
+  // LDS; the rounds' replay sorts in the workspace past its LDS.
+  DSA_REQUIRE(wave == 0 || !legacy_paths_forced() || k + int64_t(wave) * block_size <= kMaxMerge,
+              "k + wave * block_size exceeds %d on the sequential path", kMaxMerge);
   DSA_REQUIRE(key_dtype == DSA_DTYPE_BF16 || key_dtype == DSA_DTYPE_F16 || key_dtype == DSA_DTYPE_FP8_E4M3,
               "the temporal step takes fp16/bf16/fp8 keys (got %d)", key_dtype);
   DSA_REQUIRE(key_dtype != DSA_DTYPE_FP8_E4M3 || key_scales, "fp8 keys need key_scales");

@@ -381,7 +381,8 @@ int dsa_score_topk_noalloc(const void* queries, const float* weights, const void
  *   wave        0: threshold fixed at the seed minimum (static); W > 0: the
  *               threshold becomes the k-th largest evaluated score after
  *               every W blocks of the scan (W = 1 is the reference's dynamic
- *               filter).  k + wave * block_size <= 8192.
+ *               filter).  With DSA_AMD_TEMPORAL_PATH=launch (the
+ *               sequential path) k + wave * block_size <= 8192.
  *   scores      [batch, length] fp32 out: evaluated keys' scores, else -inf
  *   evaluated_blocks [batch, ceil(length / block_size)] bytes out: 1 = kept
  *   out_topk    [batch, k] int64 out: stable top-k of the evaluated keys, in

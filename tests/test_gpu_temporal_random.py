@@ -2,7 +2,8 @@
 against the oracle's replay filter (reference replay.py:172-222).
 
 Eighteen configurations drawn from a fixed seed, and eight with rows of 8K to
-40K keys and k up to 2048 from another: block sizes 16-128, the live
+40K keys and k up to 2048 from another, and three whose refresh groups hold
+more than 8192 keys with the running k largest: block sizes 16-128, the live
 step's three scan orders (oracle_current needs recorded scores: the replay
 tests cover it), refresh waves from one block to a whole-row's worth, margins from
 -sigma to +sigma, lengths that do and do not grow, k from 8 to 1000, bf16 and
@@ -51,7 +52,8 @@ CASES = draw_cases(18, seed=1582)
 def draw_long_cases(n: int, seed: int) -> list:
     """Longer rows (to 40K keys, past the one-workgroup top-k's 32K), k to
     2048, waves of one or two blocks or up to half the row, within the step's
-    limits (at most 2048 blocks, k + wave * block_size <= 8192)."""
+    limits (at most 2048 blocks; k + wave * block_size <= 8192, which only the
+    sequential path requires, is left to the three cases below)."""
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(n):
@@ -72,6 +74,13 @@ def draw_long_cases(n: int, seed: int) -> list:
 
 
 CASES += draw_long_cases(8, seed=2026)
+# Refresh groups whose keys, with the running k largest, pass the replay's
+# 8192 LDS keys (it sorts them in the workspace instead).
+CASES += [
+    (200, 64, "address", 2048, 30000, 30001, 128, 0.0, "bf16", 0, "0.25"),
+    (201, 128, "previous_hot", 4096, 60000, 60017, 64, -0.25, "f16", 0, "0.1,0.3"),
+    (202, 32, "upper_hot", 1000, 20000, 20000, 300, 0.5, "bf16", 40, "1"),
+]
 
 
 def transition(batch, prev_length, length, seed, rho=0.95):
