@@ -13,7 +13,8 @@ earliest workgroup start, as percentiles over workgroups and per XCD
 
 Configurations: ``c2`` (B=16, L=32768 bf16, K=2048 decode step), ``c5``
 (B=4, L=131072 fp8, K=2048), ``c3-static`` (B=4, 16384 -> 16385 keys,
-K=2048, block 64 static temporal step), ``c4-topk`` (the prefill top-512
+K=2048, block 64 static temporal step), ``c5-static`` (the same step on
+C5's fp8 shape, 131071 -> 131072 keys, margin 0.25 sigma), ``c4-topk`` (the prefill top-512
 of 4096 causal rows of 1..4096 scores; in this one the row-loaded mark waits
 for the row, so the trace build's timing of that kernel differs slightly),
 and ``c2-select`` / ``c5-select`` (the decode step's list select).
@@ -160,6 +161,16 @@ def _c5_replay(device):
                                                     key_scales=scales)
 
 
+def _c5_static(device):
+    from . import temporal
+
+    keys, scales, w, q1, prev_top, prev_scores, sigma, length = _transition(device, fp8=True)
+    prev_max = temporal.block_max(prev_scores, 64)
+    gamma = (0.25 * sigma).contiguous()
+    return "static", lambda: temporal.temporal_step(q1, w, keys, prev_max, length - 1, prev_top, gamma, block_size=64,
+                                                    method="static", key_scales=scales)
+
+
 def _select_of(config):
     # The same decode step, timed by the list select's marks.
     def make(device):
@@ -168,7 +179,8 @@ def _select_of(config):
 
 
 CONFIGS = {"c2": _c2, "c5": _c5, "c3-static": _c3_static, "c4-topk": _c4_topk,
-           "c2-select": _select_of(_c2), "c5-select": _select_of(_c5), "c3-replay": _c3_replay, "c5-replay": _c5_replay}
+           "c2-select": _select_of(_c2), "c5-select": _select_of(_c5), "c3-replay": _c3_replay, "c5-replay": _c5_replay,
+           "c5-static": _c5_static}
 KERNEL_SYMBOL["replay"] = "dsa_trace_temporal_resolve"
 
 
